@@ -1,0 +1,267 @@
+#!/usr/bin/env python3
+"""Q4_0 GEMV bandwidth benchmark of the KunlunK200 matmul path on one MI355X.
+
+Workload: one Llama-7B-style decode layer set at
+batch 1, Q4_0 weights from N(0, 0.02) quantized with the ggml closed form,
+F32 activations N(0, 1): K4096->N12288 (QKV), K4096->N11008 x2 (gate, up),
+K11008->N4096 (down), K4096->N32000 (LM head). One step = the five
+kunlun::matmul() calls. Three distinct device copies of the set (3 x 178 MB)
+rotate so the 256 MB Infinity Cache cannot hold the weights.
+
+value = algorithmic bytes of a step / step time, bytes per GEMV =
+n*(k/32)*18 + 4*b*k + 4*b*n. Timing uses HIP events recorded on the library's
+own stream around K steps (after W warm-up steps). roofline: the dominant
+kernel, the K4096xN11008 GEMV, timed alone the same way. cpu_baseline: the
+reference's CPU oracle (bench/native-q4-reference.h, FP64, 6 OpenMP threads)
+on the K4096xN11008 GEMV, repeated for about --cpu-seconds.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import kunlunk200_lib_amd as kl  # noqa: E402
+
+METRIC = "Q4_0 GEMV GB/s (% HBM peak) K4096×N11008 batch1; GEMM TFLOP/s at batch512"
+HBM_PEAK_GBPS = 8000.0
+LAYER = [("qkv", 4096, 12288), ("gate", 4096, 11008), ("up", 4096, 11008), ("down", 11008, 4096),
+         ("lm_head", 4096, 32000)]
+DOMINANT = ("gate", 4096, 11008)
+COPIES = 3
+ROTATE_BYTES = 640 * 1000 * 1000     # > 2x the 256 MB Infinity Cache
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def q4_bytes(k: int, n: int, b: int = 1) -> int:
+    return n * (k // 32) * 18 + 4 * b * k + 4 * b * n
+
+
+class HipEvents:
+    def __init__(self):
+        self.lib = ctypes.CDLL("libamdhip64.so")
+        self.lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.lib.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def create(self):
+        ev = ctypes.c_void_p()
+        assert self.lib.hipEventCreate(ctypes.byref(ev)) == 0
+        return ev
+
+    def record(self, ev, stream):
+        assert self.lib.hipEventRecord(ev, ctypes.c_void_p(stream)) == 0
+
+    def elapsed_ms(self, start, stop) -> float:
+        assert self.lib.hipEventSynchronize(stop) == 0
+        ms = ctypes.c_float()
+        assert self.lib.hipEventElapsedTime(ctypes.byref(ms), start, stop) == 0
+        return float(ms.value)
+
+
+def upload_q4_matrix(buf: kl.Buffer, k: int, n: int, seed: int) -> None:
+    rng = np.random.Generator(np.random.PCG64(seed))
+    row_bytes = k // 32 * 18
+    chunk = 2048
+    for r0 in range(0, n, chunk):
+        rows = min(chunk, n - r0)
+        w = (rng.standard_normal((rows, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+        buf.upload(kl.quantize_q4_0(w), offset=r0 * row_bytes)
+
+
+def cpu_baseline(seconds: float) -> dict | None:
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import _oracle
+    _, k, n = DOMINANT
+    rng = np.random.Generator(np.random.PCG64(99))
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    dec = _oracle.Oracle().q4_decode(kl.quantize_q4_0(w), k, n)
+    x = rng.standard_normal((1, k), dtype=np.float32)
+    ref = _oracle.ReferenceOracle.load()
+    if ref is not None:
+        run, kind, cores = (lambda: ref.reference(dec, x)), "reference", 6
+        what = "kref_reference = reference bench/native-q4-reference.h:98-108 (FP64, 6 OpenMP threads)"
+    else:
+        orc = _oracle.Oracle()
+        run, kind, cores = (lambda: orc.gold(dec, x, threads=6)), "port", 6
+        what = "oracle orc_gold (FP64 restatement of library-bench.cpp:121-122, 6 OpenMP threads)"
+    run()
+    reps, start = 0, time.perf_counter()
+    while True:
+        run()
+        reps += 1
+        elapsed = time.perf_counter() - start
+        if elapsed >= seconds or reps >= 10000:
+            break
+    per_call = elapsed / reps
+    return {"value": round(q4_bytes(k, n) / per_call / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": kind,
+            "sample": f"{what}; K{k}xN{n} batch 1 decoded Q4_0 weights, {reps} calls in {elapsed:.1f} s, "
+                      f"{per_call * 1e3:.3f} ms/call, host cpus={os.cpu_count()}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--kernel-reps", type=int, default=300, help="launches of the dominant GEMV for roofline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=[name for name, _, _ in LAYER],
+                    help="profiling aid: time only this GEMV's launch loop (no layer set, no CPU leg)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (this build has no "
+              "multi-GPU path)", file=sys.stderr)
+        return 2
+
+    kl.load()
+    device = 0
+    events = HipEvents()
+    stream = kl.stream(device)
+    kernel = kl.Kernel()
+
+    log("generating and uploading weights")
+    # copies[name][c]: distinct device copies of each matrix, at least
+    # ROTATE_BYTES per shape, so every launch reads its weights from HBM.
+    copies = {}
+    for i, (name, k, n) in enumerate(LAYER):
+        if args.only and name != args.only:
+            continue
+        nbytes = n * (k // 32) * 18
+        first = kl.Buffer(device, nbytes)
+        upload_q4_matrix(first, k, n, seed=1000 + i)
+        bufs = [first]
+        for _ in range(max(COPIES, -(-ROTATE_BYTES // nbytes)) - 1):
+            buf = kl.Buffer(device, nbytes)
+            with kl.runtime_mutex():
+                kl.select(device)
+                kl.check(kl.copy(buf.data, first.data, nbytes, kl.CopyKind.device_to_device))
+                kl.check(kl.wait())
+            bufs.append(buf)
+        copies[name] = bufs
+    rng = np.random.Generator(np.random.PCG64(7))
+    xs, ys = {}, {}
+    for name, k, n in LAYER:
+        xb = kl.Buffer(device, 4 * k)
+        xb.upload(rng.standard_normal(k, dtype=np.float32))
+        xs[name] = xb
+        ys[name] = kl.Buffer(device, 4 * n)
+
+    def weights(name: str, i: int) -> int:
+        bufs = copies[name]
+        return bufs[i % len(bufs)].data
+
+    def step(i: int) -> None:
+        for name, k, n in LAYER:
+            kl.matmul(kernel, device, ys[name].data, weights(name, i), xs[name].data, k, n, 1, kl.WeightType.q4_0)
+
+    host_us = {}
+
+    def timed(fn, count: int, warmup: int, tag: str = "") -> float:
+        with kl.runtime_mutex():
+            for i in range(warmup):
+                fn(i)
+            kl.select(device)
+            kl.check(kl.wait())
+            start, stop = events.create(), events.create()
+            events.record(start, stream)
+            t0 = time.perf_counter()
+            for i in range(count):
+                fn(i)
+            host_us[tag] = (time.perf_counter() - t0) * 1e6 / count
+            events.record(stop, stream)
+            ms = events.elapsed_ms(start, stop)
+            kl.check(kl.wait())
+        return ms
+
+    if args.only:
+        name, k, n = next(item for item in LAYER if item[0] == args.only)
+
+        def only(i):
+            kl.matmul(kernel, device, ys[name].data, weights(name, i), xs[name].data, k, n, 1, kl.WeightType.q4_0)
+        ms = timed(only, args.kernel_reps, args.warmup, "only") / args.kernel_reps
+        print(json.dumps({"only": name, "k": k, "n": n, "us_per_launch": round(ms * 1e3, 3),
+                          "host_us_per_call": round(host_us["only"], 3),
+                          "gbps": round(q4_bytes(k, n) / (ms * 1e-3) / 1e9, 1), "route": kernel.route}), flush=True)
+        return 0
+
+    log("timing the layer set")
+    wall0 = time.perf_counter()
+    step_ms = timed(step, args.steps, args.warmup) / args.steps
+    wall_ms = (time.perf_counter() - wall0) * 1e3
+    step_bytes = sum(q4_bytes(k, n) for _, k, n in LAYER)
+    value = step_bytes / (step_ms * 1e-3) / 1e9
+
+    per_shape = {}
+    for name, k, n in LAYER:
+        def one(i, name=name, k=k, n=n):
+            kl.matmul(kernel, device, ys[name].data, weights(name, i), xs[name].data, k, n, 1, kl.WeightType.q4_0)
+        ms = timed(one, args.kernel_reps, 5) / args.kernel_reps
+        gbps = q4_bytes(k, n) / (ms * 1e-3) / 1e9
+        per_shape[f"{name}_k{k}_n{n}"] = {"us": round(ms * 1e3, 3), "gbps": round(gbps, 1),
+                                           "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)}
+    dname, dk, dn = DOMINANT
+    dom = per_shape[f"{dname}_k{dk}_n{dn}"]
+    achieved = dom["gbps"]
+
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: Q4_0 from seeded N(0,0.02) (ggml closed form), X ~ N(0,1) f32",
+        "config": {
+            "workload": "llama7b-decode-layer-q4_0-gemv-b1 (BASELINE configs[1])",
+            "shapes_k_n": [[k, n] for _, k, n in LAYER],
+            "batch": 1,
+            "bytes_per_step": step_bytes,
+            "rotating_copies_per_shape": {name: len(bufs) for name, bufs in copies.items()},
+            "weight_set_mb": round(sum(n * (k // 32) * 18 for _, k, n in LAYER) / 1e6, 1),
+            "route": kernel.route,
+            "wall_ms_timed_region": round(wall_ms, 3),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": f"q4 GEMV K{dk}xN{dn} b1 ({kernel.route})",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "bytes_per_launch": q4_bytes(dk, dn),
+            "avg_launch_us": dom["us"],
+        },
+        "cpu_baseline": cpu,
+        "per_shape": per_shape,
+    }
+    print(json.dumps(result), flush=True)
+    for bufs in copies.values():
+        for buf in bufs:
+            buf.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,109 @@
+// KunlunK200 matmul surface, implemented for AMD Instinct MI355X (gfx950).
+//
+// This header keeps the declarations, argument meaning, defaults and class
+// layouts of the matmul subset of the reference library's public header
+// (reference include/kunlun/k200.h:10-37, 40, 62-105, 345-350) so a consumer
+// of that subset rebuilds against this library unchanged. Declarations of the
+// reference that are not on the matmul path (attention, SwiGLU, Q6_K, native
+// and common Q4 layouts, elementwise, KV caches) are not declared here.
+//
+// Device numbering: the reference drives the two processing dies of one
+// Kunlun card as devices 0 and 1. Here a device is one HIP device (one GPU);
+// valid ids are [0, device_count()), at most kunlun::max_devices.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <mutex>
+
+namespace kunlun {
+
+constexpr int max_devices = 8;
+
+// Process-wide lock around device selection, allocation and submission
+// (reference k200.h:10). Callers hold it around raw select/copy/wait runs.
+std::recursive_mutex & runtime_mutex();
+// Fail fast: print the diagnostic context and abort when status != 0
+// (reference k200.h:11).
+void check(int status);
+// Optional borrowed tensor name; dimensions are copied (reference k200.h:13).
+void diagnostic_tensor(const char * name, const int64_t * dimensions = nullptr);
+// Fail fast when the condition is false (reference k200.h:14).
+void require(bool condition);
+int device_count(int * count);                       // reference k200.h:15
+void select(int device);                             // reference k200.h:16
+// Completes every operation submitted to the selected device (reference k200.h:17).
+int wait();
+enum CopyKind { host_to_device, device_to_host, device_to_device };
+// Submits a copy on the selected device; wait() completes it (reference k200.h:18-19).
+int copy(void * dst, const void * src, size_t bytes, CopyKind kind);
+// Device-to-device copy between GPUs; completes before returning (reference k200.h:20).
+void peer(int dst_device, void * dst, int src_device, const void * src, size_t bytes);
+void * allocate(int device, size_t bytes);           // reference k200.h:21, nullptr on failure
+void release(int device, void * ptr, size_t bytes);  // reference k200.h:22
+size_t allocated_bytes(int device);                  // reference k200.h:23
+
+// RAII device allocation (reference k200.h:25-37).
+class Buffer {
+public:
+    Buffer(int device, size_t bytes);
+    ~Buffer();
+    Buffer(const Buffer &) = delete;
+    Buffer & operator=(const Buffer &) = delete;
+    void * data() const { return ptr_; }
+    size_t size() const { return bytes_; }
+private:
+    int device_;
+    size_t bytes_;
+    void * ptr_;
+};
+
+// Values match the reference enumeration (reference k200.h:40). q6_k is not
+// accepted by matmul, as in the reference.
+enum class WeightType { f32 = 0, f16 = 1, q4_0 = 2, rowwise_i8 = 3, q6_k = 4 };
+
+// Per-call state owner: binds to the first device it is used on and owns
+// lazily grown device workspaces (reference k200.h:62-88).
+class Kernel {
+public:
+    Kernel();
+    ~Kernel();
+    Kernel(const Kernel &) = delete;
+    Kernel & operator=(const Kernel &) = delete;
+    struct Impl;
+private:
+    Impl * impl_;
+    friend void matmul(Kernel &, int, void *, const void *, const void *, int, int, int,
+                       WeightType, const float *, const float *, int);
+};
+
+// Packed rowwise INT8 weight layout (reference k200.h:90-96):
+// [aligned(k*rows) int8 codes][aligned(4*rows) f32 row scales][256 B maxima].
+size_t aligned(size_t bytes);
+size_t packed_i8_size(int k, int rows);
+float * packed_i8_scales(void * weights, int k, int rows);
+float * packed_i8_maxima(void * weights, int k, int rows);
+// Quantizes F32 host rows and uploads them to a caller-owned
+// packed_i8_size(k, rows) device allocation. Completes before returning.
+void upload_i8_rows(int device, void * weights, int k, int rows,
+                    int first_row, int count, const float * input);
+
+// W: [n,k], X: [batch,k], Y: [batch,n]. All pointers refer to device memory.
+// Q4_0: 18-byte blocks (little-endian F16 scale + 16 paired 4-bit values).
+// rowwise_i8 requires scales[n] and maxima[6], also in device memory.
+// matmul submits work; select(device) + check(wait()) completes it.
+// K must be divisible by 32, K <= 16384 (reference k200.h:98-105).
+void matmul(Kernel &, int device, void * y, const void * w, const void * x,
+            int k, int n, int batch, WeightType type,
+            const float * scales = nullptr, const float * maxima = nullptr, int tile = 16);
+
+// Same layout as the reference (reference k200.h:345-350): matmul submissions
+// on devices 0 and 1, peer copy count and bytes.
+struct Statistics {
+    size_t matmuls[2];
+    size_t peer_copies, peer_bytes;
+};
+Statistics statistics();
+const char * version();
+
+} // namespace kunlun

@@ -1,0 +1,99 @@
+/* C ABI of the KunlunK200 matmul path for MI355X (gfx950).
+ *
+ * Plain pointers and sizes, no C++ or HIP types in the signatures, so that
+ * ctypes, cgo, JNI or any C caller binds the library directly. Each function
+ * forwards to the C++ drop-in surface in <kunlun/k200.h> and keeps its
+ * argument meaning and fail-fast error behaviour: invalid arguments and device
+ * errors print a diagnostic and abort(), as the reference does
+ * (reference src/k200.cpp:53-62). Functions that only exist in this library
+ * say so.
+ *
+ * All device pointers are HIP device addresses. Work is submitted to one HIP
+ * stream per device, owned by the library (kunlun_stream()).
+ */
+#ifndef KUNLUN_K200_C_H
+#define KUNLUN_K200_C_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Opaque handle that owns one kunlun::Kernel (reference include/kunlun/k200.h:62-88). */
+typedef struct kunlun_kernel kunlun_kernel;
+
+/* Copy directions, same values as kunlun::CopyKind (reference include/kunlun/k200.h:18). */
+enum { KUNLUN_HOST_TO_DEVICE = 0, KUNLUN_DEVICE_TO_HOST = 1, KUNLUN_DEVICE_TO_DEVICE = 2 };
+/* Weight formats, same values as kunlun::WeightType (reference include/kunlun/k200.h:40). */
+enum { KUNLUN_F32 = 0, KUNLUN_F16 = 1, KUNLUN_Q4_0 = 2, KUNLUN_ROWWISE_I8 = 3, KUNLUN_Q6_K = 4 };
+
+/* runtime_mutex() lock/unlock (reference include/kunlun/k200.h:10). Recursive. */
+void kunlun_lock(void);
+void kunlun_unlock(void);
+/* check() / require() (reference include/kunlun/k200.h:11,14): abort on failure. */
+void kunlun_check(int status);
+void kunlun_require(int condition);
+/* diagnostic_tensor() (reference include/kunlun/k200.h:13); dimensions may be NULL. */
+void kunlun_diagnostic_tensor(const char *name, const int64_t *dimensions);
+/* device_count() (reference include/kunlun/k200.h:15); returns a HIP status. */
+int kunlun_device_count(int *count);
+/* select() (reference include/kunlun/k200.h:16). */
+void kunlun_select(int device);
+/* wait() (reference include/kunlun/k200.h:17); returns a HIP status. */
+int kunlun_wait(void);
+/* copy() (reference include/kunlun/k200.h:19); kind is a KUNLUN_*_TO_* value. */
+int kunlun_copy(void *dst, const void *src, size_t bytes, int kind);
+/* peer() (reference include/kunlun/k200.h:20). */
+void kunlun_peer(int dst_device, void *dst, int src_device, const void *src, size_t bytes);
+/* allocate() / release() / allocated_bytes() (reference include/kunlun/k200.h:21-23). */
+void *kunlun_allocate(int device, size_t bytes);
+void kunlun_release(int device, void *ptr, size_t bytes);
+size_t kunlun_allocated_bytes(int device);
+
+/* Kernel::Kernel() / Kernel::~Kernel() (reference include/kunlun/k200.h:62-66). */
+kunlun_kernel *kunlun_kernel_create(void);
+void kunlun_kernel_destroy(kunlun_kernel *kernel);
+
+/* aligned() / packed_i8_size() / packed_i8_scales() / packed_i8_maxima()
+ * (reference include/kunlun/k200.h:90-93). */
+size_t kunlun_aligned(size_t bytes);
+size_t kunlun_packed_i8_size(int k, int rows);
+float *kunlun_packed_i8_scales(void *weights, int k, int rows);
+float *kunlun_packed_i8_maxima(void *weights, int k, int rows);
+/* upload_i8_rows() (reference include/kunlun/k200.h:95-96); input is host memory. */
+void kunlun_upload_i8_rows(int device, void *weights, int k, int rows,
+                           int first_row, int count, const float *input);
+
+/* matmul() (reference include/kunlun/k200.h:103-105). Submits Y[batch,n] =
+ * X[batch,k] * W[n,k]^T; kunlun_select(device) + kunlun_wait() completes it.
+ * scales/maxima are required for KUNLUN_ROWWISE_I8 and ignored otherwise;
+ * tile must be 1 or 16 (accepted for compatibility, no effect on results). */
+void kunlun_matmul(kunlun_kernel *kernel, int device, void *y, const void *w, const void *x,
+                   int k, int n, int batch, int type,
+                   const float *scales, const float *maxima, int tile);
+
+/* statistics() (reference include/kunlun/k200.h:345-349) as four counters:
+ * out[0..1] = matmul submissions on devices 0 and 1, out[2] = peer copies,
+ * out[3] = peer bytes. */
+void kunlun_statistics(size_t out[4]);
+/* version() (reference include/kunlun/k200.h:350). */
+const char *kunlun_version(void);
+
+/* --- Functions of this library without a counterpart in the reference --- */
+
+/* Matmul submissions on any device (statistics() only reports devices 0 and 1). */
+size_t kunlun_matmul_count(int device);
+/* The hipStream_t the library submits to on `device`, as void*. Callers that
+ * time work with HIP events record them on this stream. */
+void *kunlun_stream(int device);
+/* Name of the kernel route the last matmul on `kernel` took (for tests and
+ * profiling, e.g. "q4_gemv_pair"); NULL before the first call. */
+const char *kunlun_kernel_route(const kunlun_kernel *kernel);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KUNLUN_K200_C_H */

@@ -1,0 +1,289 @@
+"""Python host interface to the KunlunK200 matmul path on MI355X (gfx950).
+
+This mirrors the reference's C++ surface (reference include/kunlun/k200.h:10-105,
+345-350) over the library's C ABI (include/kunlun/k200_c.h): same names, same
+argument meaning, same fail-fast behaviour (invalid arguments abort the
+process, as the reference's require() does). Device memory is owned through
+`Buffer`; numpy arrays move in and out with `Buffer.upload` / `Buffer.download`.
+
+The compiled library is `kunlunk200_lib_amd/lib/libkunlunk200.so.0`, built by
+`__graft_entry__.build()` (make -C kunlunk200_lib_amd/csrc). Loading fails
+loudly when it is missing: there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+import os
+import threading
+from contextlib import contextmanager
+
+import numpy as np
+
+from .formats import q4_0_row_bytes, quantize_q4_0, weight_bytes  # noqa: F401
+
+PACKAGE_DIR = os.path.dirname(os.path.abspath(__file__))
+LIBRARY_PATH = os.path.join(PACKAGE_DIR, "lib", "libkunlunk200.so.0")
+
+_lib = None
+_lib_lock = threading.Lock()
+
+_c_size = ctypes.c_size_t
+_c_void_p = ctypes.c_void_p
+_c_int = ctypes.c_int
+
+# (name, restype, argtypes) for every function of include/kunlun/k200_c.h.
+C_FUNCTIONS = [
+    ("kunlun_lock", None, []),
+    ("kunlun_unlock", None, []),
+    ("kunlun_check", None, [_c_int]),
+    ("kunlun_require", None, [_c_int]),
+    ("kunlun_diagnostic_tensor", None, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64)]),
+    ("kunlun_device_count", _c_int, [ctypes.POINTER(_c_int)]),
+    ("kunlun_select", None, [_c_int]),
+    ("kunlun_wait", _c_int, []),
+    ("kunlun_copy", _c_int, [_c_void_p, _c_void_p, _c_size, _c_int]),
+    ("kunlun_peer", None, [_c_int, _c_void_p, _c_int, _c_void_p, _c_size]),
+    ("kunlun_allocate", _c_void_p, [_c_int, _c_size]),
+    ("kunlun_release", None, [_c_int, _c_void_p, _c_size]),
+    ("kunlun_allocated_bytes", _c_size, [_c_int]),
+    ("kunlun_kernel_create", _c_void_p, []),
+    ("kunlun_kernel_destroy", None, [_c_void_p]),
+    ("kunlun_aligned", _c_size, [_c_size]),
+    ("kunlun_packed_i8_size", _c_size, [_c_int, _c_int]),
+    ("kunlun_packed_i8_scales", _c_void_p, [_c_void_p, _c_int, _c_int]),
+    ("kunlun_packed_i8_maxima", _c_void_p, [_c_void_p, _c_int, _c_int]),
+    ("kunlun_upload_i8_rows", None, [_c_int, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p]),
+    ("kunlun_matmul", None, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
+                             _c_int, _c_void_p, _c_void_p, _c_int]),
+    ("kunlun_statistics", None, [ctypes.POINTER(_c_size)]),
+    ("kunlun_version", ctypes.c_char_p, []),
+    ("kunlun_matmul_count", _c_size, [_c_int]),
+    ("kunlun_stream", _c_void_p, [_c_int]),
+    ("kunlun_kernel_route", ctypes.c_char_p, [_c_void_p]),
+]
+
+
+def load(path: str | None = None) -> ctypes.CDLL:
+    """Load the HIP library (once) and declare every C entry point."""
+    global _lib
+    with _lib_lock:
+        if _lib is not None:
+            return _lib
+        path = path or LIBRARY_PATH
+        if not os.path.exists(path):
+            raise RuntimeError(
+                f"KunlunK200 HIP library not built: {path} is missing "
+                "(run __graft_entry__.build() or make -C kunlunk200_lib_amd/csrc)")
+        lib = ctypes.CDLL(path)
+        for name, restype, argtypes in C_FUNCTIONS:
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = lib
+        return lib
+
+
+class WeightType(enum.IntEnum):
+    """reference include/kunlun/k200.h:40"""
+    f32 = 0
+    f16 = 1
+    q4_0 = 2
+    rowwise_i8 = 3
+    q6_k = 4
+
+
+class CopyKind(enum.IntEnum):
+    """reference include/kunlun/k200.h:18"""
+    host_to_device = 0
+    device_to_host = 1
+    device_to_device = 2
+
+
+def _ptr(value) -> int | None:
+    if value is None:
+        return None
+    if isinstance(value, Buffer):
+        return value.data
+    if isinstance(value, np.ndarray):
+        return value.ctypes.data
+    return int(value)
+
+
+@contextmanager
+def runtime_mutex():
+    """Hold the process-wide recursive runtime lock (reference k200.h:10)."""
+    lib = load()
+    lib.kunlun_lock()
+    try:
+        yield
+    finally:
+        lib.kunlun_unlock()
+
+
+def check(status: int) -> None:
+    load().kunlun_check(int(status))
+
+
+def require(condition: bool) -> None:
+    load().kunlun_require(1 if condition else 0)
+
+
+def device_count() -> int:
+    count = _c_int(0)
+    check(load().kunlun_device_count(ctypes.byref(count)))
+    return count.value
+
+
+def select(device: int) -> None:
+    load().kunlun_select(int(device))
+
+
+def wait() -> int:
+    return load().kunlun_wait()
+
+
+def copy(dst, src, nbytes: int, kind: CopyKind) -> int:
+    return load().kunlun_copy(_ptr(dst), _ptr(src), int(nbytes), int(kind))
+
+
+def peer(dst_device: int, dst, src_device: int, src, nbytes: int) -> None:
+    load().kunlun_peer(int(dst_device), _ptr(dst), int(src_device), _ptr(src), int(nbytes))
+
+
+def allocate(device: int, nbytes: int) -> int | None:
+    return load().kunlun_allocate(int(device), int(nbytes))
+
+
+def release(device: int, ptr, nbytes: int) -> None:
+    load().kunlun_release(int(device), _ptr(ptr), int(nbytes))
+
+
+def allocated_bytes(device: int) -> int:
+    return load().kunlun_allocated_bytes(int(device))
+
+
+def aligned(nbytes: int) -> int:
+    return load().kunlun_aligned(int(nbytes))
+
+
+def packed_i8_size(k: int, rows: int) -> int:
+    return load().kunlun_packed_i8_size(int(k), int(rows))
+
+
+def packed_i8_scales(weights, k: int, rows: int) -> int:
+    return load().kunlun_packed_i8_scales(_ptr(weights), int(k), int(rows))
+
+
+def packed_i8_maxima(weights, k: int, rows: int) -> int:
+    return load().kunlun_packed_i8_maxima(_ptr(weights), int(k), int(rows))
+
+
+def upload_i8_rows(device: int, weights, k: int, rows: int, first_row: int, count: int,
+                   values: np.ndarray) -> None:
+    """Quantize F32 host rows [count, k] and upload them (reference k200.h:95-96)."""
+    values = np.ascontiguousarray(values, dtype=np.float32)
+    if values.size < count * k:
+        raise ValueError("upload_i8_rows: input holds fewer than count*k values")
+    load().kunlun_upload_i8_rows(int(device), _ptr(weights), int(k), int(rows), int(first_row), int(count),
+                                 values.ctypes.data)
+
+
+class Buffer:
+    """RAII device allocation (reference k200.h:25-37)."""
+
+    def __init__(self, device: int, nbytes: int):
+        self.device = int(device)
+        self.size = int(nbytes)
+        ptr = allocate(self.device, self.size)
+        require(ptr is not None and ptr != 0)
+        self.data = int(ptr)
+
+    def close(self) -> None:
+        if self.data:
+            release(self.device, self.data, self.size)
+            self.data = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def upload(self, array: np.ndarray, offset: int = 0) -> None:
+        array = np.ascontiguousarray(array)
+        if offset < 0 or offset + array.nbytes > self.size:
+            raise ValueError("Buffer.upload: out of range")
+        with runtime_mutex():
+            select(self.device)
+            check(copy(self.data + offset, array, array.nbytes, CopyKind.host_to_device))
+            check(wait())
+
+    def download(self, shape, dtype, offset: int = 0) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        if offset < 0 or offset + out.nbytes > self.size:
+            raise ValueError("Buffer.download: out of range")
+        with runtime_mutex():
+            select(self.device)
+            check(copy(out, self.data + offset, out.nbytes, CopyKind.device_to_host))
+            check(wait())
+        return out
+
+
+class Kernel:
+    """Per-call state owner bound to one device (reference k200.h:62-88)."""
+
+    def __init__(self):
+        self.handle = load().kunlun_kernel_create()
+        require(bool(self.handle))
+
+    def close(self) -> None:
+        if self.handle:
+            load().kunlun_kernel_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def route(self) -> str | None:
+        name = load().kunlun_kernel_route(self.handle)
+        return name.decode() if name else None
+
+
+def matmul(kernel: Kernel, device: int, y, w, x, k: int, n: int, batch: int, type: WeightType,
+           scales=None, maxima=None, tile: int = 16) -> None:
+    """Submit Y[batch,n] = X[batch,k] . W[n,k]^T (reference k200.h:103-105).
+
+    All pointers are device memory; select(device) + check(wait()) completes it.
+    """
+    load().kunlun_matmul(kernel.handle, int(device), _ptr(y), _ptr(w), _ptr(x), int(k), int(n), int(batch),
+                         int(type), _ptr(scales), _ptr(maxima), int(tile))
+
+
+def statistics() -> dict:
+    out = (_c_size * 4)()
+    load().kunlun_statistics(out)
+    return {"matmuls": [out[0], out[1]], "peer_copies": out[2], "peer_bytes": out[3]}
+
+
+def version() -> str:
+    return load().kunlun_version().decode()
+
+
+def matmul_count(device: int) -> int:
+    return load().kunlun_matmul_count(int(device))
+
+
+def stream(device: int) -> int:
+    """The HIP stream (as an integer handle) the library submits to on `device`."""
+    return load().kunlun_stream(int(device))

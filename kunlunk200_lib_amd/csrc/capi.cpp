@@ -1,0 +1,70 @@
+// extern "C" entry points declared in include/kunlun/k200_c.h. Each forwards
+// to the C++ surface and keeps its argument meaning and fail-fast behaviour.
+#include <kunlun/k200_c.h>
+
+#include "runtime_internal.h"
+
+struct kunlun_kernel {
+    kunlun::Kernel kernel;
+    const char * route = nullptr;
+};
+
+extern "C" {
+
+void kunlun_lock(void) { kunlun::runtime_mutex().lock(); }
+void kunlun_unlock(void) { kunlun::runtime_mutex().unlock(); }
+void kunlun_check(int status) { kunlun::check(status); }
+void kunlun_require(int condition) { kunlun::require(condition != 0); }
+void kunlun_diagnostic_tensor(const char * name, const int64_t * dimensions) {
+    kunlun::diagnostic_tensor(name, dimensions);
+}
+int kunlun_device_count(int * count) { return kunlun::device_count(count); }
+void kunlun_select(int device) { kunlun::select(device); }
+int kunlun_wait(void) { return kunlun::wait(); }
+int kunlun_copy(void * dst, const void * src, size_t bytes, int kind) {
+    kunlun::require(kind >= KUNLUN_HOST_TO_DEVICE && kind <= KUNLUN_DEVICE_TO_DEVICE);
+    return kunlun::copy(dst, src, bytes, static_cast<kunlun::CopyKind>(kind));
+}
+void kunlun_peer(int dst_device, void * dst, int src_device, const void * src, size_t bytes) {
+    kunlun::peer(dst_device, dst, src_device, src, bytes);
+}
+void * kunlun_allocate(int device, size_t bytes) { return kunlun::allocate(device, bytes); }
+void kunlun_release(int device, void * ptr, size_t bytes) { kunlun::release(device, ptr, bytes); }
+size_t kunlun_allocated_bytes(int device) { return kunlun::allocated_bytes(device); }
+
+kunlun_kernel * kunlun_kernel_create(void) { return new kunlun_kernel(); }
+void kunlun_kernel_destroy(kunlun_kernel * kernel) { delete kernel; }
+
+size_t kunlun_aligned(size_t bytes) { return kunlun::aligned(bytes); }
+size_t kunlun_packed_i8_size(int k, int rows) { return kunlun::packed_i8_size(k, rows); }
+float * kunlun_packed_i8_scales(void * weights, int k, int rows) { return kunlun::packed_i8_scales(weights, k, rows); }
+float * kunlun_packed_i8_maxima(void * weights, int k, int rows) { return kunlun::packed_i8_maxima(weights, k, rows); }
+void kunlun_upload_i8_rows(int device, void * weights, int k, int rows, int first_row, int count,
+                           const float * input) {
+    kunlun::upload_i8_rows(device, weights, k, rows, first_row, count, input);
+}
+
+void kunlun_matmul(kunlun_kernel * kernel, int device, void * y, const void * w, const void * x, int k, int n,
+                   int batch, int type, const float * scales, const float * maxima, int tile) {
+    kunlun::require(kernel != nullptr);
+    kunlun::require(type >= KUNLUN_F32 && type <= KUNLUN_Q6_K);
+    kunlun::matmul(kernel->kernel, device, y, w, x, k, n, batch, static_cast<kunlun::WeightType>(type), scales,
+                   maxima, tile);
+    kernel->route = kunlun::detail::route_of_last_matmul();
+}
+
+void kunlun_statistics(size_t out[4]) {
+    kunlun::require(out != nullptr);
+    const kunlun::Statistics s = kunlun::statistics();
+    out[0] = s.matmuls[0];
+    out[1] = s.matmuls[1];
+    out[2] = s.peer_copies;
+    out[3] = s.peer_bytes;
+}
+const char * kunlun_version(void) { return kunlun::version(); }
+
+size_t kunlun_matmul_count(int device) { return kunlun::detail::matmul_count(device); }
+void * kunlun_stream(int device) { return static_cast<void *>(kunlun::detail::context(device).stream); }
+const char * kunlun_kernel_route(const kunlun_kernel * kernel) { return kernel ? kernel->route : nullptr; }
+
+}

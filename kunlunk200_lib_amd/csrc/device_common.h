@@ -1,0 +1,88 @@
+// Device helpers shared by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace kk {
+
+constexpr int kWave = 64;
+
+// IEEE binary16 bits -> binary32 (v_cvt_f32_f16): exact, subnormals included,
+// as the reference decoder (reference kernels/kunlun-matvec.xpu:4-18).
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
+    union { uint16_t u; _Float16 h; } v;
+    v.u = static_cast<uint16_t>(bits);
+    return static_cast<float>(v.h);
+}
+
+// Byte C of a 32-bit word as float, one v_cvt_f32_ubyte{C} instruction. The
+// compiler does not select the byte forms by itself once the word was masked
+// (it emits a bit-field extract first), so they are written out.
+template <int C>
+__device__ __forceinline__ float ubyte_to_float(uint32_t word) {
+    float r;
+    if constexpr (C == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(word));
+    else if constexpr (C == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(word));
+    else if constexpr (C == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(word));
+    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(word));
+    return r;
+}
+
+// Bytes [s, s+4) of the little-endian 64-bit value hi:lo (v_alignbyte_b32).
+__device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t s) {
+    return __builtin_amdgcn_alignbyte(hi, lo, s);
+}
+
+// DPP lane move within rows of 16 lanes (quad_perm / mirror controls).
+template <int Ctrl>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), Ctrl, 0xf, 0xf, false));
+}
+
+// Sum over the 64 lanes of a wave, returned uniformly (scalar) to every lane:
+// four DPP steps reduce each row of 16 lanes, then the four row sums are read.
+__device__ __forceinline__ float wave_sum_uniform(float v) {
+    v += dpp_move<0xb1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_move<0x4e>(v);    // quad_perm [2,3,0,1]
+    v += dpp_move<0x141>(v);   // row_half_mirror: quads 0<->1, 2<->3
+    v += dpp_move<0x140>(v);   // row_mirror: halves of the row
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+// Sum over the 64 lanes of a wave; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset, kWave));
+    return v;
+}
+
+// Round half away from zero by truncating v +/- 0.5f, clamp to [-limit, limit]:
+// the host rule of the reference (reference src/k200.cpp:114,217,224).
+// Written without contraction so it rounds exactly as the host does.
+__device__ __forceinline__ int round_clamp(float value, int limit) {
+#pragma clang fp contract(off)
+    float shifted = value + (value >= 0.0f ? 0.5f : -0.5f);
+    int q = static_cast<int>(shifted);
+    q = q > limit ? limit : q;
+    q = q < -limit ? -limit : q;
+    return q;
+}
+
+// 16-byte load from an address that is only 4-byte aligned (global_load_dwordx4).
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+__device__ __forceinline__ u32x4_a4 load_u32x4(const uint32_t *p) {
+    return *reinterpret_cast<const u32x4_a4 *>(p);
+}
+
+} // namespace kk

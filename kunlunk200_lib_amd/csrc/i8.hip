@@ -1,0 +1,374 @@
+// rowwise_i8 matmul on gfx950: device-side two-pass activation quantization
+// and int8 MFMA with exact int32 accumulation and a fused combine epilogue.
+//
+// Reference path (reference src/k200.cpp:189-240): X is copied to the host,
+// quantized per tensor in two passes (k200.cpp:212-225), uploaded, multiplied
+// by the int8 weight rows in a closed vendor FC (k200.cpp:231,234-235) and
+// combined as (P*max0/127 + R*max1/127) * scale[r]
+// (reference kernels/kunlun-combine.xpu:10-19). Here all of it stays on the
+// GPU: three quantization passes (or one single-workgroup pass for small X)
+// and one MFMA kernel.
+//
+// Workspace layout (device):
+//   codes    [2*batch][k] int8, row 2b = q0 of batch row b, row 2b+1 = q1
+//   partial0 [kMaxGroups] f32  per-workgroup max|x|
+//   partial1 [kMaxGroups] f32  per-workgroup max|r|
+//   final    [4] f32           max0, max1
+#include "device_common.h"
+#include "launch.h"
+
+#include <algorithm>
+#include <cstdlib>
+
+namespace {
+
+using kk::kWave;
+
+constexpr int kMaxGroups = 1024;
+constexpr int kQuantThreads = 256;
+constexpr int kFusedThreads = 1024;
+
+struct Workspace {
+    int8_t *codes;
+    float *partial0;
+    float *partial1;
+    float *final_max;
+};
+
+size_t align256(size_t bytes) { return (bytes + 255) & ~static_cast<size_t>(255); }
+
+__host__ __device__ inline Workspace layout(void *base, int k, int batch) {
+    char *p = static_cast<char *>(base);
+    const size_t codes = ((static_cast<size_t>(2) * batch * k) + 255) & ~static_cast<size_t>(255);
+    Workspace ws;
+    ws.codes = reinterpret_cast<int8_t *>(p);
+    ws.partial0 = reinterpret_cast<float *>(p + codes);
+    ws.partial1 = ws.partial0 + kMaxGroups;
+    ws.final_max = ws.partial1 + kMaxGroups;
+    return ws;
+}
+
+__device__ __forceinline__ void flag_nonfinite(int *status) {
+    __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Block-wide max over float values held by each thread; result on all threads.
+template <int Threads>
+__device__ float block_max(float v, float *scratch) {
+    v = kk::wave_max(v);
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    __syncthreads();
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < Threads / kWave; ++i) m = fmaxf(m, scratch[i]);
+    return m;
+}
+
+// Activation quantization arithmetic, rounded exactly as the reference host
+// code (reference src/k200.cpp:216-218,223-224): no contraction.
+__device__ __forceinline__ int quant_primary(float value, float max0) {
+#pragma clang fp contract(off)
+    const float inv = 127.0f / max0;
+    return kk::round_clamp(value * inv, 127);
+}
+__device__ __forceinline__ float residual_of(float value, int q0, float max0) {
+#pragma clang fp contract(off)
+    const float step = max0 / 127.0f;
+    const float product = static_cast<float>(q0) * step;
+    return value - product;
+}
+__device__ __forceinline__ int quant_residual(float residual, float max1) {
+#pragma clang fp contract(off)
+    const float inv = 127.0f / max1;
+    return kk::round_clamp(residual * inv, 127);
+}
+
+__device__ __forceinline__ size_t code_index(size_t flat, int k, int component) {
+    const size_t b = flat / static_cast<size_t>(k), j = flat - b * static_cast<size_t>(k);
+    return (2 * b + component) * static_cast<size_t>(k) + j;
+}
+
+// Pass 1: per-workgroup max|x| and non-finite detection.
+__global__ __launch_bounds__(kQuantThreads) void i8_pass_max(const float *__restrict__ x, size_t count,
+                                                            float *__restrict__ partial0, int *status) {
+    __shared__ float scratch[kQuantThreads / kWave];
+    float m = 0.0f;
+    bool bad = false;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * kQuantThreads + threadIdx.x; i < count;
+         i += static_cast<size_t>(gridDim.x) * kQuantThreads) {
+        const float v = x[i];
+        bad |= !isfinite(v);
+        m = fmaxf(m, fabsf(v));
+    }
+    if (bad) flag_nonfinite(status);
+    m = block_max<kQuantThreads>(m, scratch);
+    if (threadIdx.x == 0) partial0[blockIdx.x] = m;
+}
+
+// Pass 2: max0 from the partials, q0 codes, per-workgroup max|r|.
+__global__ __launch_bounds__(kQuantThreads) void i8_pass_primary(const float *__restrict__ x, size_t count, int k,
+                                                                const float *__restrict__ partial0, int groups,
+                                                                int8_t *__restrict__ codes,
+                                                                float *__restrict__ partial1) {
+    __shared__ float scratch[kQuantThreads / kWave];
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < groups; i += kQuantThreads) m = fmaxf(m, partial0[i]);
+    float max0 = block_max<kQuantThreads>(m, scratch);
+    if (max0 == 0.0f) max0 = 1.0f;
+    float m1 = 0.0f;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * kQuantThreads + threadIdx.x; i < count;
+         i += static_cast<size_t>(gridDim.x) * kQuantThreads) {
+        const float v = x[i];
+        const int q0 = quant_primary(v, max0);
+        codes[code_index(i, k, 0)] = static_cast<int8_t>(q0);
+        m1 = fmaxf(m1, fabsf(residual_of(v, q0, max0)));
+    }
+    m1 = block_max<kQuantThreads>(m1, scratch);
+    if (threadIdx.x == 0) partial1[blockIdx.x] = m1;
+}
+
+// Pass 3: max1 from the partials, q1 codes; workgroup 0 publishes max0/max1.
+__global__ __launch_bounds__(kQuantThreads) void i8_pass_residual(const float *__restrict__ x, size_t count, int k,
+                                                                 const float *__restrict__ partial0,
+                                                                 const float *__restrict__ partial1, int groups,
+                                                                 int8_t *__restrict__ codes,
+                                                                 float *__restrict__ final_max) {
+    __shared__ float scratch[kQuantThreads / kWave];
+    float m0 = 0.0f, m1 = 0.0f;
+    for (int i = threadIdx.x; i < groups; i += kQuantThreads) {
+        m0 = fmaxf(m0, partial0[i]);
+        m1 = fmaxf(m1, partial1[i]);
+    }
+    float max0 = block_max<kQuantThreads>(m0, scratch);
+    float max1 = block_max<kQuantThreads>(m1, scratch);
+    if (max0 == 0.0f) max0 = 1.0f;
+    if (max1 == 0.0f) max1 = 1.0f;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * kQuantThreads + threadIdx.x; i < count;
+         i += static_cast<size_t>(gridDim.x) * kQuantThreads) {
+        const float v = x[i];
+        const int q0 = quant_primary(v, max0);
+        codes[code_index(i, k, 1)] = static_cast<int8_t>(quant_residual(residual_of(v, q0, max0), max1));
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        final_max[0] = max0;
+        final_max[1] = max1;
+    }
+}
+
+// All three passes in one workgroup, for small X.
+__global__ __launch_bounds__(kFusedThreads) void i8_quantize_fused(const float *__restrict__ x, size_t count, int k,
+                                                                  int8_t *__restrict__ codes,
+                                                                  float *__restrict__ final_max, int *status) {
+    __shared__ float scratch[kFusedThreads / kWave];
+    float m = 0.0f;
+    bool bad = false;
+    for (size_t i = threadIdx.x; i < count; i += kFusedThreads) {
+        const float v = x[i];
+        bad |= !isfinite(v);
+        m = fmaxf(m, fabsf(v));
+    }
+    if (bad) flag_nonfinite(status);
+    float max0 = block_max<kFusedThreads>(m, scratch);
+    if (max0 == 0.0f) max0 = 1.0f;
+    float m1 = 0.0f;
+    for (size_t i = threadIdx.x; i < count; i += kFusedThreads) {
+        const float v = x[i];
+        const int q0 = quant_primary(v, max0);
+        codes[code_index(i, k, 0)] = static_cast<int8_t>(q0);
+        m1 = fmaxf(m1, fabsf(residual_of(v, q0, max0)));
+    }
+    float max1 = block_max<kFusedThreads>(m1, scratch);
+    if (max1 == 0.0f) max1 = 1.0f;
+    for (size_t i = threadIdx.x; i < count; i += kFusedThreads) {
+        const float v = x[i];
+        const int q0 = quant_primary(v, max0);
+        codes[code_index(i, k, 1)] = static_cast<int8_t>(quant_residual(residual_of(v, q0, max0), max1));
+    }
+    if (threadIdx.x == 0) {
+        final_max[0] = max0;
+        final_max[1] = max1;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// int8 MFMA matmul. v_mfma_i32_16x16x64_i8 operand layout (wave64):
+//   A (16 x 64): lane l holds A[l % 16][16*(l/16) .. +16)
+//   B (64 x 16): lane l holds B[16*(l/16) .. +16)[l % 16]
+//   D (16 x 16): lane l holds D[4*(l/16) + i][l % 16], i = 0..3
+// The reduction index is permuted so that each lane reads 64 contiguous bytes
+// per 256-value K step: in MFMA s (0..3) of a step at k0, lane group g = l/16
+// covers k0 + 64*g + 16*s .. +16, for A and B alike, so the four MFMAs sum
+// exactly the products of k0 .. k0+255.
+//
+// A = activation codes (rows: 2b -> q0, 2b+1 -> q1), B^T = weight rows. Lane
+// l then holds D rows 4g..4g+3 = (q0, q1) of batch rows 2g' and 2g'+1 for one
+// weight row, so the combine happens in registers.
+typedef int int32x4 __attribute__((ext_vector_type(4)));
+
+// (P*wmax*s0 + R*wmax*s1) * row_scale, rounded after every operation.
+__device__ __forceinline__ float combine(int primary, int residual, float wmax, float scale0, float scale1,
+                                         float row_scale) {
+#pragma clang fp contract(off)
+    const float p = static_cast<float>(primary) * wmax;
+    const float q = static_cast<float>(residual) * wmax;
+    const float t0 = p * scale0;
+    const float t1 = q * scale1;
+    return (t0 + t1) * row_scale;
+}
+
+template <int MT, int NT>
+__global__ __launch_bounds__(256) void i8_mfma_matmul(const int8_t *__restrict__ codes,
+                                                     const int8_t *__restrict__ w,
+                                                     const float *__restrict__ scales,
+                                                     const float *__restrict__ maxima,
+                                                     const float *__restrict__ final_max,
+                                                     float *__restrict__ y, int k, int n, int batch,
+                                                     int m_tiles_total, int n_tiles_total) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int m_groups = (m_tiles_total + MT - 1) / MT;
+    const int n_groups = (n_tiles_total + NT - 1) / NT;
+    if (wave >= m_groups * n_groups) return;
+    const int mg = wave % m_groups, ng = wave / m_groups;
+    const int rows = 2 * batch;
+    const int g = lane >> 4, c = lane & 15;
+
+    int32x4 acc[MT][NT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[i][j] = int32x4{0, 0, 0, 0};
+
+    const int8_t *arow[MT];
+    bool avalid[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+        const int r = (mg * MT + i) * 16 + c;
+        avalid[i] = r < rows;
+        arow[i] = codes + static_cast<size_t>(avalid[i] ? r : 0) * k;
+    }
+    const int8_t *brow[NT];
+    bool bvalid[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        const int r = (ng * NT + j) * 16 + c;
+        bvalid[j] = r < n;
+        brow[j] = w + static_cast<size_t>(bvalid[j] ? r : 0) * k;
+    }
+
+    for (int k0 = 0; k0 < k; k0 += 256) {
+        const int kb = k0 + 64 * g;
+        int32x4 af[MT][4], bf[NT][4];
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int kk0 = kb + 16 * s;
+                if (avalid[i] && kk0 < k) {
+                    const kk::u32x4_a4 v = kk::load_u32x4(reinterpret_cast<const uint32_t *>(arow[i] + kk0));
+                    af[i][s] = int32x4{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
+                } else {
+                    af[i][s] = int32x4{0, 0, 0, 0};
+                }
+            }
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int kk0 = kb + 16 * s;
+                if (bvalid[j] && kk0 < k) {
+                    const kk::u32x4_a4 v = kk::load_u32x4(reinterpret_cast<const uint32_t *>(brow[j] + kk0));
+                    bf[j][s] = int32x4{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
+                } else {
+                    bf[j][s] = int32x4{0, 0, 0, 0};
+                }
+            }
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int j = 0; j < NT; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i][s], bf[j][s], acc[i][j], 0, 0, 0);
+    }
+
+    // Epilogue: y[b, r] = (P*(max0/127) + R*(max1/127)) * scale[r], where the
+    // raw products are first scaled by the weight maximum / 127 as the FC's
+    // max-pointer convention does (the uploaded maxima are 127: exact no-op).
+    const float scale0 = final_max[0] / 127.0f;
+    const float scale1 = final_max[1] / 127.0f;
+    const float wmax = maxima[0] / 127.0f;
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        const int r = (ng * NT + j) * 16 + c;
+        if (r >= n) continue;
+        const float rs = scales[r];
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int b = (mg * MT + i) * 8 + 2 * g + h;
+                if (b >= batch) continue;
+                y[static_cast<size_t>(b) * n + r] =
+                    combine(acc[i][j][2 * h], acc[i][j][2 * h + 1], wmax, scale0, scale1, rs);
+            }
+        }
+    }
+}
+
+int env_int(const char *name, int fallback) {
+    const char *value = std::getenv(name);
+    return value && *value ? std::atoi(value) : fallback;
+}
+
+template <int MT, int NT>
+hipError_t launch_i8(const int8_t *codes, const int8_t *w, const float *scales, const float *maxima,
+                     const float *final_max, float *y, int k, int n, int batch, hipStream_t stream) {
+    const int m_tiles = (2 * batch + 15) / 16;
+    const int n_tiles = (n + 15) / 16;
+    const long long waves = static_cast<long long>((m_tiles + MT - 1) / MT) * ((n_tiles + NT - 1) / NT);
+    const int groups = static_cast<int>((waves + 3) / 4);
+    hipLaunchKernelGGL((i8_mfma_matmul<MT, NT>), dim3(groups), dim3(256), 0, stream, codes, w, scales, maxima,
+                       final_max, y, k, n, batch, m_tiles, n_tiles);
+    return hipGetLastError();
+}
+
+} // namespace
+
+extern "C" size_t kk_i8_workspace_bytes(int k, int batch) {
+    return align256(static_cast<size_t>(2) * batch * k) + (2 * kMaxGroups + 64) * sizeof(float);
+}
+
+extern "C" int kk_i8_quantize(const float *x, int k, int batch, void *workspace, int *status, hipStream_t stream) {
+    if (!x || !workspace || !status || k <= 0 || batch <= 0) return hipErrorInvalidValue;
+    const Workspace ws = layout(workspace, k, batch);
+    const size_t count = static_cast<size_t>(k) * batch;
+    const size_t fused_limit = static_cast<size_t>(env_int("KUNLUN_I8_FUSED_QUANT_LIMIT", 65536));
+    if (count <= fused_limit) {
+        hipLaunchKernelGGL(i8_quantize_fused, dim3(1), dim3(kFusedThreads), 0, stream, x, count, k, ws.codes,
+                           ws.final_max, status);
+        return hipGetLastError();
+    }
+    const int groups = static_cast<int>(std::min<size_t>(kMaxGroups, (count + kQuantThreads * 8 - 1) / (kQuantThreads * 8)));
+    hipLaunchKernelGGL(i8_pass_max, dim3(groups), dim3(kQuantThreads), 0, stream, x, count, ws.partial0, status);
+    hipLaunchKernelGGL(i8_pass_primary, dim3(groups), dim3(kQuantThreads), 0, stream, x, count, k, ws.partial0,
+                       groups, ws.codes, ws.partial1);
+    hipLaunchKernelGGL(i8_pass_residual, dim3(groups), dim3(kQuantThreads), 0, stream, x, count, k, ws.partial0,
+                       ws.partial1, groups, ws.codes, ws.final_max);
+    return hipGetLastError();
+}
+
+extern "C" int kk_i8_matmul(const void *workspace, const int8_t *w, const float *scales, const float *maxima,
+                            float *y, int k, int n, int batch, hipStream_t stream, const char **route) {
+    if (!workspace || !w || !scales || !maxima || !y || k <= 0 || (k & 31) || n <= 0 || batch <= 0)
+        return hipErrorInvalidValue;
+    const Workspace ws = layout(const_cast<void *>(workspace), k, batch);
+    if (batch <= 8) {
+        if (route) *route = "i8_mfma_gemv";
+        return launch_i8<1, 2>(ws.codes, w, scales, maxima, ws.final_max, y, k, n, batch, stream);
+    }
+    if (route) *route = "i8_mfma_gemm";
+    return launch_i8<4, 4>(ws.codes, w, scales, maxima, ws.final_max, y, k, n, batch, stream);
+}

@@ -1,0 +1,29 @@
+// Internal C ABI between the host runtime (C++) and the HIP kernel launchers.
+// Each launcher validates that its grid fits the shapes it is given, submits
+// to `stream` and returns 0 or a hipError_t. `route` (optional) receives a
+// static string naming the kernel path taken.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstddef>
+#include <cstdint>
+
+extern "C" {
+
+// Y[batch,n] = X[batch,k] * W[n,k]^T for F32 (type 0), F16 (1) and Q4_0 (2)
+// weights, F32 activations and outputs, F32 accumulation.
+int kk_dense_matmul(int type, const void *w, const float *x, float *y, int k, int n, int batch,
+                    hipStream_t stream, const char **route);
+
+// Bytes of device workspace kk_i8_quantize needs for `count` activations.
+size_t kk_i8_workspace_bytes(int k, int batch);
+// Two-pass per-tensor INT8 quantization of X[batch,k] into `workspace`
+// (codes and maxima). Sets *status (device memory) to 1 on a non-finite value.
+int kk_i8_quantize(const float *x, int k, int batch, void *workspace, int *status,
+                   hipStream_t stream);
+// Y = (P*max0/127 + R*max1/127) * scales[n] from exact int32 dot products of
+// the quantized activations in `workspace` with int8 weight rows W[n,k].
+int kk_i8_matmul(const void *workspace, const int8_t *w, const float *scales, const float *maxima,
+                 float *y, int k, int n, int batch, hipStream_t stream, const char **route);
+
+}

@@ -1,0 +1,81 @@
+// kunlun::Kernel and kunlun::matmul: argument validation exactly as the
+// reference (reference src/k200.cpp:268-279), then submission of the HIP
+// kernels for the weight format (reference dispatch src/k200.cpp:187-247).
+#include "launch.h"
+#include "runtime_internal.h"
+
+#include <climits>
+#include <cstdint>
+
+namespace kunlun {
+namespace detail {
+thread_local const char * last_route = nullptr;
+const char * route_of_last_matmul() { return last_route; }
+} // namespace detail
+
+Kernel::Kernel() : impl_(new Impl{}) {}
+
+Kernel::~Kernel() {
+    std::lock_guard<std::recursive_mutex> lock(detail::mutex());
+    if (impl_->id >= 0) {
+        select(impl_->id);
+        check(wait());
+        release(impl_->id, impl_->i8_workspace, impl_->i8_workspace_size);
+    }
+    delete impl_;
+}
+
+void matmul(Kernel & kernel, int id, void * y, const void * w, const void * x, int k, int n, int batch,
+            WeightType type, const float * scales, const float * maximum, int tile) {
+    std::lock_guard<std::recursive_mutex> lock(detail::mutex());
+    require(type == WeightType::f32 || type == WeightType::f16 || type == WeightType::q4_0 ||
+            type == WeightType::rowwise_i8);
+    require(k > 0 && k <= 16384 && k % 32 == 0 && n > 0 && batch > 0 && n <= INT_MAX / batch &&
+            k <= INT_MAX / batch);
+    require((size_t)n * batch <= INT_MAX / 4 && (size_t)k * batch <= INT_MAX / 4);
+    const size_t row_bytes = type == WeightType::f32   ? (size_t)k * 4
+                             : type == WeightType::f16 ? (size_t)k * 2
+                             : type == WeightType::q4_0 ? (size_t)k / 32 * 18
+                                                        : (size_t)k;
+    require(y && w && x && (size_t)n <= INT_MAX / row_bytes && (tile == 1 || tile == 16));
+    require(kernel.impl_->id == -1 || kernel.impl_->id == id);
+    require(type != WeightType::rowwise_i8 || (scales && maximum));
+    // F32 activations and outputs must be element aligned (an F32 array always is).
+    require(((uintptr_t)x & 3) == 0 && ((uintptr_t)y & 3) == 0);
+
+    detail::DeviceContext & ctx = detail::context(id);
+    Kernel::Impl & impl = *kernel.impl_;
+    impl.id = id;
+    if (type == WeightType::rowwise_i8) {
+        require(((uintptr_t)w & 3) == 0 && ((uintptr_t)scales & 3) == 0 && ((uintptr_t)maximum & 3) == 0);
+        const size_t need = kk_i8_workspace_bytes(k, batch);
+        if (impl.i8_workspace_size < need) {
+            if (impl.i8_workspace) {
+                detail::check_hip(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize");
+                release(id, impl.i8_workspace, impl.i8_workspace_size);
+                impl.i8_workspace = nullptr;
+                impl.i8_workspace_size = 0;
+            }
+            impl.i8_workspace = allocate(id, need);
+            require(impl.i8_workspace != nullptr);
+            impl.i8_workspace_size = need;
+        }
+        detail::check_hip((hipError_t)kk_i8_quantize(static_cast<const float *>(x), k, batch, impl.i8_workspace,
+                                                     ctx.status, ctx.stream),
+                          "kk_i8_quantize");
+        ctx.status_pending = true;
+        detail::check_hip((hipError_t)kk_i8_matmul(impl.i8_workspace, static_cast<const int8_t *>(w), scales,
+                                                   maximum, static_cast<float *>(y), k, n, batch, ctx.stream,
+                                                   &impl.route),
+                          "kk_i8_matmul");
+    } else {
+        detail::check_hip((hipError_t)kk_dense_matmul((int)type, w, static_cast<const float *>(x),
+                                                      static_cast<float *>(y), k, n, batch, ctx.stream,
+                                                      &impl.route),
+                          "kk_dense_matmul");
+    }
+    detail::last_route = impl.route;
+    detail::count_matmul(id);
+}
+
+} // namespace kunlun

@@ -1,0 +1,44 @@
+// Host runtime state shared by the C++ surface, the matmul dispatcher and the
+// C ABI. Not installed.
+#pragma once
+
+#include <kunlun/k200.h>
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstddef>
+
+namespace kunlun {
+namespace detail {
+
+// Per-device submission state, created on first use of a device.
+struct DeviceContext {
+    bool ready = false;
+    hipStream_t stream = nullptr;
+    int *status = nullptr;          // device word written by kernels on bad input
+    bool status_pending = false;    // a submitted kernel may have written it
+};
+
+std::recursive_mutex & mutex();
+// Selects `device` and returns its context, creating stream and status word.
+DeviceContext & context(int device);
+int current_device();
+void count_matmul(int device);
+size_t matmul_count(int device);
+// Abort with the diagnostic context and a message (the require() text).
+[[noreturn]] void fail(const char * message);
+// Abort when a HIP call fails, naming the call.
+void check_hip(hipError_t status, const char * what);
+// Kernel route taken by the calling thread's last matmul (static string).
+const char * route_of_last_matmul();
+
+} // namespace detail
+
+struct Kernel::Impl {
+    int id = -1;
+    void * i8_workspace = nullptr;
+    size_t i8_workspace_size = 0;
+    const char * route = nullptr;
+};
+
+} // namespace kunlun

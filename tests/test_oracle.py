@@ -1,0 +1,238 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+
+Each oracle function is checked against something other than its own formula:
+the reference's own CPU oracle header compiled from the reference checkout
+(golden vectors in tests/golden/, and the live oracle/_ref build when present),
+numpy's float16 conversions, brute force and closed forms of the reference's
+deterministic bench data.
+"""
+import os
+
+import numpy as np
+import pytest
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "native_q4_reference.npz")
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(GOLDEN, allow_pickle=False)
+
+
+# --- against the reference's own CPU oracle (golden vectors) ---------------
+
+def test_fixture_q4_bytes_match_reference(oracle, golden):
+    k, n = int(golden["k"]), int(golden["n"])
+    assert np.array_equal(oracle.fixture_q4(k, n), golden["q4"])
+
+
+def test_q4_decode_matches_reference_decoded(oracle, golden):
+    k, n = int(golden["k"]), int(golden["n"])
+    dec = oracle.q4_decode(golden["q4"], k, n)
+    assert np.array_equal(dec.view(np.uint32), golden["decoded"].view(np.uint32))
+
+
+@pytest.mark.parametrize("pattern", range(5))
+def test_fixture_inputs_match_reference(oracle, golden, pattern):
+    k, batch = int(golden["k"]), int(golden["batch"])
+    x = oracle.fixture_input(k, batch, pattern)
+    assert np.array_equal(x.view(np.uint32), golden[f"x{pattern}"].view(np.uint32))
+
+
+@pytest.mark.parametrize("pattern", range(5))
+def test_gold_matches_reference_fp64(oracle, golden, pattern):
+    # The reference sums with an OpenMP simd reduction (another order), so the
+    # FP64 results agree to rounding of the sum, far below any test tolerance.
+    w, x = golden["decoded"], golden[f"x{pattern}"]
+    y = oracle.gold(w, x)
+    bound = 1e-13 * (np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T) + 1e-300
+    assert np.all(np.abs(y - golden[f"y{pattern}"]) <= bound)
+
+
+@pytest.mark.parametrize("pattern", range(5))
+def test_i8_activation_matches_reference(oracle, golden, pattern):
+    x = golden[f"x{pattern}"]
+    q0, q1, m0, m1 = oracle.i8_activation(x)
+    act, scales = golden[f"act{pattern}"], golden[f"act_scales{pattern}"]
+    assert np.array_equal(q0, act[0]) and np.array_equal(q1, act[1])
+    assert np.float32(m0 / np.float32(127)) == scales[0]
+    assert np.float32(m1 / np.float32(127)) == scales[1]
+
+
+def test_i8_rows_match_reference_one_component(oracle, golden):
+    codes, scales = oracle.i8_rows(golden["decoded"])
+    assert np.array_equal(codes, golden["row_codes"])
+    assert np.array_equal(scales, golden["row_scales8"])
+    assert np.array_equal(scales, golden["row_scales"])
+
+
+def test_reference_build_agrees_live(oracle, kref):
+    # Wider shapes than the committed fixture, straight from oracle/_ref.
+    for k, n in ((512, 37), (1024, 64), (96, 5)):
+        q4, dec, _ = kref.weights(k, n)
+        assert np.array_equal(oracle.fixture_q4(k, n), q4)
+        assert np.array_equal(oracle.q4_decode(q4, k, n).view(np.uint32), dec.view(np.uint32))
+        for pattern in range(5):
+            x = kref.input(k, 3, pattern)
+            assert np.array_equal(oracle.fixture_input(k, 3, pattern).view(np.uint32), x.view(np.uint32))
+            act, sc = kref.activation(x)
+            q0, q1, m0, m1 = oracle.i8_activation(x)
+            assert np.array_equal(q0, act[0]) and np.array_equal(q1, act[1])
+
+
+# --- F16 conversions against numpy ---------------------------------------
+
+def test_half_to_float_all_bit_patterns(oracle):
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ours = oracle.f16_decode(bits)
+    ref = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(ours), nan)
+    assert np.array_equal(ours[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_float_to_half_round_trip_and_rne(oracle):
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    values = bits.view(np.float16).astype(np.float32)
+    finite = np.isfinite(values)
+    assert np.array_equal(oracle.f16_encode(values[finite]), bits[finite])
+    # midpoints between neighbouring finite halves exercise ties-to-even
+    pos = np.sort(values[finite & (values >= 0)])
+    mids = ((pos[:-1].astype(np.float64) + pos[1:].astype(np.float64)) / 2).astype(np.float32)
+    for sample in (mids, -mids):
+        assert np.array_equal(oracle.f16_encode(sample), sample.astype(np.float16).view(np.uint16))
+    rng = np.random.default_rng(7)
+    raw = rng.integers(0, 2**32, size=1 << 20, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    raw = raw[np.isfinite(raw)]
+    with np.errstate(over="ignore"):
+        assert np.array_equal(oracle.f16_encode(raw), raw.astype(np.float16).view(np.uint16))
+
+
+# --- rounding rule against brute force -----------------------------------
+
+def _nearest_away(v: float, limit: int) -> int:
+    best = None
+    for q in range(-limit, limit + 1):
+        d = abs(np.float64(v) - q)
+        if best is None or d < best[0] - 1e-12 or (abs(d - best[0]) <= 1e-12 and abs(q) > abs(best[1])):
+            best = (d, q)
+    return best[1]
+
+
+def test_round_clamp_brute_force(oracle):
+    values = [0.0, -0.0, 0.49, 0.5, -0.5, 1.5, -1.5, 2.5, -2.5, 126.5, -126.5, 126.49, 127.0, -127.0,
+              127.4, 300.0, -300.0, 1e-30, -1e-30, 63.5, -63.5]
+    for v in values:
+        assert oracle.round_clamp(np.float32(v), 127) == _nearest_away(np.float32(v), 127), v
+
+
+# --- closed forms of the reference's deterministic benches ----------------
+
+@pytest.mark.parametrize("k,n", [(256, 65), (4096, 3), (96, 17)])
+def test_bench_weights_q4_and_f16_encode_the_same_values(oracle, k, n):
+    w, wh, q4 = oracle.bench_weights(k, n)
+    r = np.arange(n)[:, None]
+    j = np.arange(k)[None, :]
+    assert np.array_equal(w, (((r + j) % 16 - 8) * 0.0625).astype(np.float32))
+    assert np.array_equal(oracle.q4_decode(q4, k, n), w)
+    assert np.array_equal(oracle.f16_decode(wh), w)
+
+
+def test_fused_bench_rows_repeat_every_16(oracle):
+    k, n = 256, 48
+    w, q4 = oracle.fused_bench_weights(k, n)
+    assert np.array_equal(oracle.q4_decode(q4, k, n), w)
+    x = oracle.bench_input(k, 2)
+    y = oracle.gold(w, x)
+    for r in range(n):
+        assert np.array_equal(y[:, r], y[:, r % 16])
+
+
+def test_bench_input_is_sine(oracle):
+    x = oracle.bench_input(64, 3).ravel()
+    expect = np.sin(np.arange(x.size, dtype=np.float32) * np.float32(0.017)).astype(np.float32)
+    assert np.max(np.abs(x - expect)) <= 2e-7
+
+
+# --- FP64 gold, F32 order, integer dots, combine ----------------------------
+
+def test_gold_against_numpy_float64(oracle):
+    rng = np.random.default_rng(1)
+    w = rng.standard_normal((37, 96)).astype(np.float32)
+    x = rng.standard_normal((3, 96)).astype(np.float32)
+    ref = x.astype(np.float64) @ w.astype(np.float64).T
+    assert np.allclose(oracle.gold(w, x), ref, rtol=1e-13, atol=1e-13)
+
+
+def test_matvec_f32_order_within_f32_error(oracle):
+    rng = np.random.default_rng(2)
+    k, n = 512, 40
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    x = rng.standard_normal((2, k)).astype(np.float32)
+    gold = oracle.gold(w, x)
+    for type_, wb in ((0, w), (1, w.astype(np.float16)), (2, oracle.q4_quantize(w))):
+        dec = w if type_ == 0 else (wb.astype(np.float32) if type_ == 1 else oracle.q4_decode(wb, k, n))
+        ref = oracle.gold(dec, x)
+        got = oracle.matvec_f32(np.asarray(wb), type_, x, k, n)
+        bound = 2 * k * 2.0**-24 * (np.abs(x.astype(np.float64)) @ np.abs(dec.astype(np.float64)).T)
+        assert np.all(np.abs(got - ref) <= bound + 1e-30)
+    assert gold.shape == (2, n)
+
+
+def test_i8_dots_against_numpy(oracle):
+    rng = np.random.default_rng(3)
+    a = rng.integers(-127, 128, size=(5, 160)).astype(np.int8)
+    w = rng.integers(-127, 128, size=(9, 160)).astype(np.int8)
+    assert np.array_equal(oracle.i8_dots(a, w), a.astype(np.int64) @ w.astype(np.int64).T)
+    big = np.full((1, 16384), 127, np.int8)
+    assert oracle.i8_dots(big, -big)[0, 0] == -16384 * 127 * 127
+
+
+def test_i8_combine_known_answers(oracle):
+    # s0 = 127/127 = 1, s1 = 254/127 = 2: (10*1 + 4*2) * 0.25 = 4.5; swapping the
+    # components or scales would give 6.0.
+    y = oracle.i8_combine(np.array([[10]]), np.array([[4]]), np.array([0.25], np.float32), 127.0, 254.0)
+    assert y[0, 0] == np.float32(4.5)
+    y = oracle.i8_combine(np.array([[10, -3]]), np.array([[4, 5]]), np.array([0.25, 2.0], np.float32),
+                          63.5, 127.0)
+    assert y[0, 0] == np.float32(2.25) and y[0, 1] == np.float32(7.0)
+
+
+def test_i8_activation_rejects_nonfinite(oracle):
+    x = np.ones((1, 64), np.float32)
+    x[0, 5] = np.inf
+    assert oracle.i8_activation(x) is None
+    x[0, 5] = np.nan
+    assert oracle.i8_activation(x) is None
+
+
+def test_i8_activation_zero_tensor(oracle):
+    q0, q1, m0, m1 = oracle.i8_activation(np.zeros((2, 64), np.float32))
+    assert m0 == 1.0 and m1 == 1.0 and not q0.any() and not q1.any()
+
+
+# --- Q4_0 quantizer: properties only (ggml absent: parity unpinned) --------
+
+def test_q4_quantize_properties(oracle):
+    rng = np.random.default_rng(4)
+    k, n = 256, 64
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    w[3, 32:64] = 0.0
+    q4 = oracle.q4_quantize(w)
+    blocks = q4.reshape(n, k // 32, 18)
+    d = blocks[..., :2].copy().view(np.float16).astype(np.float32)[..., 0]
+    dec = oracle.q4_decode(q4, k, n).reshape(n, k // 32, 32)
+    wb = w.reshape(n, k // 32, 32)
+    nib = np.concatenate([blocks[..., 2:] & 15, blocks[..., 2:] >> 4], axis=2)
+    # the signed extreme maps to nibble 0 and decodes to -8*d (d = max/-8)
+    idx = np.argmax(np.abs(wb), axis=2)
+    nonzero = d != 0
+    assert np.all(np.take_along_axis(nib, idx[..., None], 2)[..., 0][nonzero] == 0)
+    assert np.all(np.sign(d) == -np.sign(np.take_along_axis(wb, idx[..., None], 2)[..., 0]))
+    # every element within half a step of its value (plus F16 scale rounding)
+    err = np.abs(dec - wb)
+    tol = np.abs(d)[..., None] * (0.5 + 8 * 2.0**-11) + 1e-12
+    clamp = nib == 15
+    assert np.all(err[~clamp] <= tol[..., 0:1].repeat(32, 2)[~clamp])
+    # the all-zero block: zero scale, every nibble 8
+    assert d[3, 1] == 0 and np.all(nib[3, 1] == 8)
