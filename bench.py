@@ -112,6 +112,41 @@ def cpu_baseline(seconds: float) -> dict | None:
                       f"{per_call * 1e3:.3f} ms/call, host cpus={os.cpu_count()}"}
 
 
+GEMM_SHAPES = [("k4096_n4096", 4096, 4096), ("k4096_n11008", 4096, 11008)]
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def gemm_leg(kernel, events, stream, device: int, reps: int) -> dict:
+    """Q4_0 prefill GEMM at batch 512: TFLOP/s = 2*b*k*n / time."""
+    batch = 512
+    out = {}
+    rng = np.random.Generator(np.random.PCG64(11))
+    for tag, k, n in GEMM_SHAPES:
+        wbuf = kl.Buffer(device, n * (k // 32) * 18)
+        upload_q4_matrix(wbuf, k, n, seed=2000 + n)
+        xbuf = kl.Buffer(device, 4 * batch * k)
+        xbuf.upload(rng.standard_normal((batch, k), dtype=np.float32))
+        ybuf = kl.Buffer(device, 4 * batch * n)
+        with kl.runtime_mutex():
+            for _ in range(3):
+                kl.matmul(kernel, device, ybuf.data, wbuf.data, xbuf.data, k, n, batch, kl.WeightType.q4_0)
+            kl.select(device)
+            kl.check(kl.wait())
+            start, stop = events.create(), events.create()
+            events.record(start, stream)
+            for _ in range(reps):
+                kl.matmul(kernel, device, ybuf.data, wbuf.data, xbuf.data, k, n, batch, kl.WeightType.q4_0)
+            events.record(stop, stream)
+            ms = events.elapsed_ms(start, stop) / reps
+            kl.check(kl.wait())
+        tflops = 2.0 * batch * k * n / (ms * 1e-3) / 1e12
+        out[tag] = {"us": round(ms * 1e3, 2), "tflops": round(tflops, 1),
+                    "mfma_f16_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "route": kernel.route}
+        for b in (wbuf, xbuf, ybuf):
+            b.close()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -120,7 +155,8 @@ def main() -> int:
     ap.add_argument("--kernel-reps", type=int, default=300, help="launches of the dominant GEMV for roofline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=[name for name, _, _ in LAYER],
+    ap.add_argument("--gemm-reps", type=int, default=50, help="timed batch-512 GEMM calls per shape (0: skip)")
+    ap.add_argument("--only", choices=[name for name, _, _ in LAYER] + ["gemm"],
                     help="profiling aid: time only this GEMV's launch loop (no layer set, no CPU leg)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -133,6 +169,10 @@ def main() -> int:
     events = HipEvents()
     stream = kl.stream(device)
     kernel = kl.Kernel()
+
+    if args.only == "gemm":
+        print(json.dumps({"gemm_b512": gemm_leg(kernel, events, stream, device, args.gemm_reps)}), flush=True)
+        return 0
 
     log("generating and uploading weights")
     # copies[name][c]: distinct device copies of each matrix, at least
@@ -218,6 +258,7 @@ def main() -> int:
     dom = per_shape[f"{dname}_k{dk}_n{dn}"]
     achieved = dom["gbps"]
 
+    gemm = gemm_leg(kernel, events, stream, device, args.gemm_reps) if args.gemm_reps > 0 else None
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     result = {
         "metric": METRIC,
@@ -255,6 +296,7 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
         "per_shape": per_shape,
+        "gemm_b512": gemm,
     }
     print(json.dumps(result), flush=True)
     for bufs in copies.values():

@@ -15,6 +15,13 @@ extern "C" {
 int kk_dense_matmul(int type, const void *w, const float *x, float *y, int k, int n, int batch,
                     hipStream_t stream, const char **route);
 
+// Prefill GEMM on fp16 MFMA for Q4_0 (type 2) and F16 (type 1) weights. The
+// workspace (kk_gemm_workspace_bytes) holds the fp16 activations and their
+// row scales.
+size_t kk_gemm_workspace_bytes(int k, int n, int batch);
+int kk_gemm(int type, const void *w, const float *x, float *y, int k, int n, int batch, void *workspace,
+            hipStream_t stream, const char **route);
+
 // Bytes of device workspace kk_i8_quantize needs for `count` activations.
 size_t kk_i8_workspace_bytes(int k, int batch);
 // Two-pass per-tensor INT8 quantization of X[batch,k] into `workspace`

@@ -6,12 +6,42 @@
 
 #include <climits>
 #include <cstdint>
+#include <cstdlib>
 
 namespace kunlun {
 namespace detail {
 thread_local const char * last_route = nullptr;
 const char * route_of_last_matmul() { return last_route; }
 } // namespace detail
+
+namespace {
+
+// Grows a Kernel-owned device workspace; waits for work that may still use
+// the old one before releasing it.
+void * grow(int id, detail::DeviceContext & ctx, void *& ptr, size_t & size, size_t need) {
+    if (size < need) {
+        if (ptr) {
+            detail::check_hip(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize");
+            release(id, ptr, size);
+            ptr = nullptr;
+            size = 0;
+        }
+        ptr = allocate(id, need);
+        require(ptr != nullptr);
+        size = need;
+    }
+    return ptr;
+}
+
+// Smallest batch that uses the fp16-MFMA prefill GEMM (F16 and Q4_0 weights);
+// smaller batches keep the F32-accumulate GEMV kernels.
+int gemm_min_batch() {
+    const char * value = std::getenv("KUNLUN_GEMM_MIN_BATCH");
+    const int v = value && *value ? std::atoi(value) : 64;
+    return v > 0 ? v : 64;
+}
+
+} // namespace
 
 Kernel::Kernel() : impl_(new Impl{}) {}
 
@@ -21,6 +51,7 @@ Kernel::~Kernel() {
         select(impl_->id);
         check(wait());
         release(impl_->id, impl_->i8_workspace, impl_->i8_workspace_size);
+        release(impl_->id, impl_->gemm_workspace, impl_->gemm_workspace_size);
     }
     delete impl_;
 }
@@ -48,18 +79,7 @@ void matmul(Kernel & kernel, int id, void * y, const void * w, const void * x, i
     impl.id = id;
     if (type == WeightType::rowwise_i8) {
         require(((uintptr_t)w & 3) == 0 && ((uintptr_t)scales & 3) == 0 && ((uintptr_t)maximum & 3) == 0);
-        const size_t need = kk_i8_workspace_bytes(k, batch);
-        if (impl.i8_workspace_size < need) {
-            if (impl.i8_workspace) {
-                detail::check_hip(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize");
-                release(id, impl.i8_workspace, impl.i8_workspace_size);
-                impl.i8_workspace = nullptr;
-                impl.i8_workspace_size = 0;
-            }
-            impl.i8_workspace = allocate(id, need);
-            require(impl.i8_workspace != nullptr);
-            impl.i8_workspace_size = need;
-        }
+        grow(id, ctx, impl.i8_workspace, impl.i8_workspace_size, kk_i8_workspace_bytes(k, batch));
         detail::check_hip((hipError_t)kk_i8_quantize(static_cast<const float *>(x), k, batch, impl.i8_workspace,
                                                      ctx.status, ctx.stream),
                           "kk_i8_quantize");
@@ -68,6 +88,12 @@ void matmul(Kernel & kernel, int id, void * y, const void * w, const void * x, i
                                                    maximum, static_cast<float *>(y), k, n, batch, ctx.stream,
                                                    &impl.route),
                           "kk_i8_matmul");
+    } else if ((type == WeightType::q4_0 || (type == WeightType::f16 && ((uintptr_t)w & 15) == 0)) &&
+               batch >= gemm_min_batch() && ((uintptr_t)x & 15) == 0) {
+        grow(id, ctx, impl.gemm_workspace, impl.gemm_workspace_size, kk_gemm_workspace_bytes(k, n, batch));
+        detail::check_hip((hipError_t)kk_gemm((int)type, w, static_cast<const float *>(x), static_cast<float *>(y), k,
+                                              n, batch, impl.gemm_workspace, ctx.stream, &impl.route),
+                          "kk_gemm");
     } else {
         detail::check_hip((hipError_t)kk_dense_matmul((int)type, w, static_cast<const float *>(x),
                                                       static_cast<float *>(y), k, n, batch, ctx.stream,

@@ -36,8 +36,10 @@ const char * route_of_last_matmul();
 
 struct Kernel::Impl {
     int id = -1;
-    void * i8_workspace = nullptr;
+    void * i8_workspace = nullptr;      // rowwise_i8 activation codes and maxima
     size_t i8_workspace_size = 0;
+    void * gemm_workspace = nullptr;    // fp16 activations of the prefill GEMM
+    size_t gemm_workspace_size = 0;
     const char * route = nullptr;
 };
 
