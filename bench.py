@@ -112,6 +112,41 @@ def cpu_baseline(seconds: float) -> dict | None:
                       f"{per_call * 1e3:.3f} ms/call, host cpus={os.cpu_count()}"}
 
 
+COPY_BYTES = 512 << 20
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "q4_gemv_dot8_k4096_n11008_traffic.md")
+
+
+def copy_leg(events, stream, device: int, reps: int = 10) -> dict:
+    """A plain device-to-device copy of COPY_BYTES: its FETCH_SIZE and WRITE_SIZE per dispatch
+    calibrate the counters (the copy reads and writes exactly COPY_BYTES)."""
+    src, dst = kl.Buffer(device, COPY_BYTES), kl.Buffer(device, COPY_BYTES)
+    with kl.runtime_mutex():
+        kl.select(device)
+        start, stop = events.create(), events.create()
+        events.record(start, stream)
+        for _ in range(reps):
+            kl.check(kl.copy(dst.data, src.data, COPY_BYTES, kl.CopyKind.device_to_device))
+        events.record(stop, stream)
+        ms = events.elapsed_ms(start, stop) / reps
+        kl.check(kl.wait())
+    src.close()
+    dst.close()
+    return {"bytes": COPY_BYTES, "reps": reps, "us": round(ms * 1e3, 2)}
+
+
+def measured_traffic() -> int | None:
+    """HBM bytes per launch of the dominant GEMV from the committed counter summary
+    (line 'traffic_bytes_per_launch: N'), or None when it is absent."""
+    try:
+        with open(TRAFFIC_PROFILE, encoding="utf-8") as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except (OSError, ValueError):
+        return None
+    return None
+
+
 GEMM_SHAPES = [("k4096_n4096", 4096, 4096), ("k4096_n11008", 4096, 11008)]
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
@@ -156,8 +191,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gemm-reps", type=int, default=50, help="timed batch-512 GEMM calls per shape (0: skip)")
-    ap.add_argument("--only", choices=[name for name, _, _ in LAYER] + ["gemm"],
-                    help="profiling aid: time only this GEMV's launch loop (no layer set, no CPU leg)")
+    ap.add_argument("--only", choices=[name for name, _, _ in LAYER] + ["gemm", "copy"],
+                    help="profiling aid: time only this GEMV's launch loop, the GEMM leg, or (copy) a "
+                         f"{COPY_BYTES >> 20} MiB device-to-device copy that calibrates the traffic counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (this build has no "
@@ -172,6 +208,9 @@ def main() -> int:
 
     if args.only == "gemm":
         print(json.dumps({"gemm_b512": gemm_leg(kernel, events, stream, device, args.gemm_reps)}), flush=True)
+        return 0
+    if args.only == "copy":
+        print(json.dumps({"copy": copy_leg(events, stream, device)}), flush=True)
         return 0
 
     log("generating and uploading weights")
@@ -253,7 +292,7 @@ def main() -> int:
         ms = timed(one, args.kernel_reps, 5) / args.kernel_reps
         gbps = q4_bytes(k, n) / (ms * 1e-3) / 1e9
         per_shape[f"{name}_k{k}_n{n}"] = {"us": round(ms * 1e3, 3), "gbps": round(gbps, 1),
-                                           "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)}
+                                           "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "route": kernel.route}
     dname, dk, dn = DOMINANT
     dom = per_shape[f"{dname}_k{dk}_n{dn}"]
     achieved = dom["gbps"]
@@ -280,17 +319,18 @@ def main() -> int:
             "bytes_per_step": step_bytes,
             "rotating_copies_per_shape": {name: len(bufs) for name, bufs in copies.items()},
             "weight_set_mb": round(sum(n * (k // 32) * 18 for _, k, n in LAYER) / 1e6, 1),
-            "route": kernel.route,
+            "route": dom["route"],
             "wall_ms_timed_region": round(wall_ms, 3),
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"q4 GEMV K{dk}xN{dn} b1 ({kernel.route})",
+            "kernel": f"q4 GEMV K{dk}xN{dn} b1 ({dom['route']})",
             "achieved": achieved,
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
+            "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT) if measured_traffic() else None,
             "bytes_per_launch": q4_bytes(dk, dn),
             "avg_launch_us": dom["us"],
         },
