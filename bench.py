@@ -148,11 +148,13 @@ def measured_traffic() -> int | None:
 
 
 GEMM_SHAPES = [("k4096_n4096", 4096, 4096), ("k4096_n11008", 4096, 11008)]
+PAIR_N = 11008
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
 
 def gemm_leg(kernel, events, stream, device: int, reps: int) -> dict:
-    """Q4_0 prefill GEMM at batch 512: TFLOP/s = 2*b*k*n / time."""
+    """Q4_0 prefill GEMM at batch 512: TFLOP/s = 2*b*k*n / time; the
+    gate/up pair with SiLU * up counts 2 * 2*b*k*n per call."""
     batch = 512
     out = {}
     rng = np.random.Generator(np.random.PCG64(11))
@@ -177,6 +179,29 @@ def gemm_leg(kernel, events, stream, device: int, reps: int) -> dict:
         tflops = 2.0 * batch * k * n / (ms * 1e-3) / 1e12
         out[tag] = {"us": round(ms * 1e3, 2), "tflops": round(tflops, 1),
                     "mfma_f16_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "route": kernel.route}
+        if n == PAIR_N:
+            # gate/up pair sharing X, then SiLU(gate) * up, one call
+            ubuf = kl.Buffer(device, n * (k // 32) * 18)
+            upload_q4_matrix(ubuf, k, n, seed=3000 + n)
+            with kl.runtime_mutex():
+                for _ in range(3):
+                    kl.matmul_swiglu(kernel, device, ybuf.data, wbuf.data, ubuf.data, xbuf.data, k, n, batch,
+                                     kl.WeightType.q4_0)
+                kl.select(device)
+                kl.check(kl.wait())
+                start, stop = events.create(), events.create()
+                events.record(start, stream)
+                for _ in range(reps):
+                    kl.matmul_swiglu(kernel, device, ybuf.data, wbuf.data, ubuf.data, xbuf.data, k, n, batch,
+                                     kl.WeightType.q4_0)
+                events.record(stop, stream)
+                ms = events.elapsed_ms(start, stop) / reps
+                kl.check(kl.wait())
+            tflops = 4.0 * batch * k * n / (ms * 1e-3) / 1e12
+            out[f"pair_swiglu_{tag}"] = {"us": round(ms * 1e3, 2), "tflops": round(tflops, 1),
+                                         "mfma_f16_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                                         "route": kernel.route}
+            ubuf.close()
         for b in (wbuf, xbuf, ybuf):
             b.close()
     return out

@@ -2,10 +2,11 @@
 //
 // This header keeps the declarations, argument meaning, defaults and class
 // layouts of the matmul subset of the reference library's public header
-// (reference include/kunlun/k200.h:10-37, 40, 62-105, 345-350) so a consumer
-// of that subset rebuilds against this library unchanged. Declarations of the
-// reference that are not on the matmul path (attention, SwiGLU, Q6_K, native
-// and common Q4 layouts, elementwise, KV caches) are not declared here.
+// (reference include/kunlun/k200.h:10-37, 40, 62-105, 132, 185-199, 345-350)
+// so a consumer of that subset rebuilds against this library unchanged.
+// Declarations of the reference that are not on the matmul path (attention,
+// Q6_K, native and common Q4 layouts, elementwise, KV caches) are not
+// declared here. matmul_swiglu has no reference counterpart (see below).
 //
 // Device numbering: the reference drives the two processing dies of one
 // Kunlun card as devices 0 and 1. Here a device is one HIP device (one GPU);
@@ -62,6 +63,8 @@ private:
 // accepted by matmul, as in the reference.
 enum class WeightType { f32 = 0, f16 = 1, q4_0 = 2, rowwise_i8 = 3, q6_k = 4 };
 
+struct SwiGLULayout;
+
 // Per-call state owner: binds to the first device it is used on and owns
 // lazily grown device workspaces (reference k200.h:62-88).
 class Kernel {
@@ -75,6 +78,10 @@ private:
     Impl * impl_;
     friend void matmul(Kernel &, int, void *, const void *, const void *, int, int, int,
                        WeightType, const float *, const float *, int);
+    friend bool swiglu(Kernel &, int, void *, size_t, const void *, size_t, const void *, size_t,
+                       const SwiGLULayout &);
+    friend void matmul_swiglu(Kernel &, int, void *, const void *, const void *, const void *, int, int, int,
+                              WeightType);
 };
 
 // Packed rowwise INT8 weight layout (reference k200.h:90-96):
@@ -96,6 +103,38 @@ void upload_i8_rows(int device, void * weights, int k, int rows,
 void matmul(Kernel &, int device, void * y, const void * w, const void * x,
             int k, int n, int batch, WeightType type,
             const float * scales = nullptr, const float * maxima = nullptr, int tile = 16);
+
+// Element type of SwiGLU inputs and outputs (reference k200.h:132).
+enum class InputType { f32, f16 };
+
+// SiLU(gate) * up over `rows` rows of `width` contiguous values
+// (reference k200.h:185-199). Strides are bytes between rows.
+struct SwiGLULayout {
+    int width, rows;
+    int gate_stride, up_stride, output_stride;
+    InputType type;
+};
+// Empty string: the layout is supported; otherwise "type", "shape", "stride"
+// or "byte extent" names the first rule it breaks.
+const char * swiglu_reason(const SwiGLULayout &);
+// Computes SiLU(gate)*up with F32 intermediates and one final output
+// rounding, and completes before returning. y may alias gate or up element
+// for element (equal row strides), or hold rows disjoint from them; any other
+// overlap, a span beyond the given byte sizes, misalignment, a bad device or
+// a Kernel bound to another device returns false with no work submitted.
+bool swiglu(Kernel &, int device, void * y, size_t y_bytes,
+            const void * gate, size_t gate_bytes, const void * up, size_t up_bytes,
+            const SwiGLULayout &);
+
+// No counterpart in the reference, which computes this as two matmul calls
+// followed by swiglu (or common_q4_matmul_pair then swiglu, reference
+// src/q4-pair.inc:9-80): Y[batch,n] = SiLU(X W_gate^T) * (X W_up^T), F32 Y.
+// w_gate and w_up are [n,k] weights of one type (f32, f16 or q4_0) and the
+// arguments follow matmul's rules. At batch >= 64 (Q4_0, F16) both products
+// run in one fp16-MFMA GEMM with the SiLU * up epilogue; smaller batches run
+// two GEMVs and the SwiGLU kernel. Submits; select + wait completes it.
+void matmul_swiglu(Kernel &, int device, void * y, const void * w_gate, const void * w_up, const void * x,
+                   int k, int n, int batch, WeightType type);
 
 // Same layout as the reference (reference k200.h:345-350): matmul submissions
 // on devices 0 and 1, peer copy count and bytes.

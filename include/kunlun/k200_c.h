@@ -74,6 +74,20 @@ void kunlun_matmul(kunlun_kernel *kernel, int device, void *y, const void *w, co
                    int k, int n, int batch, int type,
                    const float *scales, const float *maxima, int tile);
 
+/* Element types of SwiGLU, same values as kunlun::InputType (reference include/kunlun/k200.h:132). */
+enum { KUNLUN_INPUT_F32 = 0, KUNLUN_INPUT_F16 = 1 };
+/* swiglu_reason() (reference include/kunlun/k200.h:192) on the SwiGLULayout
+ * {width, rows, gate_stride, up_stride, output_stride, type}: "" when
+ * supported, else the first rule broken ("type", "shape", "stride",
+ * "byte extent"). */
+const char *kunlun_swiglu_reason(int width, int rows, int gate_stride, int up_stride, int output_stride, int type);
+/* swiglu() (reference include/kunlun/k200.h:197-199): y = SiLU(gate) * up
+ * with F32 intermediates, completed before returning. Returns 1, or 0 when
+ * the layout or pointer contract is not met (nothing submitted). */
+int kunlun_swiglu(kunlun_kernel *kernel, int device, void *y, size_t y_bytes, const void *gate,
+                  size_t gate_bytes, const void *up, size_t up_bytes, int width, int rows,
+                  int gate_stride, int up_stride, int output_stride, int type);
+
 /* statistics() (reference include/kunlun/k200.h:345-349) as four counters:
  * out[0..1] = matmul submissions on devices 0 and 1, out[2] = peer copies,
  * out[3] = peer bytes. */
@@ -91,6 +105,13 @@ void *kunlun_stream(int device);
 /* Name of the kernel route the last matmul on `kernel` took (for tests and
  * profiling, e.g. "q4_gemv_pair"); NULL before the first call. */
 const char *kunlun_kernel_route(const kunlun_kernel *kernel);
+/* matmul_swiglu(): Y[batch,n] = SiLU(X W_gate^T) * (X W_up^T) for two [n,k]
+ * weights of one type (KUNLUN_F32, KUNLUN_F16, KUNLUN_Q4_0), with matmul()'s
+ * argument rules. The reference computes this with two matmul calls and
+ * swiglu; here batch >= 64 fuses both products and the SwiGLU into one GEMM.
+ * Submits; kunlun_select(device) + kunlun_wait() completes it. */
+void kunlun_matmul_swiglu(kunlun_kernel *kernel, int device, void *y, const void *w_gate, const void *w_up,
+                          const void *x, int k, int n, int batch, int type);
 
 #ifdef __cplusplus
 }

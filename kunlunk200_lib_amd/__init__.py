@@ -13,6 +13,7 @@ loudly when it is missing: there is no CPU fallback.
 from __future__ import annotations
 
 import ctypes
+import dataclasses
 import enum
 import os
 import threading
@@ -61,6 +62,11 @@ C_FUNCTIONS = [
     ("kunlun_matmul_count", _c_size, [_c_int]),
     ("kunlun_stream", _c_void_p, [_c_int]),
     ("kunlun_kernel_route", ctypes.c_char_p, [_c_void_p]),
+    ("kunlun_swiglu_reason", ctypes.c_char_p, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
+    ("kunlun_swiglu", _c_int, [_c_void_p, _c_int, _c_void_p, _c_size, _c_void_p, _c_size, _c_void_p, _c_size,
+                               _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
+    ("kunlun_matmul_swiglu", None, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int,
+                                    _c_int, _c_int]),
 ]
 
 
@@ -268,6 +274,48 @@ def matmul(kernel: Kernel, device: int, y, w, x, k: int, n: int, batch: int, typ
     """
     load().kunlun_matmul(kernel.handle, int(device), _ptr(y), _ptr(w), _ptr(x), int(k), int(n), int(batch),
                          int(type), _ptr(scales), _ptr(maxima), int(tile))
+
+
+class InputType(enum.IntEnum):
+    """Element type of SwiGLU inputs and outputs (reference k200.h:132)."""
+    f32 = 0
+    f16 = 1
+
+
+@dataclasses.dataclass
+class SwiGLULayout:
+    """reference k200.h:185-190; strides are bytes between rows."""
+    width: int
+    rows: int
+    gate_stride: int
+    up_stride: int
+    output_stride: int
+    type: InputType = InputType.f32
+
+    def _args(self):
+        return (int(self.width), int(self.rows), int(self.gate_stride), int(self.up_stride),
+                int(self.output_stride), int(self.type))
+
+
+def swiglu_reason(layout: SwiGLULayout) -> str:
+    """"" when supported, else the first rule broken (reference k200.h:192)."""
+    return load().kunlun_swiglu_reason(*layout._args()).decode()
+
+
+def swiglu(kernel: Kernel, device: int, y, y_bytes: int, gate, gate_bytes: int, up, up_bytes: int,
+           layout: SwiGLULayout) -> bool:
+    """y = SiLU(gate) * up, completed before returning; False when the layout or the
+    pointer contract is not met (reference k200.h:197-199)."""
+    return bool(load().kunlun_swiglu(kernel.handle, int(device), _ptr(y), int(y_bytes), _ptr(gate),
+                                     int(gate_bytes), _ptr(up), int(up_bytes), *layout._args()))
+
+
+def matmul_swiglu(kernel: Kernel, device: int, y, w_gate, w_up, x, k: int, n: int, batch: int,
+                  type: WeightType) -> None:
+    """Submit Y[batch,n] = SiLU(X W_gate^T) * (X W_up^T) (no reference counterpart:
+    the reference runs two matmul calls and swiglu)."""
+    load().kunlun_matmul_swiglu(kernel.handle, int(device), _ptr(y), _ptr(w_gate), _ptr(w_up), _ptr(x), int(k),
+                                int(n), int(batch), int(type))
 
 
 def statistics() -> dict:

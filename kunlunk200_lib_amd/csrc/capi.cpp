@@ -63,6 +63,32 @@ void kunlun_statistics(size_t out[4]) {
 }
 const char * kunlun_version(void) { return kunlun::version(); }
 
+const char * kunlun_swiglu_reason(int width, int rows, int gate_stride, int up_stride, int output_stride, int type) {
+    const kunlun::SwiGLULayout layout{width, rows, gate_stride, up_stride, output_stride,
+                                      static_cast<kunlun::InputType>(type)};
+    return kunlun::swiglu_reason(layout);
+}
+
+int kunlun_swiglu(kunlun_kernel * kernel, int device, void * y, size_t y_bytes, const void * gate, size_t gate_bytes,
+                  const void * up, size_t up_bytes, int width, int rows, int gate_stride, int up_stride,
+                  int output_stride, int type) {
+    if (!kernel) return 0;
+    const kunlun::SwiGLULayout layout{width, rows, gate_stride, up_stride, output_stride,
+                                      static_cast<kunlun::InputType>(type)};
+    const bool done = kunlun::swiglu(kernel->kernel, device, y, y_bytes, gate, gate_bytes, up, up_bytes, layout);
+    if (done) kernel->route = kunlun::detail::route_of_last_matmul();
+    return done ? 1 : 0;
+}
+
+void kunlun_matmul_swiglu(kunlun_kernel * kernel, int device, void * y, const void * w_gate, const void * w_up,
+                          const void * x, int k, int n, int batch, int type) {
+    kunlun::require(kernel != nullptr);
+    kunlun::require(type >= KUNLUN_F32 && type <= KUNLUN_Q6_K);
+    kunlun::matmul_swiglu(kernel->kernel, device, y, w_gate, w_up, x, k, n, batch,
+                          static_cast<kunlun::WeightType>(type));
+    kernel->route = kunlun::detail::route_of_last_matmul();
+}
+
 size_t kunlun_matmul_count(int device) { return kunlun::detail::matmul_count(device); }
 void * kunlun_stream(int device) { return static_cast<void *>(kunlun::detail::context(device).stream); }
 const char * kunlun_kernel_route(const kunlun_kernel * kernel) { return kernel ? kernel->route : nullptr; }

@@ -85,4 +85,27 @@ __device__ __forceinline__ u32x4_a4 load_u32x4(const uint32_t *p) {
     return *reinterpret_cast<const u32x4_a4 *>(p);
 }
 
+// SiLU(g) * u in F32 with the reference's non-finite rules (reference
+// kernels/kunlun-swiglu.xpu:27-39): finite inputs give (g / (1 + e^-g)) * u;
+// otherwise NaN when g or u is NaN or g is -Inf, +-Inf with the product sign
+// when exactly one side is infinite and the other side (SiLU(g) for a finite
+// g) is non-zero, NaN for Inf * 0.
+__device__ __forceinline__ float swiglu_value(float g, float u) {
+#pragma clang fp contract(off)
+    const uint32_t gb = __float_as_uint(g), ub = __float_as_uint(u);
+    const uint32_t ga = gb & 0x7fffffffu, ua = ub & 0x7fffffffu;
+    if (ga < 0x7f800000u && ua < 0x7f800000u) return (g / (1.0f + expf(-g))) * u;
+    const uint32_t sign = (gb ^ ub) & 0x80000000u;
+    uint32_t bits;
+    if (ga > 0x7f800000u || ua > 0x7f800000u || gb == 0xff800000u) {
+        bits = 0x7fc00000u;
+    } else if (ga == 0x7f800000u) {
+        bits = ua == 0 ? 0x7fc00000u : (sign | 0x7f800000u);
+    } else {
+        const float act = g / (1.0f + expf(-g));
+        bits = (__float_as_uint(act) & 0x7fffffffu) == 0 ? 0x7fc00000u : (sign | 0x7f800000u);
+    }
+    return __uint_as_float(bits);
+}
+
 } // namespace kk

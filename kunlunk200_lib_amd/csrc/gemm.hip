@@ -160,16 +160,24 @@ constexpr size_t gemm_lds_bytes() {
     return 2 * static_cast<size_t>(kLdsA + BN * kLdsStride) * sizeof(_Float16);
 }
 
-template <bool F16W, int BN>
+// PAIR (gate/up): the B tile holds 64 rows of each of two weight matrices w
+// and w2 (same shape); B row j is row (j >> 6) * 32 + (j & 31) of the output
+// tile from matrix (j >> 5) & 1, so each wave's first 32-column MFMA tile is
+// gate and its second is up for the same 32 output columns, and the epilogue
+// writes y = SiLU(gate) * up.
+template <bool F16W, int BN, bool PAIR>
 __global__ __launch_bounds__(kGemmThreads) void mfma_gemm(const uint8_t *__restrict__ w,
+                                                         const uint8_t *__restrict__ w2,
                                                          const _Float16 *__restrict__ x16,
                                                          const float *__restrict__ row_inv,
                                                          float *__restrict__ y, int m_rows, int n_rows,
                                                          int k, int k_pad, size_t w_bytes, int n_tiles,
                                                          int tiles, int tiles_per_xcd) {
     static_assert(BN == 64 || BN == 128, "tile N");
+    static_assert(!PAIR || BN == 128, "a pair tile holds 64 rows of each matrix");
     constexpr int kLdsB = BN * kLdsStride;
     constexpr int kNT = BN / 64;                         // 32-column MFMA tiles per wave
+    constexpr int kOutN = PAIR ? 64 : BN;                // output columns per tile
     extern __shared__ __align__(16) _Float16 lds[];      // 2 x (A tile + B tile)
 
     const int bid = blockIdx.x;
@@ -184,7 +192,7 @@ __global__ __launch_bounds__(kGemmThreads) void mfma_gemm(const uint8_t *__restr
     const int kh = wid >> 2;                             // k-group
     const int wm = wid & 1, wn = (wid >> 1) & 1;         // wave tile rows 64*wm, columns wn*BN/2
     const int m0 = mt * kBM;
-    const int n0 = nt * BN;
+    const int n0 = nt * kOutN;
     const int blocks = k >> 5;
     const size_t row_bytes = F16W ? static_cast<size_t>(k) * 2 : static_cast<size_t>(blocks) * 18;
     const int steps = k_pad / kBK;                       // multiple of kStages
@@ -203,14 +211,18 @@ __global__ __launch_bounds__(kGemmThreads) void mfma_gemm(const uint8_t *__restr
     //          BN = 64: half (tid & 1) of block ((tid >> 1) & 3) of row tid >> 3.
     // B, F16: 16-byte chunks tid + 512 i of the BN x 128 fp16 tile.
     constexpr int kQShift = BN == 128 ? 2 : 3;
+    // B tile row j -> weight matrix and output column of the tile
+    auto b_matrix = [](int j) { return PAIR ? (j >> 5) & 1 : 0; };
+    auto b_column = [](int j) { return PAIR ? ((j >> 6) << 5) | (j & 31) : j; };
     const int qb_row = tid >> kQShift;
     const int qb_blk = BN == 128 ? (tid & 3) : ((tid >> 1) & 3);
     const int qb_half = BN == 128 ? 0 : (tid & 1);
-    const int q_wrow = min(n0 + qb_row, n_rows - 1);
-    const bool q_live_row = n0 + qb_row < n_rows;
-    const size_t w_mis = reinterpret_cast<uintptr_t>(w) & 3;
+    const int q_wrow = min(n0 + b_column(qb_row), n_rows - 1);
+    const bool q_live_row = n0 + b_column(qb_row) < n_rows;
+    const uint8_t *q_w = b_matrix(qb_row) ? w2 : w;
+    const size_t w_mis = reinterpret_cast<uintptr_t>(q_w) & 3;
     const size_t w_last_dword = (w_mis + w_bytes - 1) >> 2;
-    const uint32_t *w_base32 = reinterpret_cast<const uint32_t *>(w - w_mis);
+    const uint32_t *w_base32 = reinterpret_cast<const uint32_t *>(q_w - w_mis);
 
     // Register sets: 4 A chunks plus the B words (6 raw Q4_0 dwords with their
     // byte shift and liveness, or BN/32 fp16 chunks).
@@ -230,9 +242,10 @@ __global__ __launch_bounds__(kGemmThreads) void mfma_gemm(const uint8_t *__restr
 #pragma unroll
             for (int i = 0; i < kF16Chunks; ++i) {
                 const int c = tid + kGemmThreads * i;
-                const int r = min(n0 + (c >> 4), n_rows - 1);
+                const int r = min(n0 + b_column(c >> 4), n_rows - 1);
                 const int kk0 = min(ks * kBK + (c & 15) * 8, k - 8);
-                const u32x4 v = *reinterpret_cast<const u32x4 *>(w + static_cast<size_t>(r) * row_bytes +
+                const uint8_t *src = b_matrix(c >> 4) ? w2 : w;
+                const u32x4 v = *reinterpret_cast<const u32x4 *>(src + static_cast<size_t>(r) * row_bytes +
                                                                  static_cast<size_t>(kk0) * 2);
 #pragma unroll
                 for (int t = 0; t < 4; ++t) b_reg[set][4 * i + t] = v[t];
@@ -264,7 +277,7 @@ __global__ __launch_bounds__(kGemmThreads) void mfma_gemm(const uint8_t *__restr
 #pragma unroll
             for (int i = 0; i < kF16Chunks; ++i) {
                 const int c = tid + kGemmThreads * i;
-                const bool in = n0 + (c >> 4) < n_rows && ks * kBK + (c & 15) * 8 < k;
+                const bool in = n0 + b_column(c >> 4) < n_rows && ks * kBK + (c & 15) * 8 < k;
                 u32x4 v;
 #pragma unroll
                 for (int t = 0; t < 4; ++t) v[t] = in ? b_reg[set][4 * i + t] : 0u;
@@ -355,6 +368,21 @@ __global__ __launch_bounds__(kGemmThreads) void mfma_gemm(const uint8_t *__restr
     __syncthreads();
     if (kh == 1) return;
     const float wscale = F16W ? 1.0f : 8.0f;
+    if constexpr (PAIR) {
+        const int n = n0 + wn * 32 + (lane & 31);
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm * 64 + it * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const float s = row_inv[m] * wscale;
+                const float g = (acc[it][0][r] + red[(((sw * 2 + it) * kNT + 0) * 16 + r) * kWave + lane]) * s;
+                const float u = (acc[it][1][r] + red[(((sw * 2 + it) * kNT + 1) * 16 + r) * kWave + lane]) * s;
+                if (m < m_rows && n < n_rows) y[static_cast<size_t>(m) * n_rows + n] = kk::swiglu_value(g, u);
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
 #pragma unroll
@@ -391,9 +419,9 @@ GemmPlan plan(int k, int n, int batch) {
     return p;
 }
 
-template <bool F16W, int BN>
-hipError_t launch_gemm(const void *w, const _Float16 *x16, const float *row_inv, float *y, int batch, int n, int k,
-                       const GemmPlan &p, size_t w_bytes, hipStream_t stream) {
+template <bool F16W, int BN, bool PAIR = false>
+hipError_t launch_gemm(const void *w, const void *w2, const _Float16 *x16, const float *row_inv, float *y, int batch,
+                       int n, int k, const GemmPlan &p, size_t w_bytes, hipStream_t stream) {
     // dynamic LDS above 64 KiB is opted into once per device (callers hold the runtime lock)
     constexpr int kMaxDevices = 64;
     static bool configured[kMaxDevices] = {};
@@ -402,16 +430,16 @@ hipError_t launch_gemm(const void *w, const _Float16 *x16, const float *row_inv,
     if (rc != hipSuccess) return rc;
     if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
     if (!configured[device]) {
-        rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&mfma_gemm<F16W, BN>),
+        rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&mfma_gemm<F16W, BN, PAIR>),
                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(gemm_lds_bytes<BN>()));
         if (rc != hipSuccess) return rc;
         configured[device] = true;
     }
     const int tiles = p.m_tiles * p.n_tiles;
     const int tiles_per_xcd = (tiles + kXcds - 1) / kXcds;
-    hipLaunchKernelGGL((mfma_gemm<F16W, BN>), dim3(tiles_per_xcd * kXcds), dim3(kGemmThreads), gemm_lds_bytes<BN>(),
-                       stream, static_cast<const uint8_t *>(w), x16, row_inv, y, batch, n, k, p.k_pad, w_bytes,
-                       p.n_tiles, tiles, tiles_per_xcd);
+    hipLaunchKernelGGL((mfma_gemm<F16W, BN, PAIR>), dim3(tiles_per_xcd * kXcds), dim3(kGemmThreads),
+                       gemm_lds_bytes<BN>(), stream, static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(w2),
+                       x16, row_inv, y, batch, n, k, p.k_pad, w_bytes, p.n_tiles, tiles, tiles_per_xcd);
     return hipGetLastError();
 }
 
@@ -444,8 +472,36 @@ extern "C" int kk_gemm(int type, const void *w, const float *x, float *y, int k,
     const size_t w_bytes = type == 1 ? static_cast<size_t>(n) * k * 2 : static_cast<size_t>(n) * (k / 32) * 18;
     if (route) *route = type == 2 ? "q4_gemm_mfma" : "f16_gemm_mfma";
     if (type == 2)
-        return p.bn == 128 ? launch_gemm<false, 128>(w, x16, row_inv, y, batch, n, k, p, w_bytes, stream)
-                           : launch_gemm<false, 64>(w, x16, row_inv, y, batch, n, k, p, w_bytes, stream);
-    return p.bn == 128 ? launch_gemm<true, 128>(w, x16, row_inv, y, batch, n, k, p, w_bytes, stream)
-                       : launch_gemm<true, 64>(w, x16, row_inv, y, batch, n, k, p, w_bytes, stream);
+        return p.bn == 128 ? launch_gemm<false, 128>(w, w, x16, row_inv, y, batch, n, k, p, w_bytes, stream)
+                           : launch_gemm<false, 64>(w, w, x16, row_inv, y, batch, n, k, p, w_bytes, stream);
+    return p.bn == 128 ? launch_gemm<true, 128>(w, w, x16, row_inv, y, batch, n, k, p, w_bytes, stream)
+                       : launch_gemm<true, 64>(w, w, x16, row_inv, y, batch, n, k, p, w_bytes, stream);
+}
+
+extern "C" int kk_gemm_swiglu(int type, const void *w_gate, const void *w_up, const float *x, float *y, int k, int n,
+                              int batch, void *workspace, hipStream_t stream, const char **route) {
+    if ((type != 1 && type != 2) || !w_gate || !w_up || !x || !y || !workspace || k <= 0 || (k & 31) || n <= 0 ||
+        batch <= 0 || k > 16384)
+        return hipErrorInvalidValue;
+    if (type == 1 && ((reinterpret_cast<uintptr_t>(w_gate) & 15) || (reinterpret_cast<uintptr_t>(w_up) & 15)))
+        return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(x) & 15)) return hipErrorInvalidValue;
+    GemmPlan p = plan(k, n, batch);
+    p.bn = 128;                                 // 64 rows of each matrix per tile
+    p.n_tiles = (n + 63) / 64;
+    char *ws = static_cast<char *>(workspace);
+    _Float16 *x16 = reinterpret_cast<_Float16 *>(ws);
+    float *row_inv = reinterpret_cast<float *>(ws + p.x16_bytes);
+    if (type == 2)
+        hipLaunchKernelGGL(x_to_f16<true>, dim3(p.m_pad), dim3(kPrepassThreads), 0, stream, x, batch, k, p.k_pad, x16,
+                           row_inv);
+    else
+        hipLaunchKernelGGL(x_to_f16<false>, dim3(p.m_pad), dim3(kPrepassThreads), 0, stream, x, batch, k, p.k_pad, x16,
+                           row_inv);
+    hipError_t rc = hipGetLastError();
+    if (rc != hipSuccess) return rc;
+    const size_t w_bytes = type == 1 ? static_cast<size_t>(n) * k * 2 : static_cast<size_t>(n) * (k / 32) * 18;
+    if (route) *route = type == 2 ? "q4_gemm_swiglu_mfma" : "f16_gemm_swiglu_mfma";
+    if (type == 2) return launch_gemm<false, 128, true>(w_gate, w_up, x16, row_inv, y, batch, n, k, p, w_bytes, stream);
+    return launch_gemm<true, 128, true>(w_gate, w_up, x16, row_inv, y, batch, n, k, p, w_bytes, stream);
 }

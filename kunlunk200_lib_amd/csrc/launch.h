@@ -22,6 +22,16 @@ size_t kk_gemm_workspace_bytes(int k, int n, int batch);
 int kk_gemm(int type, const void *w, const float *x, float *y, int k, int n, int batch, void *workspace,
             hipStream_t stream, const char **route);
 
+// Y[batch,n] = SiLU(X W_gate^T) * (X W_up^T) on the prefill GEMM (same types,
+// workspace and alignment rules as kk_gemm; both matrices [n,k]).
+int kk_gemm_swiglu(int type, const void *w_gate, const void *w_up, const float *x, float *y, int k, int n,
+                   int batch, void *workspace, hipStream_t stream, const char **route);
+
+// y = SiLU(gate) * up over `rows` rows of `width` contiguous values of
+// `bytes` (4: F32, 2: F16) each; strides in bytes. F32 intermediates.
+int kk_swiglu(void *y, const void *gate, const void *up, int width, int rows, int gate_stride, int up_stride,
+              int output_stride, int bytes, hipStream_t stream);
+
 // Bytes of device workspace kk_i8_quantize needs for `count` activations.
 size_t kk_i8_workspace_bytes(int k, int batch);
 // Two-pass per-tensor INT8 quantization of X[batch,k] into `workspace`

@@ -12,6 +12,7 @@ namespace kunlun {
 namespace detail {
 thread_local const char * last_route = nullptr;
 const char * route_of_last_matmul() { return last_route; }
+void note_route(const char * route) { last_route = route; }
 } // namespace detail
 
 namespace {
@@ -41,6 +42,23 @@ int gemm_min_batch() {
     return v > 0 ? v : 64;
 }
 
+// The reference's matmul argument rules (reference src/k200.cpp:271-275):
+// supported type, K % 32 == 0, K <= 16384, products that fit int, and a
+// weight matrix of at most INT_MAX bytes.
+void validate_shape(const void * y, const void * w, const void * x, int k, int n, int batch, WeightType type,
+                    int tile) {
+    require(type == WeightType::f32 || type == WeightType::f16 || type == WeightType::q4_0 ||
+            type == WeightType::rowwise_i8);
+    require(k > 0 && k <= 16384 && k % 32 == 0 && n > 0 && batch > 0 && n <= INT_MAX / batch &&
+            k <= INT_MAX / batch);
+    require((size_t)n * batch <= INT_MAX / 4 && (size_t)k * batch <= INT_MAX / 4);
+    const size_t row_bytes = type == WeightType::f32   ? (size_t)k * 4
+                             : type == WeightType::f16 ? (size_t)k * 2
+                             : type == WeightType::q4_0 ? (size_t)k / 32 * 18
+                                                        : (size_t)k;
+    require(y && w && x && (size_t)n <= INT_MAX / row_bytes && (tile == 1 || tile == 16));
+}
+
 } // namespace
 
 Kernel::Kernel() : impl_(new Impl{}) {}
@@ -52,6 +70,7 @@ Kernel::~Kernel() {
         check(wait());
         release(impl_->id, impl_->i8_workspace, impl_->i8_workspace_size);
         release(impl_->id, impl_->gemm_workspace, impl_->gemm_workspace_size);
+        release(impl_->id, impl_->pair_workspace, impl_->pair_workspace_size);
     }
     delete impl_;
 }
@@ -59,16 +78,7 @@ Kernel::~Kernel() {
 void matmul(Kernel & kernel, int id, void * y, const void * w, const void * x, int k, int n, int batch,
             WeightType type, const float * scales, const float * maximum, int tile) {
     std::lock_guard<std::recursive_mutex> lock(detail::mutex());
-    require(type == WeightType::f32 || type == WeightType::f16 || type == WeightType::q4_0 ||
-            type == WeightType::rowwise_i8);
-    require(k > 0 && k <= 16384 && k % 32 == 0 && n > 0 && batch > 0 && n <= INT_MAX / batch &&
-            k <= INT_MAX / batch);
-    require((size_t)n * batch <= INT_MAX / 4 && (size_t)k * batch <= INT_MAX / 4);
-    const size_t row_bytes = type == WeightType::f32   ? (size_t)k * 4
-                             : type == WeightType::f16 ? (size_t)k * 2
-                             : type == WeightType::q4_0 ? (size_t)k / 32 * 18
-                                                        : (size_t)k;
-    require(y && w && x && (size_t)n <= INT_MAX / row_bytes && (tile == 1 || tile == 16));
+    validate_shape(y, w, x, k, n, batch, type, tile);
     require(kernel.impl_->id == -1 || kernel.impl_->id == id);
     require(type != WeightType::rowwise_i8 || (scales && maximum));
     // F32 activations and outputs must be element aligned (an F32 array always is).
@@ -101,6 +111,50 @@ void matmul(Kernel & kernel, int id, void * y, const void * w, const void * x, i
                           "kk_dense_matmul");
     }
     detail::last_route = impl.route;
+    detail::count_matmul(id);
+}
+
+void matmul_swiglu(Kernel & kernel, int id, void * y, const void * w_gate, const void * w_up, const void * x,
+                   int k, int n, int batch, WeightType type) {
+    std::lock_guard<std::recursive_mutex> lock(detail::mutex());
+    require(type == WeightType::f32 || type == WeightType::f16 || type == WeightType::q4_0);
+    validate_shape(y, w_gate, x, k, n, batch, type, 16);
+    require(w_up != nullptr);
+    require(kernel.impl_->id == -1 || kernel.impl_->id == id);
+    require(((uintptr_t)x & 3) == 0 && ((uintptr_t)y & 3) == 0);
+
+    detail::DeviceContext & ctx = detail::context(id);
+    Kernel::Impl & impl = *kernel.impl_;
+    impl.id = id;
+    const bool f16_aligned = ((uintptr_t)w_gate & 15) == 0 && ((uintptr_t)w_up & 15) == 0;
+    if ((type == WeightType::q4_0 || (type == WeightType::f16 && f16_aligned)) && batch >= gemm_min_batch() &&
+        ((uintptr_t)x & 15) == 0) {
+        grow(id, ctx, impl.gemm_workspace, impl.gemm_workspace_size, kk_gemm_workspace_bytes(k, n, batch));
+        detail::check_hip((hipError_t)kk_gemm_swiglu((int)type, w_gate, w_up, static_cast<const float *>(x),
+                                                     static_cast<float *>(y), k, n, batch, impl.gemm_workspace,
+                                                     ctx.stream, &impl.route),
+                          "kk_gemm_swiglu");
+    } else {
+        // gate and up rows side by side in the workspace: [batch][2n] F32
+        const size_t half = (size_t)batch * n * 4;
+        grow(id, ctx, impl.pair_workspace, impl.pair_workspace_size, 2 * half);
+        float * gate = static_cast<float *>(impl.pair_workspace);
+        float * up = reinterpret_cast<float *>(static_cast<char *>(impl.pair_workspace) + half);
+        const char * route = nullptr;
+        detail::check_hip((hipError_t)kk_dense_matmul((int)type, w_gate, static_cast<const float *>(x), gate, k, n,
+                                                      batch, ctx.stream, &route),
+                          "kk_dense_matmul");
+        detail::check_hip((hipError_t)kk_dense_matmul((int)type, w_up, static_cast<const float *>(x), up, k, n,
+                                                      batch, ctx.stream, &route),
+                          "kk_dense_matmul");
+        detail::check_hip((hipError_t)kk_swiglu(y, gate, up, n, batch, n * 4, n * 4, n * 4, 4, ctx.stream),
+                          "kk_swiglu");
+        impl.route = type == WeightType::q4_0 ? "q4_gemv_pair_swiglu"
+                     : type == WeightType::f16 ? "f16_gemv_pair_swiglu"
+                                               : "f32_gemv_pair_swiglu";
+    }
+    detail::last_route = impl.route;
+    detail::count_matmul(id);
     detail::count_matmul(id);
 }
 

@@ -29,8 +29,9 @@ size_t matmul_count(int device);
 [[noreturn]] void fail(const char * message);
 // Abort when a HIP call fails, naming the call.
 void check_hip(hipError_t status, const char * what);
-// Kernel route taken by the calling thread's last matmul (static string).
+// Kernel route taken by the calling thread's last matmul or swiglu (static string).
 const char * route_of_last_matmul();
+void note_route(const char * route);
 
 } // namespace detail
 
@@ -40,6 +41,8 @@ struct Kernel::Impl {
     size_t i8_workspace_size = 0;
     void * gemm_workspace = nullptr;    // fp16 activations of the prefill GEMM
     size_t gemm_workspace_size = 0;
+    void * pair_workspace = nullptr;    // gate and up GEMV outputs of matmul_swiglu
+    size_t pair_workspace_size = 0;
     const char * route = nullptr;
 };
 

@@ -384,3 +384,71 @@ void orc_i8_combine(const int64_t *primary, const int64_t *residual, const float
         }
     }
 }
+
+/* SiLU(g) * u in F32 with the reference's non-finite classification
+ * (reference kernels/kunlun-swiglu.xpu:27-39): finite inputs give
+ * (g / (1 + expf(-g))) * u; NaN if g or u is NaN or g is -Inf; +-Inf with
+ * sign(g) ^ sign(u) if one side is infinite and the other side (SiLU(g) for
+ * a finite g) is non-zero, NaN for Inf * 0. */
+float orc_swiglu_value(float g, float u) {
+    uint32_t gb, ub, bits;
+    float out;
+    memcpy(&gb, &g, 4);
+    memcpy(&ub, &u, 4);
+    uint32_t ga = gb & 0x7fffffffu, ua = ub & 0x7fffffffu;
+    if (ga < 0x7f800000u && ua < 0x7f800000u) {
+        float e = expf(-g);
+        float den = 1.0f + e;
+        float act = g / den;
+        return act * u;
+    }
+    uint32_t sign = (gb ^ ub) & 0x80000000u;
+    if (ga > 0x7f800000u || ua > 0x7f800000u || gb == 0xff800000u) {
+        bits = 0x7fc00000u;
+    } else if (ga == 0x7f800000u) {
+        bits = ua == 0 ? 0x7fc00000u : (sign | 0x7f800000u);
+    } else {
+        float e = expf(-g);
+        float act = g / (1.0f + e);
+        uint32_t ab;
+        memcpy(&ab, &act, 4);
+        bits = (ab & 0x7fffffffu) == 0 ? 0x7fc00000u : (sign | 0x7f800000u);
+    }
+    memcpy(&out, &bits, 4);
+    return out;
+}
+
+/* y = SiLU(gate) * up over rows of F32 (bytes == 4) or F16 (bytes == 2)
+ * values, strides in bytes, F32 intermediates and one final rounding (RNE to
+ * F16) (reference src/k200.cpp:324-368). Elements are processed in order, so
+ * an output that aliases an input element for element is handled. */
+void orc_swiglu(const void *gate, const void *up, void *y, int width, int rows, int gate_stride,
+                int up_stride, int output_stride, int bytes) {
+    const uint8_t *g8 = (const uint8_t *)gate, *u8 = (const uint8_t *)up;
+    uint8_t *y8 = (uint8_t *)y;
+    for (int r = 0; r < rows; ++r) {
+        for (int j = 0; j < width; ++j) {
+            const uint8_t *gp = g8 + (size_t)r * gate_stride + (size_t)j * bytes;
+            const uint8_t *up_ = u8 + (size_t)r * up_stride + (size_t)j * bytes;
+            uint8_t *yp = y8 + (size_t)r * output_stride + (size_t)j * bytes;
+            float g, u, v;
+            if (bytes == 4) {
+                memcpy(&g, gp, 4);
+                memcpy(&u, up_, 4);
+            } else {
+                uint16_t hg, hu;
+                memcpy(&hg, gp, 2);
+                memcpy(&hu, up_, 2);
+                g = orc_half_to_float(hg);
+                u = orc_half_to_float(hu);
+            }
+            v = orc_swiglu_value(g, u);
+            if (bytes == 4) {
+                memcpy(yp, &v, 4);
+            } else {
+                uint16_t h = orc_float_to_half(v);
+                memcpy(yp, &h, 2);
+            }
+        }
+    }
+}

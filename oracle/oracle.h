@@ -26,7 +26,13 @@
  *                            one-component Activation on single rows;
  *   orc_i8_dots            - brute-force small cases and numpy int64 matmul;
  *   orc_i8_combine         - hand-computed known answers;
- *   orc_matvec_f32         - within f32 accumulation error of orc_gold.
+ *   orc_matvec_f32         - within f32 accumulation error of orc_gold;
+ *   orc_swiglu_value       - every non-finite case of the reference rule
+ *                            worked by hand, and finite inputs within a few
+ *                            ulp of the FP64 closed form g*u/(1+exp(-g));
+ *   orc_swiglu             - strided rows, F16 rounding and aliasing against
+ *                            an element-by-element numpy loop over
+ *                            orc_swiglu_value.
  */
 #ifndef KUNLUN_ORACLE_H
 #define KUNLUN_ORACLE_H
@@ -67,6 +73,10 @@ int orc_i8_activation(const float *x, size_t count, int8_t *q0, int8_t *q1,
 void orc_i8_dots(const int8_t *a, int rows, const int8_t *w, int n, int k, int64_t *out);
 void orc_i8_combine(const int64_t *primary, const int64_t *residual, const float *scales,
                     float max0, float max1, int n, int batch, float *y);
+
+float orc_swiglu_value(float g, float u);
+void orc_swiglu(const void *gate, const void *up, void *y, int width, int rows, int gate_stride,
+                int up_stride, int output_stride, int bytes);
 
 #ifdef __cplusplus
 }

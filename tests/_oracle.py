@@ -49,6 +49,8 @@ class Oracle:
             "orc_i8_activation": (I, [P, Z, P, P, P, P]),
             "orc_i8_dots": (None, [P, I, P, I, I, P]),
             "orc_i8_combine": (None, [P, P, P, ctypes.c_float, ctypes.c_float, I, I, P]),
+            "orc_swiglu_value": (ctypes.c_float, [ctypes.c_float, ctypes.c_float]),
+            "orc_swiglu": (None, [P, P, P, I, I, I, I, I, I]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -171,6 +173,31 @@ class Oracle:
         batch, n = primary.shape
         y = np.empty((batch, n), np.float32)
         self.lib.orc_i8_combine(_p(primary), _p(residual), _p(scales), float(max0), float(max1), n, batch, _p(y))
+        return y
+
+    def swiglu_value(self, g: float, u: float) -> float:
+        return self.lib.orc_swiglu_value(g, u)
+
+    def swiglu_bytes(self, gate: np.ndarray, up: np.ndarray, y: np.ndarray, width: int, rows: int,
+                     gate_stride: int, up_stride: int, output_stride: int, bytes_: int,
+                     gate_offset: int = 0, up_offset: int = 0, output_offset: int = 0) -> None:
+        """orc_swiglu on byte buffers (uint8 arrays), in place into y; offsets in bytes."""
+        for a in (gate, up, y):
+            assert a.dtype == np.uint8 and a.flags.c_contiguous
+        base = lambda a, off: ctypes.c_void_p(a.ctypes.data + off)  # noqa: E731
+        self.lib.orc_swiglu(base(gate, gate_offset), base(up, up_offset), base(y, output_offset), width, rows,
+                            gate_stride, up_stride, output_stride, bytes_)
+
+    def swiglu(self, g: np.ndarray, u: np.ndarray) -> np.ndarray:
+        """Dense [rows, width] F32 (or float16) SwiGLU; output dtype follows the input."""
+        g = np.ascontiguousarray(g)
+        u = np.ascontiguousarray(u, dtype=g.dtype)
+        bytes_ = g.dtype.itemsize
+        assert bytes_ in (2, 4)
+        rows, width = g.shape
+        y = np.empty_like(g)
+        gb, ub, yb = (a.view(np.uint8).reshape(-1) for a in (g, u, y))
+        self.swiglu_bytes(gb, ub, yb, width, rows, width * bytes_, width * bytes_, width * bytes_, bytes_)
         return y
 
     def rowwise_i8_matmul(self, w: np.ndarray, x: np.ndarray) -> np.ndarray:

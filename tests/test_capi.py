@@ -143,3 +143,66 @@ def test_upload_i8_rows_contract_aborts():
     env = dict(os.environ, PYTHONPATH=ROOT, HIP_VISIBLE_DEVICES="")
     proc = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=120)
     assert proc.returncode == -signal.SIGABRT and "NOT REJECTED" not in proc.stdout
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU layout and pointer contract (reference src/k200.cpp:324-350;
+# contract cases of reference bench/swiglu-contract.cpp). Every case is
+# rejected before any device work, so these run without a GPU.
+
+def test_swiglu_reason_rules(kl):
+    L = kl.SwiGLULayout
+    f32, f16 = kl.InputType.f32, kl.InputType.f16
+    assert kl.swiglu_reason(L(256, 2, 1024, 1024, 1024, f32)) == ""
+    assert kl.swiglu_reason(L(256, 2, 512, 512, 512, f16)) == ""
+    assert kl.swiglu_reason(L(256, 2, 1024, 1024, 1024, 99)) == "type"
+    for width, rows in ((0, 1), (1, 0), (65537, 1), (-3, 2), (256, 2 ** 31 // 256 // 4 + 1)):
+        assert kl.swiglu_reason(L(width, rows, 2 ** 20, 2 ** 20, 2 ** 20, f32)) == "shape"
+    assert kl.swiglu_reason(L(65536, 1, 262144, 262144, 262144, f32)) == ""
+    assert kl.swiglu_reason(L(256, 2, 1023, 1024, 1024, f32)) == "stride"      # shorter than a row
+    assert kl.swiglu_reason(L(256, 2, 1024, 1026, 1024, f32)) == "stride"      # not a multiple of 4
+    assert kl.swiglu_reason(L(256, 2, 1024, 1024, 514, f16)) == ""             # f16: multiple of 2 is enough
+    assert kl.swiglu_reason(L(256, 2, 1024, 1024, 513, f16)) == "stride"
+    # rows - 1 strides plus one row must stay within INT_MAX bytes
+    assert kl.swiglu_reason(L(256, 2 ** 16, 2 ** 15 + 1024, 1024, 1024, f32)) == "byte extent"
+
+
+SWIGLU_CONTRACT = list(range(11))
+
+
+@pytest.mark.parametrize("case", SWIGLU_CONTRACT)
+def test_swiglu_contract_rejects_before_device(kl, case):
+    count = ctypes.c_int(0)
+    if kl.load().kunlun_device_count(ctypes.byref(count)) == 0 and count.value > 0:
+        pytest.skip("contract cases pass fabricated pointers: they run on a host without a GPU")
+    base = kl.SwiGLULayout(256, 2, 1024, 1024, 1024, kl.InputType.f32)
+    layout = kl.SwiGLULayout(**vars(base))
+    device, y, g, u = 0, 0x100000, 0x200000, 0x300000
+    yb = gb = ub = 2048
+    if case == 0:
+        layout.width = 0
+    elif case == 1:
+        layout.rows = 0
+    elif case == 2:
+        layout.width = 65537
+    elif case == 3:
+        layout.gate_stride = 1023
+    elif case == 4:
+        layout.rows = 2 ** 31 - 1
+    elif case == 5:
+        layout.type = 99
+    elif case == 6:
+        yb = 1024                       # output span beyond its size
+    elif case == 7:
+        g = None
+    elif case == 8:
+        y = 0x100001                    # misaligned output
+    elif case == 9:
+        y = g + 4                       # partial overlap with gate
+    elif case == 10:
+        device = -1
+    kernel = kl.Kernel()
+    before = kl.allocated_bytes(0)
+    assert kl.swiglu(kernel, device, y, yb, g, gb, u, ub, layout) is False
+    assert kl.allocated_bytes(0) == before
+    assert kernel.route is None

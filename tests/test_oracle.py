@@ -236,3 +236,87 @@ def test_q4_quantize_properties(oracle):
     assert np.all(err[~clamp] <= tol[..., 0:1].repeat(32, 2)[~clamp])
     # the all-zero block: zero scale, every nibble 8
     assert d[3, 1] == 0 and np.all(nib[3, 1] == 8)
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU (reference kernels/kunlun-swiglu.xpu:27-39): the non-finite cases
+# worked by hand from the rule, and finite values against the FP64 closed form.
+
+INF, NAN = float("inf"), float("nan")
+
+
+def _classify(v):
+    if np.isnan(v):
+        return "nan"
+    if np.isinf(v):
+        return "+inf" if v > 0 else "-inf"
+    return "finite"
+
+
+@pytest.mark.parametrize("g,u,expected", [
+    (0.0, INF, "nan"),        # SiLU(0) = 0, 0 * Inf
+    (-0.0, -INF, "nan"),
+    (1.0, INF, "+inf"),
+    (-1.0, INF, "-inf"),      # SiLU(-1) < 0
+    (-1.0, -INF, "+inf"),
+    (-200.0, INF, "nan"),     # SiLU(-200) underflows to -0
+    (INF, 0.0, "nan"),
+    (INF, 2.0, "+inf"),
+    (INF, -2.0, "-inf"),
+    (-INF, 0.0, "nan"),       # g = -Inf is always NaN
+    (-INF, 5.0, "nan"),
+    (1.0, NAN, "nan"),
+    (NAN, 1.0, "nan"),
+    (NAN, INF, "nan"),
+])
+def test_swiglu_nonfinite_rule(oracle, g, u, expected):
+    assert _classify(oracle.swiglu_value(g, u)) == expected
+
+
+def test_swiglu_finite_closed_form(oracle):
+    rng = np.random.default_rng(3)
+    g = np.concatenate([rng.standard_normal(4000) * 8, np.linspace(-100, 100, 1001), [0.0, -0.0, 1e-8, -1e-8]])
+    u = rng.standard_normal(g.size) * 4
+    got = np.array([oracle.swiglu_value(float(a), float(b)) for a, b in zip(g.astype(np.float32),
+                                                                          u.astype(np.float32))])
+    g64, u64 = g.astype(np.float32).astype(np.float64), u.astype(np.float32).astype(np.float64)
+    ref = g64 * u64 / (1.0 + np.exp(-g64))
+    # e^-g overflows F32 below g = -88.72: the F32 formula then gives g / Inf = -0
+    # exactly, times u (a signed zero), where FP64 still has a subnormal result
+    overflow = -g64 > np.log(np.finfo(np.float32).max)
+    assert np.all(got[overflow] == 0.0)
+    # elsewhere expf, the division and the product round once each: a few ulp of F32
+    tol = 4 * np.finfo(np.float32).eps * np.abs(ref) + 1e-44
+    assert np.all(np.abs(got - ref)[~overflow] <= tol[~overflow])
+    # sign and zero structure
+    assert oracle.swiglu_value(0.0, 3.0) == 0.0
+    assert oracle.swiglu_value(2.0, 0.0) == 0.0
+
+
+def test_swiglu_rows_strides_f16_and_alias(oracle):
+    rng = np.random.default_rng(4)
+    width, rows = 37, 5
+    for bytes_, dt in ((4, np.float32), (2, np.float16)):
+        stride = width * bytes_ + 3 * bytes_          # gap between rows
+        gate = np.zeros(rows * stride, np.uint8)
+        up = np.zeros(rows * stride, np.uint8)
+        gv = (rng.standard_normal((rows, width)) * 3).astype(dt)
+        uv = (rng.standard_normal((rows, width)) * 3).astype(dt)
+        for r in range(rows):
+            gate[r * stride:r * stride + width * bytes_] = gv[r].view(np.uint8)
+            up[r * stride:r * stride + width * bytes_] = uv[r].view(np.uint8)
+        y = np.full(rows * stride, 0xA5, np.uint8)
+        oracle.swiglu_bytes(gate, up, y, width, rows, stride, stride, stride, bytes_)
+        for r in range(rows):
+            row = y[r * stride:(r + 1) * stride]
+            out = row[:width * bytes_].view(dt)
+            expect = np.array([oracle.swiglu_value(float(a), float(b)) for a, b in zip(gv[r], uv[r])],
+                              np.float32).astype(dt)   # one final rounding (numpy float16 is RNE)
+            assert np.array_equal(out.view(np.uint8), expect.view(np.uint8))
+            assert np.all(row[width * bytes_:] == 0xA5)  # the gap is not written
+        # output aliasing gate element for element gives the same values
+        alias = gate.copy()
+        oracle.swiglu_bytes(alias, up, alias, width, rows, stride, stride, stride, bytes_)
+        for r in range(rows):
+            assert np.array_equal(alias[r * stride:r * stride + width * bytes_],
+                                  y[r * stride:r * stride + width * bytes_])
