@@ -207,6 +207,61 @@ def gemm_leg(kernel, events, stream, device: int, reps: int) -> dict:
     return out
 
 
+SMALL_BATCH_Q4 = (4096, 14336, (2, 4, 8, 16))
+SMALL_DENSE = (4096, 4096, (1, 8))                   # F16 / F32 part of configs[2]
+
+
+def small_batch_leg(kernel, events, stream, device: int, reps: int) -> dict:
+    """Q4_0 K4096 x N14336 at batch 2..16 and F16/F32 4096^2 at
+    batch 1 and 8, each over rotating weight copies (>= 640 MB) so weights stream
+    from HBM. GB/s = algorithmic bytes (weights + 4bk + 4bn) / launch time."""
+    out = {}
+    rng = np.random.Generator(np.random.PCG64(21))
+
+    def run(tag, type_, k, n, batch, nbytes, fill):
+        first = kl.Buffer(device, nbytes)
+        fill(first)
+        bufs = [first]
+        for _ in range(max(2, -(-ROTATE_BYTES // nbytes)) - 1):
+            b = kl.Buffer(device, nbytes)
+            with kl.runtime_mutex():
+                kl.select(device)
+                kl.check(kl.copy(b.data, first.data, nbytes, kl.CopyKind.device_to_device))
+                kl.check(kl.wait())
+            bufs.append(b)
+        xb = kl.Buffer(device, 4 * batch * k)
+        xb.upload(rng.standard_normal((batch, k), dtype=np.float32))
+        yb = kl.Buffer(device, 4 * batch * n)
+        with kl.runtime_mutex():
+            for i in range(5):
+                kl.matmul(kernel, device, yb.data, bufs[i % len(bufs)].data, xb.data, k, n, batch, type_)
+            kl.select(device)
+            kl.check(kl.wait())
+            start, stop = events.create(), events.create()
+            events.record(start, stream)
+            for i in range(reps):
+                kl.matmul(kernel, device, yb.data, bufs[i % len(bufs)].data, xb.data, k, n, batch, type_)
+            events.record(stop, stream)
+            ms = events.elapsed_ms(start, stop) / reps
+            kl.check(kl.wait())
+        total = nbytes + 4 * batch * k + 4 * batch * n
+        out[tag] = {"us": round(ms * 1e3, 3), "gbps": round(total / (ms * 1e-3) / 1e9, 1),
+                    "hbm_frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "route": kernel.route}
+        for b in bufs + [xb, yb]:
+            b.close()
+
+    k, n, batches = SMALL_BATCH_Q4
+    for batch in batches:
+        run(f"q4_k{k}_n{n}_b{batch}", kl.WeightType.q4_0, k, n, batch, n * (k // 32) * 18,
+            lambda b: upload_q4_matrix(b, k, n, seed=4000 + n))
+    k, n, batches = SMALL_DENSE
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+    for type_, name, arr in ((kl.WeightType.f16, "f16", w.astype(np.float16)), (kl.WeightType.f32, "f32", w)):
+        for batch in batches:
+            run(f"{name}_k{k}_n{n}_b{batch}", type_, k, n, batch, arr.nbytes, lambda b, arr=arr: b.upload(arr))
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -216,7 +271,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gemm-reps", type=int, default=50, help="timed batch-512 GEMM calls per shape (0: skip)")
-    ap.add_argument("--only", choices=[name for name, _, _ in LAYER] + ["gemm", "copy"],
+    ap.add_argument("--small-reps", type=int, default=100, help="timed calls per small-batch config (0: skip)")
+    ap.add_argument("--only", choices=[name for name, _, _ in LAYER] + ["gemm", "copy", "small"],
                     help="profiling aid: time only this GEMV's launch loop, the GEMM leg, or (copy) a "
                          f"{COPY_BYTES >> 20} MiB device-to-device copy that calibrates the traffic counters")
     args = ap.parse_args()
@@ -233,6 +289,10 @@ def main() -> int:
 
     if args.only == "gemm":
         print(json.dumps({"gemm_b512": gemm_leg(kernel, events, stream, device, args.gemm_reps)}), flush=True)
+        return 0
+    if args.only == "small":
+        print(json.dumps({"small_batch": small_batch_leg(kernel, events, stream, device, args.small_reps)}),
+              flush=True)
         return 0
     if args.only == "copy":
         print(json.dumps({"copy": copy_leg(events, stream, device)}), flush=True)
@@ -323,6 +383,7 @@ def main() -> int:
     achieved = dom["gbps"]
 
     gemm = gemm_leg(kernel, events, stream, device, args.gemm_reps) if args.gemm_reps > 0 else None
+    small = small_batch_leg(kernel, events, stream, device, args.small_reps) if args.small_reps > 0 else None
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     result = {
         "metric": METRIC,
@@ -362,6 +423,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "per_shape": per_shape,
         "gemm_b512": gemm,
+        "small_batch": small,
     }
     print(json.dumps(result), flush=True)
     for bufs in copies.values():

@@ -32,6 +32,13 @@ int kk_gemm_swiglu(int type, const void *w_gate, const void *w_up, const float *
 int kk_swiglu(void *y, const void *gate, const void *up, int width, int rows, int gate_stride, int up_stride,
               int output_stride, int bytes, hipStream_t stream);
 
+// Q4_0 GEMV for batch 1..16 on fp16 MFMA (one pass over W): K % 64 == 0,
+// 4-byte aligned weights; workspace of kk_q4_mfma_gemv_workspace_bytes(k)
+// holds the activation fragments; `cus` sizes the grid.
+size_t kk_q4_mfma_gemv_workspace_bytes(int k);
+int kk_q4_mfma_gemv(const void *w, const float *x, float *y, int k, int n, int batch, void *workspace, int cus,
+                    hipStream_t stream);
+
 // Bytes of device workspace kk_i8_quantize needs for `count` activations.
 size_t kk_i8_workspace_bytes(int k, int batch);
 // Two-pass per-tensor INT8 quantization of X[batch,k] into `workspace`

@@ -4,6 +4,7 @@
 #include "launch.h"
 #include "runtime_internal.h"
 
+#include <algorithm>
 #include <climits>
 #include <cstdint>
 #include <cstdlib>
@@ -40,6 +41,16 @@ int gemm_min_batch() {
     const char * value = std::getenv("KUNLUN_GEMM_MIN_BATCH");
     const int v = value && *value ? std::atoi(value) : 64;
     return v > 0 ? v : 64;
+}
+
+// Batch range of the single-pass Q4_0 MFMA GEMV (KUNLUN_Q4_MFMA_MIN/MAX, within
+// 1..16). Below 5 columns the batch-1 kernel's passes (two columns each) are faster.
+bool q4_mfma_batch(int batch) {
+    const char * lo = std::getenv("KUNLUN_Q4_MFMA_MIN");
+    const char * hi = std::getenv("KUNLUN_Q4_MFMA_MAX");
+    const int min_b = std::max(1, lo && *lo ? std::atoi(lo) : 5);
+    const int max_b = std::min(16, hi && *hi ? std::atoi(hi) : 16);
+    return batch >= min_b && batch <= max_b;
 }
 
 // The reference's matmul argument rules (reference src/k200.cpp:271-275):
@@ -104,6 +115,12 @@ void matmul(Kernel & kernel, int id, void * y, const void * w, const void * x, i
         detail::check_hip((hipError_t)kk_gemm((int)type, w, static_cast<const float *>(x), static_cast<float *>(y), k,
                                               n, batch, impl.gemm_workspace, ctx.stream, &impl.route),
                           "kk_gemm");
+    } else if (type == WeightType::q4_0 && q4_mfma_batch(batch) && k % 64 == 0 && ((uintptr_t)w & 3) == 0) {
+        grow(id, ctx, impl.gemm_workspace, impl.gemm_workspace_size, kk_q4_mfma_gemv_workspace_bytes(k));
+        detail::check_hip((hipError_t)kk_q4_mfma_gemv(w, static_cast<const float *>(x), static_cast<float *>(y), k, n,
+                                                      batch, impl.gemm_workspace, ctx.cus, ctx.stream),
+                          "kk_q4_mfma_gemv");
+        impl.route = "q4_mfma_gemv";
     } else {
         detail::check_hip((hipError_t)kk_dense_matmul((int)type, w, static_cast<const float *>(x),
                                                       static_cast<float *>(y), k, n, batch, ctx.stream,

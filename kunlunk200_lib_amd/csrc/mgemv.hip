@@ -1,0 +1,354 @@
+// Small-batch (2..16) Q4_0 GEMV on gfx950 fp16 MFMA, one pass over the
+// weights for the whole batch.
+//
+// Y[b, r] = sum_k X[b, k] * W[r, k]  (reference kernels/kunlun-matvec.xpu:24-79,
+// which re-reads W once per batch column). HBM-bound: every weight byte is
+// read once per call, like the batch-1 GEMV.
+//
+// Per 32-value Q4_0 block, one v_mfma_f32_16x16x32_f16 pair computes the
+// block sums S[m][r] = sum_k X[m][k] * (q[r][k] - 8) for 16 batch rows (A) by
+// 16 weight rows (B); the block's F16 scale d[r] then scales them in F32:
+// acc += d * S. The weights enter as exact fp16 (q - 8) (magic-number
+// decode), and each activation row as fp16 hi + lo of x * 2^s_m, a per-row
+// power of two with max |x * 2^s_m| < 2^14: |x*2^s - hi - lo| <= 2^-22
+// |x*2^s| (about the F32 input precision), so the only other rounding is the
+// F32 accumulation.
+//
+// Data flow: a prepass (x_to_frag) writes the activations as MFMA A
+// fragments [block][hi|lo][lane][8 halves] in the weight nibble order (block
+// position 8g + t of lane group g holds value (4g, 4g+2, 4g+1, 4g+3, 16+4g,
+// 16+4g+2, 16+4g+1, 16+4g+3)[t], the order a nibble dword decodes to). The
+// GEMV workgroup (4 waves, one 16-row weight tile per wave) walks K in
+// chunks of 16 blocks: the chunk's A fragments (32 KiB, shared by the four
+// waves, from L2) arrive one chunk ahead and each wave's raw 18-byte weight
+// blocks (16 rows x 288 B, padded rows, from HBM) three chunks ahead, by
+// direct global -> LDS copies; each lane then reads its nibble dword and
+// scale.
+#include "device_common.h"
+#include "launch.h"
+
+#include <algorithm>
+
+namespace {
+
+using kk::kWave;
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBatchRows = 16;                      // MFMA M (batch rows >= batch are zero)
+constexpr int kTileRows = 16;                       // MFMA N: weight rows per wave task
+constexpr int kWaves = 4;
+constexpr int kThreads = kWave * kWaves;
+constexpr int kChunkBlocks = 16;                    // K chunk of 512 values
+constexpr int kChunkRowBytes = kChunkBlocks * 18;   // 288 bytes of one weight row per chunk
+constexpr int kStageStride = 304;                   // staged row stride: lane reads hit 64 distinct banks
+constexpr int kStageBytes = 5 * 1024;               // per wave and buffer: 16 x 304 B rounded to whole 1 KiB copies
+constexpr int kFragBlockBytes = 2 * kWave * 16;     // hi and lo A fragments of one block: 2 KiB
+constexpr int kChunkFragBytes = kChunkBlocks * kFragBlockBytes;           // 32 KiB
+constexpr int kXBuffers = 2;                        // A fragments: one chunk ahead (from L2)
+constexpr int kWBuffers = 4;                        // weights: three chunks ahead (from HBM)
+constexpr int kWAhead = kWBuffers - 1;
+constexpr int kStageSetBytes = kWaves * kStageBytes;                      // one chunk of all four tiles
+constexpr int kLdsBytes = kXBuffers * kChunkFragBytes + kWBuffers * kStageSetBytes;   // 144 KiB
+constexpr int kWCopies = kStageBytes / 1024;        // 16-byte copies of a full weight chunk per lane
+// s_waitcnt with vmcnt = kWCopies (expcnt, lgkmcnt not waited on): the copy
+// issued last (weights, kWCopies instructions) may stay in flight
+constexpr int kWaitAllButWeights = 0x0F70 | kWCopies;
+constexpr int kPrepassThreads = 1024;
+static_assert(kTileRows * kStageStride <= kStageBytes, "staged tile fits its copies");
+static_assert(kStageStride % 16 == 0 && kChunkRowBytes % 16 == 0, "16-byte copies never straddle a row");
+
+// ---------------------------------------------------------------------------
+// Prepass: one workgroup per A row m (16); each thread holds its items' values
+// between the max reduction and the stores (one pass over X). Row scale
+// s_m = 2^(14 - e), 2^(e-1) <= max|x_m| < 2^e (non-finite or zero rows keep
+// s = 1); frag holds blocks_pad blocks (zero beyond k and for rows >= batch).
+__global__ __launch_bounds__(kPrepassThreads) void x_to_frag(const float *__restrict__ x, int batch, int k,
+                                                             int blocks_pad, _Float16 *__restrict__ frag,
+                                                             float *__restrict__ row_inv) {
+    __shared__ float partial[kPrepassThreads / kWave];
+    constexpr int kMaxItems = 16384 / 32 * 4 / kPrepassThreads;   // 2: (block, lane group) items per thread
+    const int m = blockIdx.x;
+    const bool real = m < batch;
+    const float *row = x + static_cast<size_t>(real ? m : 0) * k;
+    const int blocks = k >> 5;
+    float v[kMaxItems][8];
+    float mx = 0.0f;
+#pragma unroll
+    for (int it = 0; it < kMaxItems; ++it) {
+        const int item = threadIdx.x + kPrepassThreads * it;
+        const int j = item >> 2, g = item & 3;
+        if (real && j < blocks) {
+            // block positions (4g, 4g+2, 4g+1, 4g+3, 16+4g, 16+4g+2, 16+4g+1, 16+4g+3)
+            const float4 lo = *reinterpret_cast<const float4 *>(row + j * 32 + 4 * g);
+            const float4 hi = *reinterpret_cast<const float4 *>(row + j * 32 + 16 + 4 * g);
+            v[it][0] = lo.x; v[it][1] = lo.z; v[it][2] = lo.y; v[it][3] = lo.w;
+            v[it][4] = hi.x; v[it][5] = hi.z; v[it][6] = hi.y; v[it][7] = hi.w;
+        } else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) v[it][t] = 0.0f;
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) mx = fmaxf(mx, fabsf(v[it][t]));
+    }
+    mx = kk::wave_max(mx);
+    if ((threadIdx.x & (kWave - 1)) == 0) partial[threadIdx.x / kWave] = mx;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kPrepassThreads / kWave; ++i) mx = fmaxf(mx, partial[i]);
+    int e = __builtin_amdgcn_frexp_expf(mx);
+    const bool finite = mx <= 3.402823466e38f && mx > 0.0f;
+    e = finite ? max(min(e, 126), -100) : 14;
+    const float s = ldexpf(1.0f, 14 - e);
+    if (threadIdx.x == 0) row_inv[m] = ldexpf(1.0f, e - 14);
+#pragma unroll
+    for (int it = 0; it < kMaxItems; ++it) {
+        const int item = threadIdx.x + kPrepassThreads * it;
+        if (item >= blocks_pad * 4) break;
+        const int j = item >> 2, g = item & 3;
+        half8 hi, lo;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const float a = v[it][t] * s;
+            const _Float16 h = static_cast<_Float16>(a);
+            hi[t] = h;
+            lo[t] = static_cast<_Float16>(a - static_cast<float>(h));
+        }
+        const int lane = g * kBatchRows + m;
+        *reinterpret_cast<half8 *>(frag + (static_cast<size_t>(j * 2 + 0) * kWave + lane) * 8) = hi;
+        *reinterpret_cast<half8 *>(frag + (static_cast<size_t>(j * 2 + 1) * kWave + lane) * 8) = lo;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// B fragment of lane (row n, group g) from nibble dword g of a block:
+// positions (4g, 4g+2, 4g+1, 4g+3, 16+4g, 16+4g+2, 16+4g+1, 16+4g+3), each
+// the exact fp16 q - 8 via (0x6400 | q) - 1032.
+__device__ __forceinline__ half8 decode_nibbles(uint32_t qs) {
+    union { uint32_t u; half2v h; } p0, p1, p2, p3;
+    p0.u = (qs & 0x000f000fu) | 0x64006400u;
+    p1.u = ((qs >> 8) & 0x000f000fu) | 0x64006400u;
+    p2.u = ((qs >> 4) & 0x000f000fu) | 0x64006400u;
+    p3.u = ((qs >> 12) & 0x000f000fu) | 0x64006400u;
+    const half2v off = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
+    const half2v a = p0.h + off, b = p1.h + off, c = p2.h + off, d = p3.h + off;
+    half8 out;
+    out[0] = a[0]; out[1] = a[1]; out[2] = b[0]; out[3] = b[1];
+    out[4] = c[0]; out[5] = c[1]; out[6] = d[0]; out[7] = d[1];
+    return out;
+}
+
+// Workgroup barrier without a memory fence. The LDS reads of a wave are
+// complete when it reaches the barrier (their values feed the MFMAs before
+// it), and the copies a step reads were waited for with s_waitcnt; the asm
+// statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+}
+
+// One block: lane (n, g) reads its scale and nibble dword from the staged row
+// (`srow` = row n, `qrow` = row n + 4 g + 2 bytes) and its A fragments.
+__device__ __forceinline__ void block_mma(const uint8_t *srow, const uint8_t *qrow, const uint8_t *frow, int j,
+                                          float4v &acc) {
+    const uint32_t d16 = *reinterpret_cast<const uint16_t *>(srow + 18 * j);
+    const uint32_t qs = *reinterpret_cast<const uint16_t *>(qrow + 18 * j) |
+                        (static_cast<uint32_t>(*reinterpret_cast<const uint16_t *>(qrow + 18 * j + 2)) << 16);
+    const half8 bf = decode_nibbles(qs);
+    const half8 ahi = *reinterpret_cast<const half8 *>(frow + j * kFragBlockBytes);
+    const half8 alo = *reinterpret_cast<const half8 *>(frow + j * kFragBlockBytes + kWave * 16);
+    float4v t = {0.0f, 0.0f, 0.0f, 0.0f};
+    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bf, t, 0, 0, 0);
+    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bf, t, 0, 0, 0);
+    const float d = kk::half_bits_to_float(d16);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = fmaf(d, t[r], acc[r]);
+}
+
+// kGroup consecutive blocks: all LDS reads first, then the MFMA pairs (one
+// independent chain per block), then the scaled accumulation, so the reads'
+// latency and the MFMA latency overlap across blocks.
+constexpr int kGroup = 8;
+__device__ __forceinline__ void block_group(const uint8_t *srow, const uint8_t *qrow, const uint8_t *frow, int j0,
+                                            float4v &acc) {
+    uint32_t d16[kGroup], qlo[kGroup], qhi[kGroup];
+    half8 ahi[kGroup], alo[kGroup];
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i) {
+        const int j = j0 + i;
+        d16[i] = *reinterpret_cast<const uint16_t *>(srow + 18 * j);
+        qlo[i] = *reinterpret_cast<const uint16_t *>(qrow + 18 * j);
+        qhi[i] = *reinterpret_cast<const uint16_t *>(qrow + 18 * j + 2);
+        ahi[i] = *reinterpret_cast<const half8 *>(frow + j * kFragBlockBytes);
+        alo[i] = *reinterpret_cast<const half8 *>(frow + j * kFragBlockBytes + kWave * 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);   // reads issued in block order, consumed in block order
+    float4v t[kGroup];
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i) {
+        const half8 bf = decode_nibbles(qlo[i] | (qhi[i] << 16));
+        t[i] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+        t[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[i], bf, t[i], 0, 0, 0);
+        t[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[i], bf, t[i], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i) {
+        const float d = kk::half_bits_to_float(d16[i]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = fmaf(d, t[i][r], acc[r]);
+    }
+}
+
+// Workgroup: 4 waves, wave w owns weight tile (base + w) of 16 rows; every
+// wave runs every chunk (tiles past the end read a valid tile and store
+// nothing), so the barriers are uniform. Chunk c + 1 is copied global -> LDS
+// (global_load_lds, no registers) while chunk c is computed.
+__global__ __launch_bounds__(kThreads) void q4_mfma_gemv(const uint8_t *__restrict__ w,
+                                                        const _Float16 *__restrict__ frag,
+                                                        const float *__restrict__ row_inv, float *__restrict__ y,
+                                                        int k, int n, int batch, int tiles) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int blocks = k >> 5;
+    const size_t row_bytes = static_cast<size_t>(blocks) * 18;      // multiple of 4 (K % 64 == 0)
+    const int chunks = (blocks + kChunkBlocks - 1) / kChunkBlocks;
+    const int nl = lane & 15, g = lane >> 4;
+    const uint8_t *fbytes = reinterpret_cast<const uint8_t *>(frag);
+
+    for (int base = blockIdx.x * kWaves; base < tiles; base += gridDim.x * kWaves) {
+        const int tile = base + wid;
+        const int r0 = min(tile, tiles - 1) * kTileRows;
+        uint8_t *const xbase = lds;
+        uint8_t *const wbase = lds + kXBuffers * kChunkFragBytes;
+
+        // This wave's quarter of chunk c's A fragments (8 x 1 KiB) into X buffer c % 2.
+        auto copy_x = [&](int c) {
+            c = min(c, chunks - 1);                         // past the end: a copy nobody reads
+            uint8_t *xb = xbase + (c & 1) * kChunkFragBytes;
+            const uint8_t *fsrc = fbytes + static_cast<size_t>(c) * kChunkFragBytes;
+#pragma unroll
+            for (int i = 0; i < kChunkFragBytes / (kWaves * 1024); ++i) {
+                const int block_kib = i * kWaves + wid;
+                __builtin_amdgcn_global_load_lds(fsrc + block_kib * 1024 + lane * 16, xb + block_kib * 1024, 16, 0, 0);
+            }
+        };
+        // This wave's tile rows of chunk c into stage buffer `slot`: the staged
+        // [row][304 B] image as 5 x 1 KiB copies (padding lanes and bytes past
+        // a row's end copy a dummy in-bounds source and are never read). A
+        // partial last chunk copies dwords so that no copy crosses a row's end.
+        auto copy_w = [&](int c, int slot) {
+            c = min(c, chunks - 1);
+            uint8_t *sb = wbase + slot * kStageSetBytes + wid * kStageBytes;
+            const int valid = min(kChunkBlocks, blocks - c * kChunkBlocks) * 18;
+            const size_t chunk_off = static_cast<size_t>(c) * kChunkRowBytes;
+            if (valid == kChunkRowBytes) {
+#pragma unroll
+                for (int i = 0; i < kWCopies; ++i) {
+                    const int p = i * 1024 + lane * 16;
+                    const int row = p / kStageStride, col = p - row * kStageStride;
+                    const bool in = row < kTileRows && col < kChunkRowBytes;
+                    const size_t off = in ? static_cast<size_t>(min(r0 + row, n - 1)) * row_bytes + chunk_off + col : 0;
+                    __builtin_amdgcn_global_load_lds(w + off, sb + i * 1024, 16, 0, 0);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < kStageBytes / 256; ++i) {
+                    const int p = i * 256 + lane * 4;
+                    const int row = p / kStageStride, col = p - row * kStageStride;
+                    const bool in = row < kTileRows && col + 4 <= valid;
+                    const size_t off = in ? static_cast<size_t>(min(r0 + row, n - 1)) * row_bytes + chunk_off + col : 0;
+                    __builtin_amdgcn_global_load_lds(w + off, sb + i * 256, 4, 0, 0);
+                }
+            }
+        };
+
+        float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        // Issue order per step: X (c + 1), then W (c + 3). At the top of step c
+        // everything but the last weight copy (chunk c + 2) must have landed,
+        // which includes X (c) and W (c); a partial-chunk copy has more
+        // instructions, so the wait is then stricter than needed, never looser.
+        copy_x(0);
+        for (int a = 0; a < kWAhead; ++a) copy_w(a, a);
+        for (int c = 0; c < chunks; ++c) {
+            if (c == 0) __builtin_amdgcn_s_waitcnt(0);
+            else __builtin_amdgcn_s_waitcnt(kWaitAllButWeights);
+            // every wave's copies of chunk c landed and its reads of step c - 1
+            // are done. A bare s_barrier: a fenced __syncthreads would also wait
+            // for the copies still meant to be in flight.
+            lds_barrier();
+            copy_x(c + 1);
+            copy_w(c + kWAhead, (c + kWAhead) % kWBuffers);
+            const uint8_t *xb = xbase + (c & 1) * kChunkFragBytes;
+            const uint8_t *srow = wbase + (c % kWBuffers) * kStageSetBytes + wid * kStageBytes + nl * kStageStride;
+            const uint8_t *qrow = srow + 2 + 4 * g;
+            const uint8_t *frow = xb + lane * 16;
+            const int nb = min(kChunkBlocks, blocks - c * kChunkBlocks);
+            if (nb == kChunkBlocks) {
+#pragma unroll
+                for (int j0 = 0; j0 < kChunkBlocks; j0 += kGroup) block_group(srow, qrow, frow, j0, acc);
+            } else {
+                for (int j = 0; j < nb; ++j) block_mma(srow, qrow, frow, j, acc);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);                      // the trailing copies land before
+        __syncthreads();                                    // the next tile group reuses the buffers
+        // D reg r of lane (n, g): batch row 4g + r, weight row r0 + n
+        const int rr = r0 + nl;
+        if (tile < tiles && rr < n) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = 4 * g + r;
+                if (m < batch) y[static_cast<size_t>(m) * n + rr] = acc[r] * row_inv[m];
+            }
+        }
+    }
+}
+
+} // namespace
+
+extern "C" size_t kk_q4_mfma_gemv_workspace_bytes(int k) {
+    const int blocks_pad = ((k >> 5) + kChunkBlocks - 1) / kChunkBlocks * kChunkBlocks;
+    return static_cast<size_t>(blocks_pad) * kFragBlockBytes + 256;
+}
+
+extern "C" int kk_q4_mfma_gemv(const void *w, const float *x, float *y, int k, int n, int batch, void *workspace,
+                               int cus, hipStream_t stream) {
+    if (!w || !x || !y || !workspace || k <= 0 || (k & 63) || k > 16384 || n <= 0 || batch < 1 ||
+        batch > kBatchRows || cus <= 0 || (reinterpret_cast<uintptr_t>(w) & 3))
+        return hipErrorInvalidValue;
+    const int blocks_pad = ((k >> 5) + kChunkBlocks - 1) / kChunkBlocks * kChunkBlocks;
+    _Float16 *frag = static_cast<_Float16 *>(workspace);
+    float *row_inv = reinterpret_cast<float *>(static_cast<char *>(workspace) +
+                                               static_cast<size_t>(blocks_pad) * kFragBlockBytes);
+    hipLaunchKernelGGL(x_to_frag, dim3(kBatchRows), dim3(kPrepassThreads), 0, stream, x, batch, k, blocks_pad, frag,
+                       row_inv);
+    hipError_t rc = hipGetLastError();
+    if (rc != hipSuccess) return rc;
+    // dynamic LDS above 64 KiB is opted into once per device (callers hold the runtime lock)
+    constexpr int kMaxDevices = 64;
+    static bool configured[kMaxDevices] = {};
+    int device = 0;
+    rc = hipGetDevice(&device);
+    if (rc != hipSuccess) return rc;
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    if (!configured[device]) {
+        rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&q4_mfma_gemv),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+        if (rc != hipSuccess) return rc;
+        configured[device] = true;
+    }
+    const int tiles = (n + kTileRows - 1) / kTileRows;
+    const int groups = std::max(1, std::min((tiles + kWaves - 1) / kWaves, cus));
+    hipLaunchKernelGGL(q4_mfma_gemv, dim3(groups), dim3(kThreads), kLdsBytes, stream, static_cast<const uint8_t *>(w),
+                       frag, row_inv, y, k, n, batch, tiles);
+    return hipGetLastError();
+}

@@ -87,6 +87,8 @@ DeviceContext & context(int device) {
         const int zero = 0;
         check_hip(hipMemcpy(word, &zero, sizeof(zero), hipMemcpyHostToDevice), "hipMemcpy(status)");
         ctx.status = static_cast<int *>(word);
+        check_hip(hipDeviceGetAttribute(&ctx.cus, hipDeviceAttributeMultiprocessorCount, device),
+                  "hipDeviceGetAttribute(multiprocessors)");
         ctx.ready = true;
     }
     return ctx;

@@ -17,6 +17,7 @@ struct DeviceContext {
     hipStream_t stream = nullptr;
     int *status = nullptr;          // device word written by kernels on bad input
     bool status_pending = false;    // a submitted kernel may have written it
+    int cus = 0;                    // compute units of the device
 };
 
 std::recursive_mutex & mutex();

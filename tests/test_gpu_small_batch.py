@@ -1,0 +1,82 @@
+"""GPU parity of the single-pass small-batch Q4_0 GEMV (batch 2..16, fp16
+MFMA with hi/lo activations): BASELINE configs[2] shapes, K chunk tails, N
+tails, extreme and zero activation rows, against the FP64 gold of the exactly
+decoded weights (reference bench/library-bench.cpp:121-122) with the
+f32-accumulate bound |err| <= 1e-4 * ||x_b|| * ||w_r||.
+"""
+import numpy as np
+import pytest
+
+# The MFMA GEMV takes batch 5..16 by default; tests reach batch 2..4 through
+# KUNLUN_Q4_MFMA_MIN (read per call).
+
+import kunlunk200_lib_amd as kl
+from gpu_util import check_f32_accumulate, run_matmul
+
+pytestmark = pytest.mark.gpu
+
+
+def gaussian(shape, sigma, seed):
+    return (np.random.default_rng(seed).standard_normal(shape) * sigma).astype(np.float32)
+
+
+@pytest.fixture(autouse=True)
+def mfma_from_batch_two(monkeypatch):
+    monkeypatch.setenv("KUNLUN_Q4_MFMA_MIN", "2")
+
+
+def q4_case(oracle, k, n, batch, seed, x=None):
+    w = gaussian((n, k), 0.02, seed)
+    if x is None:
+        x = gaussian((batch, k), 1.0, seed + 1)
+    q4 = kl.quantize_q4_0(w)
+    dec = oracle.q4_decode(q4, k, n)
+    y, route, guard_ok = run_matmul(kl.WeightType.q4_0, q4, x, k, n, batch)
+    gold = oracle.gold(dec, x, threads=16)
+    res = check_f32_accumulate(y, gold, dec, x)
+    print(f"  q4 k={k} n={n} b={batch} route={route} {res}", flush=True)
+    return y, route, guard_ok, res
+
+
+@pytest.mark.parametrize("batch", [2, 4, 8, 16])
+def test_config2_shapes(gpu, oracle, batch):
+    y, route, guard_ok, res = q4_case(oracle, 4096, 14336, batch, 100 + batch)
+    assert route == "q4_mfma_gemv"
+    assert guard_ok and res["finite"] and res["north_star"] and res["reference"]
+
+
+@pytest.mark.parametrize("k,n,batch", [(64, 1, 2), (64, 17, 16), (4160, 33, 3), (11008, 4096, 4), (16384, 70, 16),
+                                       (1024, 16, 5), (2048, 1000, 9), (4096, 4096, 15)])
+def test_tails(gpu, oracle, k, n, batch):
+    y, route, guard_ok, res = q4_case(oracle, k, n, batch, k + n + batch)
+    assert route == "q4_mfma_gemv"
+    assert guard_ok and res["finite"] and res["north_star"] and res["reference"]
+
+
+def test_extreme_rows(gpu, oracle):
+    k, n, batch = 4096, 300, 6
+    x = gaussian((batch, k), 1.0, 77)
+    x[1] *= 1e6
+    x[2] *= 1e-30
+    x[3] = 0.0
+    x[4, ::7] *= 1000.0           # a row with a wide dynamic range
+    y, route, guard_ok, res = q4_case(oracle, k, n, batch, 78, x=x)
+    assert route == "q4_mfma_gemv"
+    assert guard_ok and res["finite"] and res["north_star"]
+    assert np.all(y[3] == 0.0)
+
+
+def test_matches_batch_one_kernel(gpu, oracle, monkeypatch):
+    # the same call with the MFMA GEMV disabled (pairs of dot8 columns)
+    k, n, batch = 4096, 1000, 8
+    w = gaussian((n, k), 0.02, 5)
+    x = gaussian((batch, k), 1.0, 6)
+    q4 = kl.quantize_q4_0(w)
+    y_mfma, r1, _ = run_matmul(kl.WeightType.q4_0, q4, x, k, n, batch)
+    monkeypatch.setenv("KUNLUN_Q4_MFMA_MIN", "17")
+    y_dot8, r2, _ = run_matmul(kl.WeightType.q4_0, q4, x, k, n, batch)
+    assert r1 == "q4_mfma_gemv" and r2 == "q4_gemv_dot8"
+    dec = oracle.q4_decode(q4, k, n)
+    xn = np.linalg.norm(x.astype(np.float64), axis=1)[:, None]
+    wn = np.linalg.norm(dec.astype(np.float64), axis=1)[None, :]
+    assert np.all(np.abs(y_mfma.astype(np.float64) - y_dot8) <= 2e-4 * xn * wn)
