@@ -39,6 +39,11 @@ size_t kk_q4_mfma_gemv_workspace_bytes(int k);
 int kk_q4_mfma_gemv(const void *w, const float *x, float *y, int k, int n, int batch, void *workspace, int cus,
                     hipStream_t stream);
 
+// F32 (type 0) / F16 (type 1) GEMV for batch 1..16 on fp32 MFMA, one pass over
+// W; 16-byte aligned weights and activations.
+int kk_dense_mfma_gemv(int type, const void *w, const float *x, float *y, int k, int n, int batch,
+                       hipStream_t stream);
+
 // Bytes of device workspace kk_i8_quantize needs for `count` activations.
 size_t kk_i8_workspace_bytes(int k, int batch);
 // Two-pass per-tensor INT8 quantization of X[batch,k] into `workspace`

@@ -53,6 +53,15 @@ bool q4_mfma_batch(int batch) {
     return batch >= min_b && batch <= max_b;
 }
 
+// Batch range of the single-pass F32/F16 MFMA GEMV (KUNLUN_DENSE_MFMA_MIN/MAX, within 1..16).
+bool dense_mfma_batch(int batch) {
+    const char * lo = std::getenv("KUNLUN_DENSE_MFMA_MIN");
+    const char * hi = std::getenv("KUNLUN_DENSE_MFMA_MAX");
+    const int min_b = std::max(1, lo && *lo ? std::atoi(lo) : 2);
+    const int max_b = std::min(16, hi && *hi ? std::atoi(hi) : 16);
+    return batch >= min_b && batch <= max_b;
+}
+
 // The reference's matmul argument rules (reference src/k200.cpp:271-275):
 // supported type, K % 32 == 0, K <= 16384, products that fit int, and a
 // weight matrix of at most INT_MAX bytes.
@@ -115,6 +124,12 @@ void matmul(Kernel & kernel, int id, void * y, const void * w, const void * x, i
         detail::check_hip((hipError_t)kk_gemm((int)type, w, static_cast<const float *>(x), static_cast<float *>(y), k,
                                               n, batch, impl.gemm_workspace, ctx.stream, &impl.route),
                           "kk_gemm");
+    } else if ((type == WeightType::f32 || type == WeightType::f16) && dense_mfma_batch(batch) &&
+               ((uintptr_t)w & 15) == 0 && ((uintptr_t)x & 15) == 0) {
+        detail::check_hip((hipError_t)kk_dense_mfma_gemv((int)type, w, static_cast<const float *>(x),
+                                                         static_cast<float *>(y), k, n, batch, ctx.stream),
+                          "kk_dense_mfma_gemv");
+        impl.route = type == WeightType::f16 ? "f16_mfma_gemv" : "f32_mfma_gemv";
     } else if (type == WeightType::q4_0 && q4_mfma_batch(batch) && k % 64 == 0 && ((uintptr_t)w & 3) == 0) {
         grow(id, ctx, impl.gemm_workspace, impl.gemm_workspace_size, kk_q4_mfma_gemv_workspace_bytes(k));
         detail::check_hip((hipError_t)kk_q4_mfma_gemv(w, static_cast<const float *>(x), static_cast<float *>(y), k, n,

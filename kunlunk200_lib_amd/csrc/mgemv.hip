@@ -352,3 +352,111 @@ extern "C" int kk_q4_mfma_gemv(const void *w, const float *x, float *y, int k, i
                        frag, row_inv, y, k, n, batch, tiles);
     return hipGetLastError();
 }
+
+// ---------------------------------------------------------------------------
+// Small-batch (1..16) F32 / F16 GEMV on fp32 MFMA (v_mfma_f32_16x16x4_f32):
+// exact F32 products (an F16 weight widens exactly), F32 accumulation, one
+// pass over the weights for the whole batch.
+//
+// Workgroup = one 16-row weight tile; its 8 waves take K eighths (32-value
+// steps, 4 in flight per wave) and meet in LDS at the end in wave order. Per step a lane
+// (n = lane % 16, g = lane / 16) loads 8 consecutive weights of row n and the
+// 8 activations of batch row n at k0 + 8g .. k0 + 8g + 7 with 16-byte loads;
+// MFMA t (0..7) of the step takes k0 + 8g + t from lane group g, so both
+// operands come straight from global memory in the MFMA layout (A[m][k] in
+// lane m + 16 k, B[k][n] in lane n + 16 k, D[4g + i][n] in lane n + 16 g).
+namespace {
+
+constexpr int kDenseWaves = 8;     // K split over the workgroup's waves (two per SIMD)
+constexpr int kDenseDepth = 4;     // 32-value steps of loads in flight per wave
+
+template <bool F16W>
+__global__ __launch_bounds__(kWave * kDenseWaves) void dense_mfma_gemv(const uint8_t *__restrict__ w,
+                                                                      const float *__restrict__ x,
+                                                                      float *__restrict__ y, int k, int n,
+                                                                      int batch) {
+    __shared__ float4v partial[kDenseWaves][kWave];
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int q = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nl = lane & 15, g = lane >> 4;
+    const int r = min(static_cast<int>(blockIdx.x) * 16 + nl, n - 1);
+    const bool live_m = nl < batch;
+    const float *xrow = x + static_cast<size_t>(min(nl, batch - 1)) * k + 8 * g;
+    const uint8_t *wrow = w + static_cast<size_t>(r) * k * (F16W ? 2 : 4) + 8 * g * (F16W ? 2 : 4);
+    const int steps = k >> 5;
+    const int s0 = steps * q / kDenseWaves, s1 = steps * (q + 1) / kDenseWaves;
+
+    // one step: 8 activations and 8 weights of this lane (a past-the-end step
+    // reloads the wave's last step; its MFMAs are skipped)
+    auto load = [&](int s, float (&a)[8], float (&b)[8]) {
+        s = min(s, max(s1 - 1, s0));
+        const float4 *xs = reinterpret_cast<const float4 *>(xrow + static_cast<size_t>(s) * 32);
+        const float4 x0 = xs[0], x1 = xs[1];
+        a[0] = x0.x; a[1] = x0.y; a[2] = x0.z; a[3] = x0.w; a[4] = x1.x; a[5] = x1.y; a[6] = x1.z; a[7] = x1.w;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) a[t] = live_m ? a[t] : 0.0f;
+        if constexpr (F16W) {
+            const half8 h = *reinterpret_cast<const half8 *>(wrow + static_cast<size_t>(s) * 64);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) b[t] = static_cast<float>(h[t]);
+        } else {
+            const float4 *ws = reinterpret_cast<const float4 *>(wrow + static_cast<size_t>(s) * 128);
+            const float4 w0 = ws[0], w1 = ws[1];
+            b[0] = w0.x; b[1] = w0.y; b[2] = w0.z; b[3] = w0.w; b[4] = w1.x; b[5] = w1.y; b[6] = w1.z; b[7] = w1.w;
+        }
+    };
+
+    float4v acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
+    float a[kDenseDepth][8], b[kDenseDepth][8];
+#pragma unroll
+    for (int d = 0; d < kDenseDepth; ++d) load(s0 + d, a[d], b[d]);
+    for (int s = s0; s < s1; s += kDenseDepth) {
+#pragma unroll
+        for (int d = 0; d < kDenseDepth; ++d) {
+            if (s + d < s1) {                               // uniform: every lane of the wave agrees
+                float ca[8], cb[8];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) { ca[t] = a[d][t]; cb[t] = b[d][t]; }
+                load(s + d + kDenseDepth, a[d], b[d]);
+#pragma unroll
+                for (int t = 0; t < 8; t += 2) {
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(ca[t], cb[t], acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(ca[t + 1], cb[t + 1], acc1, 0, 0, 0);
+                }
+            }
+        }
+    }
+    partial[q][lane] = acc0 + acc1;
+    __syncthreads();
+    if (q != 0) return;
+    float4v sum = partial[0][lane];
+#pragma unroll
+    for (int i = 1; i < kDenseWaves; ++i) sum += partial[i][lane];
+    // D reg i of lane (n, g): batch row 4g + i, weight row tile*16 + n
+    const int row = static_cast<int>(blockIdx.x) * 16 + nl;
+    if (row < n) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = 4 * g + i;
+            if (m < batch) y[static_cast<size_t>(m) * n + row] = sum[i];
+        }
+    }
+}
+
+} // namespace
+
+extern "C" int kk_dense_mfma_gemv(int type, const void *w, const float *x, float *y, int k, int n, int batch,
+                                  hipStream_t stream) {
+    if ((type != 0 && type != 1) || !w || !x || !y || k <= 0 || (k & 31) || n <= 0 || batch < 1 ||
+        batch > 16 || (reinterpret_cast<uintptr_t>(w) & 15) || (reinterpret_cast<uintptr_t>(x) & 15))
+        return hipErrorInvalidValue;
+    const int tiles = (n + 15) / 16;
+    if (type == 1)
+        hipLaunchKernelGGL(dense_mfma_gemv<true>, dim3(tiles), dim3(kWave * kDenseWaves), 0, stream,
+                           static_cast<const uint8_t *>(w), x, y, k, n, batch);
+    else
+        hipLaunchKernelGGL(dense_mfma_gemv<false>, dim3(tiles), dim3(kWave * kDenseWaves), 0, stream,
+                           static_cast<const uint8_t *>(w), x, y, k, n, batch);
+    return hipGetLastError();
+}

@@ -80,3 +80,39 @@ def test_matches_batch_one_kernel(gpu, oracle, monkeypatch):
     xn = np.linalg.norm(x.astype(np.float64), axis=1)[:, None]
     wn = np.linalg.norm(dec.astype(np.float64), axis=1)[None, :]
     assert np.all(np.abs(y_mfma.astype(np.float64) - y_dot8) <= 2e-4 * xn * wn)
+
+
+# ---------------------------------------------------------------------------
+# F16 / F32 weights, batch 2..16: the fp32-MFMA single-pass GEMV
+
+def dense_case(oracle, type_, k, n, batch, seed):
+    from gpu_util import weight_payload
+    w = gaussian((n, k), 0.02, seed)
+    x = gaussian((batch, k), 1.0, seed + 1)
+    payload, dec = weight_payload(type_, w, oracle)
+    y, route, guard_ok = run_matmul(type_, payload, x, k, n, batch)
+    gold = oracle.gold(dec, x, threads=16)
+    res = check_f32_accumulate(y, gold, dec, x)
+    print(f"  {int(type_)} k={k} n={n} b={batch} route={route} {res}", flush=True)
+    return y, route, guard_ok, res, payload, x
+
+
+@pytest.mark.parametrize("type_", [kl.WeightType.f16, kl.WeightType.f32], ids=["f16", "f32"])
+@pytest.mark.parametrize("k,n,batch", [(4096, 4096, 8), (4096, 4096, 2), (4096, 1000, 16), (32, 17, 3),
+                                       (16384, 40, 5), (11008, 300, 12), (96, 1, 16)])
+def test_dense_mfma(gpu, oracle, type_, k, n, batch):
+    _, route, guard_ok, res, _, _ = dense_case(oracle, type_, k, n, batch, k + 5 * n + batch)
+    assert route == ("f16_mfma_gemv" if type_ == kl.WeightType.f16 else "f32_mfma_gemv")
+    assert guard_ok and res["finite"] and res["north_star"] and res["reference"]
+
+
+def test_dense_mfma_matches_vector_kernel(gpu, oracle, monkeypatch):
+    for type_ in (kl.WeightType.f16, kl.WeightType.f32):
+        y1, r1, _, _, payload, x = dense_case(oracle, type_, 2048, 700, 8, 41)
+        monkeypatch.setenv("KUNLUN_DENSE_MFMA_MIN", "17")
+        y2, r2, _ = run_matmul(type_, payload, x, 2048, 700, 8)
+        monkeypatch.delenv("KUNLUN_DENSE_MFMA_MIN")
+        assert r1.endswith("mfma_gemv") and not r2.endswith("mfma_gemv")
+        # both accumulate exact products in F32, in different orders
+        scale = np.abs(y2).max()
+        assert np.max(np.abs(y1 - y2)) <= 1e-5 * scale
