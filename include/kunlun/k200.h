@@ -2,10 +2,10 @@
 //
 // This header keeps the declarations, argument meaning, defaults and class
 // layouts of the matmul subset of the reference library's public header
-// (reference include/kunlun/k200.h:10-37, 40, 62-105, 132, 185-199, 345-350)
+// (reference include/kunlun/k200.h:10-37, 40-41, 62-107, 132, 185-199, 345-350)
 // so a consumer of that subset rebuilds against this library unchanged.
 // Declarations of the reference that are not on the matmul path (attention,
-// Q6_K, native and common Q4 layouts, elementwise, KV caches) are not
+// Q6_K, native and common Q4 layouts, KV caches) are not
 // declared here. matmul_swiglu has no reference counterpart (see below).
 //
 // Device numbering: the reference drives the two processing dies of one
@@ -62,6 +62,8 @@ private:
 // Values match the reference enumeration (reference k200.h:40). q6_k is not
 // accepted by matmul, as in the reference.
 enum class WeightType { f32 = 0, f16 = 1, q4_0 = 2, rowwise_i8 = 3, q6_k = 4 };
+// Elementwise operations (reference k200.h:41).
+enum class ElementwiseOp { add = 0, multiply = 1, silu = 2, rms_norm = 3, scale = 4 };
 
 struct SwiGLULayout;
 
@@ -82,6 +84,8 @@ private:
                        const SwiGLULayout &);
     friend void matmul_swiglu(Kernel &, int, void *, const void *, const void *, const void *, int, int, int,
                               WeightType);
+    friend void elementwise(Kernel &, int, void *, const void *, const void *, int, int, int, ElementwiseOp,
+                            float);
 };
 
 // Packed rowwise INT8 weight layout (reference k200.h:90-96):
@@ -135,6 +139,15 @@ bool swiglu(Kernel &, int device, void * y, size_t y_bytes,
 // two GEMVs and the SwiGLU kernel. Submits; select + wait completes it.
 void matmul_swiglu(Kernel &, int device, void * y, const void * w_gate, const void * w_up, const void * x,
                    int k, int n, int batch, WeightType type);
+
+// F32 elementwise op over `count` values, completed before returning
+// (reference k200.h:106-107): add and multiply take b of b_count == count
+// values or of b_count == width values repeated every row; silu, scale
+// (a * parameter) and rms_norm (each `width` row scaled by
+// 1 / sqrt(mean(a^2) + parameter)) ignore b. count % width == 0,
+// width <= 16384; y may equal a or b.
+void elementwise(Kernel &, int device, void * y, const void * a, const void * b,
+                 int count, int width, int b_count, ElementwiseOp op, float parameter = 0);
 
 // Same layout as the reference (reference k200.h:345-350): matmul submissions
 // on devices 0 and 1, peer copy count and bytes.

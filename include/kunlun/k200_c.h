@@ -74,6 +74,13 @@ void kunlun_matmul(kunlun_kernel *kernel, int device, void *y, const void *w, co
                    int k, int n, int batch, int type,
                    const float *scales, const float *maxima, int tile);
 
+/* Elementwise ops, same values as kunlun::ElementwiseOp (reference include/kunlun/k200.h:41). */
+enum { KUNLUN_EW_ADD = 0, KUNLUN_EW_MULTIPLY = 1, KUNLUN_EW_SILU = 2, KUNLUN_EW_RMS_NORM = 3, KUNLUN_EW_SCALE = 4 };
+/* elementwise() (reference include/kunlun/k200.h:106-107): F32 op over count
+ * values, completed before returning; invalid arguments abort. */
+void kunlun_elementwise(kunlun_kernel *kernel, int device, void *y, const void *a, const void *b, int count,
+                        int width, int b_count, int op, float parameter);
+
 /* Element types of SwiGLU, same values as kunlun::InputType (reference include/kunlun/k200.h:132). */
 enum { KUNLUN_INPUT_F32 = 0, KUNLUN_INPUT_F16 = 1 };
 /* swiglu_reason() (reference include/kunlun/k200.h:192) on the SwiGLULayout

@@ -62,6 +62,8 @@ C_FUNCTIONS = [
     ("kunlun_matmul_count", _c_size, [_c_int]),
     ("kunlun_stream", _c_void_p, [_c_int]),
     ("kunlun_kernel_route", ctypes.c_char_p, [_c_void_p]),
+    ("kunlun_elementwise", None, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
+                                  _c_int, ctypes.c_float]),
     ("kunlun_swiglu_reason", ctypes.c_char_p, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     ("kunlun_swiglu", _c_int, [_c_void_p, _c_int, _c_void_p, _c_size, _c_void_p, _c_size, _c_void_p, _c_size,
                                _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
@@ -274,6 +276,22 @@ def matmul(kernel: Kernel, device: int, y, w, x, k: int, n: int, batch: int, typ
     """
     load().kunlun_matmul(kernel.handle, int(device), _ptr(y), _ptr(w), _ptr(x), int(k), int(n), int(batch),
                          int(type), _ptr(scales), _ptr(maxima), int(tile))
+
+
+class ElementwiseOp(enum.IntEnum):
+    """reference k200.h:41"""
+    add = 0
+    multiply = 1
+    silu = 2
+    rms_norm = 3
+    scale = 4
+
+
+def elementwise(kernel: Kernel, device: int, y, a, b, count: int, width: int, b_count: int, op: ElementwiseOp,
+                parameter: float = 0.0) -> None:
+    """F32 elementwise op, completed before returning (reference k200.h:106-107)."""
+    load().kunlun_elementwise(kernel.handle, int(device), _ptr(y), _ptr(a), _ptr(b), int(count), int(width),
+                              int(b_count), int(op), float(parameter))
 
 
 class InputType(enum.IntEnum):

@@ -63,6 +63,14 @@ void kunlun_statistics(size_t out[4]) {
 }
 const char * kunlun_version(void) { return kunlun::version(); }
 
+void kunlun_elementwise(kunlun_kernel * kernel, int device, void * y, const void * a, const void * b, int count,
+                        int width, int b_count, int op, float parameter) {
+    kunlun::require(kernel != nullptr);
+    kunlun::elementwise(kernel->kernel, device, y, a, b, count, width, b_count, static_cast<kunlun::ElementwiseOp>(op),
+                        parameter);
+    kernel->route = kunlun::detail::route_of_last_matmul();
+}
+
 const char * kunlun_swiglu_reason(int width, int rows, int gate_stride, int up_stride, int output_stride, int type) {
     const kunlun::SwiGLULayout layout{width, rows, gate_stride, up_stride, output_stride,
                                       static_cast<kunlun::InputType>(type)};

@@ -44,6 +44,12 @@ int kk_q4_mfma_gemv(const void *w, const float *x, float *y, int k, int n, int b
 int kk_dense_mfma_gemv(int type, const void *w, const float *x, float *y, int k, int n, int batch,
                        hipStream_t stream);
 
+// Elementwise F32 op over `count` values: 0 add, 1 multiply (b of b_count
+// values repeated), 2 silu, 3 rms_norm of each `width` row (eps =
+// parameter), 4 scale by parameter.
+int kk_elementwise(float *y, const float *a, const float *b, int count, int width, int b_count, int op,
+                   float parameter, hipStream_t stream);
+
 // Bytes of device workspace kk_i8_quantize needs for `count` activations.
 size_t kk_i8_workspace_bytes(int k, int batch);
 // Two-pass per-tensor INT8 quantization of X[batch,k] into `workspace`

@@ -42,7 +42,7 @@ struct Kernel::Impl {
     size_t i8_workspace_size = 0;
     void * gemm_workspace = nullptr;    // fp16 activations of the prefill GEMM
     size_t gemm_workspace_size = 0;
-    void * pair_workspace = nullptr;    // gate and up GEMV outputs of matmul_swiglu
+    void * pair_workspace = nullptr;    // gate/up GEMV outputs of matmul_swiglu; elementwise copy of b
     size_t pair_workspace_size = 0;
     const char * route = nullptr;
 };

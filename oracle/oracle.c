@@ -452,3 +452,37 @@ void orc_swiglu(const void *gate, const void *up, void *y, int width, int rows, 
         }
     }
 }
+
+/* Elementwise F32 op over n values (reference kernels/kunlun-elementwise.xpu
+ * and src/k200.cpp:280-323): 0 add and 1 multiply with b[e % bn], 2 silu
+ * a / (1 + expf(-a)), 4 scale a * parameter, 3 rms_norm of each `width` row:
+ * sum of squares accumulated in F32 in element order, then
+ * a * (1 / sqrtf(sum / width + parameter)). y may equal a or b: every input
+ * an output depends on is read before it is written (rms_norm reads its row
+ * twice, and the second read of element j precedes the write of element j). */
+void orc_elementwise(float *y, const float *a, const float *b, int n, int width, int bn, int op, float parameter) {
+    if (op == 3) {
+        for (int r = 0; r < n / width; ++r) {
+            const float *row = a + (size_t)r * width;
+            float *out = y + (size_t)r * width;
+            float sum = 0.0f;
+            for (int j = 0; j < width; ++j) sum += row[j] * row[j];
+            float scale = 1.0f / sqrtf(sum / (float)width + parameter);
+            for (int j = 0; j < width; ++j) out[j] = row[j] * scale;
+        }
+        return;
+    }
+    for (int e = 0; e < n; ++e) {
+        float v = a[e], out;
+        if (op == 0) {
+            out = v + b[e % bn];
+        } else if (op == 1) {
+            out = v * b[e % bn];
+        } else if (op == 2) {
+            out = v / (1.0f + expf(-v));
+        } else {
+            out = v * parameter;
+        }
+        y[e] = out;
+    }
+}

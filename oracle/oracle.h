@@ -33,6 +33,12 @@
  *   orc_swiglu             - strided rows, F16 rounding and aliasing against
  *                            an element-by-element numpy loop over
  *                            orc_swiglu_value.
+ *   orc_elementwise        - add, multiply and scale bit-exact against numpy
+ *                            F32 with b tiled; silu within a few ulp of the
+ *                            FP64 closed form; rms_norm within 1e-6 relative
+ *                            of the FP64 closed form, constant rows exactly
+ *                            (c / |c| = sign), and the reference
+ *                            library-bench gold (max_abs < 1e-4).
  */
 #ifndef KUNLUN_ORACLE_H
 #define KUNLUN_ORACLE_H
@@ -77,6 +83,7 @@ void orc_i8_combine(const int64_t *primary, const int64_t *residual, const float
 float orc_swiglu_value(float g, float u);
 void orc_swiglu(const void *gate, const void *up, void *y, int width, int rows, int gate_stride,
                 int up_stride, int output_stride, int bytes);
+void orc_elementwise(float *y, const float *a, const float *b, int n, int width, int bn, int op, float parameter);
 
 #ifdef __cplusplus
 }

@@ -51,6 +51,7 @@ class Oracle:
             "orc_i8_combine": (None, [P, P, P, ctypes.c_float, ctypes.c_float, I, I, P]),
             "orc_swiglu_value": (ctypes.c_float, [ctypes.c_float, ctypes.c_float]),
             "orc_swiglu": (None, [P, P, P, I, I, I, I, I, I]),
+            "orc_elementwise": (None, [P, P, P, I, I, I, I, ctypes.c_float]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -198,6 +199,17 @@ class Oracle:
         y = np.empty_like(g)
         gb, ub, yb = (a.view(np.uint8).reshape(-1) for a in (g, u, y))
         self.swiglu_bytes(gb, ub, yb, width, rows, width * bytes_, width * bytes_, width * bytes_, bytes_)
+        return y
+
+    def elementwise(self, a: np.ndarray, b: np.ndarray, width: int, op: int, parameter: float = 0.0,
+                    out: np.ndarray | None = None) -> np.ndarray:
+        """orc_elementwise over F32 a (n values) and b (n or width values);
+        out may be a itself (aliasing)."""
+        a = np.ascontiguousarray(a, dtype=np.float32).ravel()
+        b = np.ascontiguousarray(b, dtype=np.float32).ravel()
+        y = np.empty_like(a) if out is None else out
+        assert y.dtype == np.float32 and y.flags.c_contiguous and y.size == a.size
+        self.lib.orc_elementwise(_p(y), _p(a), _p(b), a.size, int(width), b.size, int(op), float(parameter))
         return y
 
     def rowwise_i8_matmul(self, w: np.ndarray, x: np.ndarray) -> np.ndarray:

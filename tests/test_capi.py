@@ -132,6 +132,7 @@ def test_matmul_contract_aborts(case):
     assert "NOT REJECTED" not in proc.stdout
     assert proc.returncode == -signal.SIGABRT, proc.stderr
     assert "invalid argument" in proc.stderr
+    assert "device=-1" in proc.stderr, "rejected only after selecting a device"
 
 
 def test_upload_i8_rows_contract_aborts():
@@ -206,3 +207,52 @@ def test_swiglu_contract_rejects_before_device(kl, case):
     assert kl.swiglu(kernel, device, y, yb, g, gb, u, ub, layout) is False
     assert kl.allocated_bytes(0) == before
     assert kernel.route is None
+
+
+# ---------------------------------------------------------------------------
+# elementwise argument rules (reference src/k200.cpp:283-286). Each call aborts
+# before selecting a device; pointers are fake and never dereferenced.
+EW_BAD_CALLS = {
+    "null_y": "y=0",
+    "null_a": "a=0",
+    "null_b": "b=0",
+    "count_zero": "count=0, width=1, b_count=1",
+    "count_above_int_max_over_4": "count=(2 ** 31 - 1) // 4 + 1, width=1, b_count=1",
+    "width_zero": "width=0",
+    "width_above_16384": "count=16385 * 2, width=16385, b_count=16385",
+    "count_not_multiple_of_width": "count=1000, width=256, b_count=256",
+    "op_5": "op=5",
+    "op_negative": "op=-1",
+    "b_count_other": "b_count=100",
+    "rms_eps_zero": "op=3, parameter=0.0",
+    "rms_eps_negative": "op=3, parameter=-1e-5",
+    "rms_eps_nan": "op=3, parameter=float('nan')",
+    "rms_eps_inf": "op=3, parameter=float('inf')",
+    "misaligned_y": "y=8192 + 2",
+}
+
+
+@pytest.mark.parametrize("case", sorted(EW_BAD_CALLS))
+def test_elementwise_contract_aborts(case):
+    args = dict(y="8192", a="4096", b="12288", count="1024", width="256", b_count="256", op="0",
+                parameter="1e-5")
+    for part in EW_BAD_CALLS[case].split(", "):
+        key, value = part.split("=", 1)
+        args[key.strip()] = value
+    code = (
+        "import kunlunk200_lib_amd as kl\n"
+        "kern = kl.Kernel()\n"
+        f"kl.elementwise(kern, 0, {args['y']}, {args['a']}, {args['b']}, {args['count']}, {args['width']}, "
+        f"{args['b_count']}, {args['op']}, {args['parameter']})\n"
+        "print('NOT REJECTED')\n"
+    )
+    env = dict(os.environ, PYTHONPATH=ROOT, HIP_VISIBLE_DEVICES="")
+    proc = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=120)
+    assert "NOT REJECTED" not in proc.stdout
+    assert proc.returncode == -signal.SIGABRT, proc.stderr
+    assert "invalid argument" in proc.stderr
+    assert "device=-1" in proc.stderr, "rejected only after selecting a device"
+
+
+def test_elementwise_op_values(kl):
+    assert [int(o) for o in kl.ElementwiseOp] == [0, 1, 2, 3, 4]

@@ -320,3 +320,85 @@ def test_swiglu_rows_strides_f16_and_alias(oracle):
         for r in range(rows):
             assert np.array_equal(alias[r * stride:r * stride + width * bytes_],
                                   y[r * stride:r * stride + width * bytes_])
+
+
+# ---------------------------------------------------------------------------
+# Elementwise (reference kernels/kunlun-elementwise.xpu, src/k200.cpp:280-323)
+
+def _library_bench_data(k: int, batch: int):
+    """Inputs of the reference bench/library-bench.cpp:51-53."""
+    count = k * batch
+    a = np.sin(np.arange(count, dtype=np.float32) * np.float32(0.021)).astype(np.float32)
+    b = np.cos(np.arange(k, dtype=np.float32) * np.float32(0.04)).astype(np.float32)
+    return a, b
+
+
+def _library_bench_gold(a, b, k, batch, op, parameter):
+    """The reference's gold (bench/library-bench.cpp:62-67): FP64 row sums."""
+    rows = a.reshape(batch, k).astype(np.float64)
+    if op == 0:
+        return (rows + b).ravel()
+    if op == 1:
+        return (rows * b).ravel()
+    if op == 2:
+        return (rows / (1 + np.exp(-rows))).ravel()
+    if op == 4:
+        return (rows * parameter).ravel()
+    sums = (rows * rows).sum(axis=1, keepdims=True)
+    return (rows / np.sqrt(sums / k + parameter)).ravel()
+
+
+@pytest.mark.parametrize("op", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("k,batch", [(256, 4), (4096, 1), (32, 32)])
+def test_elementwise_library_bench_gold(oracle, op, k, batch):
+    a, b = _library_bench_data(k, batch)
+    parameter = 0.75 if op == 4 else 1e-5
+    y = oracle.elementwise(a, b, k, op, parameter)
+    assert np.all(np.isfinite(y))
+    assert np.max(np.abs(y - _library_bench_gold(a, b, k, batch, op, parameter))) < 1e-4
+
+
+def test_elementwise_add_multiply_scale_exact(oracle):
+    rng = np.random.default_rng(5)
+    width, rows = 96, 7
+    a = rng.standard_normal(width * rows).astype(np.float32) * 100
+    full = rng.standard_normal(width * rows).astype(np.float32)
+    row = rng.standard_normal(width).astype(np.float32)
+    assert np.array_equal(oracle.elementwise(a, full, width, 0), a + full)
+    assert np.array_equal(oracle.elementwise(a, row, width, 0), a + np.tile(row, rows))
+    assert np.array_equal(oracle.elementwise(a, row, width, 1), a * np.tile(row, rows))
+    assert np.array_equal(oracle.elementwise(a, full, width, 1), a * full)
+    assert np.array_equal(oracle.elementwise(a, row, width, 4, -0.375), a * np.float32(-0.375))
+
+
+def test_elementwise_silu_closed_form(oracle):
+    v = np.concatenate([np.linspace(-80, 80, 4001), [0.0, -0.0, 1e-30, -1e-30, 87.0, -87.0]]).astype(np.float32)
+    y = oracle.elementwise(v, v, v.size, 2)
+    exact = v.astype(np.float64) / (1 + np.exp(-v.astype(np.float64)))
+    ulp = np.spacing(np.abs(exact).astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(y - exact) <= 4 * ulp)
+    assert y[v.size - 6] == 0.0
+    # a << 0: expf(-a) overflows to inf and a / inf is -0
+    assert oracle.elementwise(np.float32([-100.0]), np.float32([0]), 1, 2)[0] == 0.0
+
+
+def test_elementwise_rms_norm_closed_form_and_alias(oracle):
+    rng = np.random.default_rng(11)
+    width, rows = 1000, 5
+    a = (rng.standard_normal(width * rows) * rng.uniform(0.01, 50, width * rows)).astype(np.float32)
+    eps = 1e-5
+    y = oracle.elementwise(a, a, width, 3, eps)
+    r = a.reshape(rows, width).astype(np.float64)
+    exact = r / np.sqrt((r * r).mean(axis=1, keepdims=True) + eps)
+    assert np.max(np.abs(y.reshape(rows, width) - exact) / np.max(np.abs(exact))) < 1e-6
+    # constant row c: y = c / sqrt(c^2 + eps) -> sign(c) for eps << c^2
+    const = np.full(64, -3.0, np.float32)
+    yc = oracle.elementwise(const, const, 64, 3, 1e-30)
+    assert np.all(np.abs(yc + 1) <= 2 ** -22)
+    # output aliasing the input gives the same values
+    alias = a.copy()
+    oracle.elementwise(alias, alias, width, 3, eps, out=alias)
+    assert np.array_equal(alias, y)
+    # a dropped eps would fail: a zero row stays zero only with eps > 0
+    z = oracle.elementwise(np.zeros(32, np.float32), np.zeros(1, np.float32), 32, 3, 1e-5)
+    assert np.array_equal(z, np.zeros(32, np.float32))
