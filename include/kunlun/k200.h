@@ -2,10 +2,10 @@
 //
 // This header keeps the declarations, argument meaning, defaults and class
 // layouts of the matmul subset of the reference library's public header
-// (reference include/kunlun/k200.h:10-37, 40-41, 62-107, 132, 185-199, 345-350)
+// (reference include/kunlun/k200.h:10-37, 40-41, 62-107, 127-132, 185-224, 345-350)
 // so a consumer of that subset rebuilds against this library unchanged.
 // Declarations of the reference that are not on the matmul path (attention,
-// Q6_K, native and common Q4 layouts, KV caches) are not
+// Q6_K, the common Q4 ABI, KV caches) are not
 // declared here. matmul_swiglu has no reference counterpart (see below).
 //
 // Device numbering: the reference drives the two processing dies of one
@@ -148,6 +148,55 @@ void matmul_swiglu(Kernel &, int device, void * y, const void * w_gate, const vo
 // width <= 16384; y may equal a or b.
 void elementwise(Kernel &, int device, void * y, const void * a, const void * b,
                  int count, int width, int b_count, ElementwiseOp op, float parameter = 0);
+
+// Native Q4 layout (reference k200.h:127-131): the Q4_0 values and FP16
+// block scales of an [n,k] matrix repacked as [N32 tile][K32 block][16 K
+// pairs][32 rows] signed 4-bit values, then the scales [N32 tile][K32
+// block][32 rows]; N is padded to 32 with zeros. Supported for
+// 0 < k <= 16384, k % 32 == 0, 0 < n <= 90000000 / k.
+bool native_q4_layout_supported(int k, int n);
+// Bytes of the layout, 0 when unsupported.
+size_t native_q4_size(int k, int n);
+// Host repack of n rows of Q4_0 blocks into `destination` (bytes >=
+// native_q4_size); false for an unsupported shape, a short or null buffer or
+// overlapping ranges.
+bool pack_native_q4(void * destination, size_t bytes, const void * q4, int k, int n);
+// Packs on the host and copies to device memory `weights`; completes before
+// returning. Invalid arguments abort.
+void upload_native_q4(int device, void * weights, const void * q4, int k, int n);
+
+// Empty string when the reference would take its accelerated route for this
+// shape, otherwise the reference's reason (reference k200.h:200-203).
+const char * native_q4_reason(int k, int n, int batch, InputType type);
+// Reference k200.h:204-207. Here every call runs the same exact kernels, and
+// no HBM or L3 workspace is held (both sizes are 0).
+struct NativeQ4Statistics {
+    size_t accelerated, fallback;
+    size_t hbm_workspace_bytes, l3_workspace_bytes;
+};
+class NativeQ4Workspace {                            // reference k200.h:208-219
+public:
+    NativeQ4Workspace();
+    ~NativeQ4Workspace();
+    NativeQ4Workspace(const NativeQ4Workspace &) = delete;
+    NativeQ4Workspace & operator=(const NativeQ4Workspace &) = delete;
+    NativeQ4Statistics statistics() const;
+    struct Impl;
+private:
+    Impl * impl_;
+    friend bool native_q4_matmul(NativeQ4Workspace &, int, void *, const void *, const void *, int, int, int,
+                                 InputType);
+};
+// Y[batch,n] = X[batch,k] W^T for W in the native layout (256-byte aligned),
+// X F32 or F16, Y F32; completes before returning (reference k200.h:220-224).
+// The result is exact up to a 23-bit fixed-point view of each 32-value
+// activation block, on every route. Returns true where the reference returns
+// true (native_q4_reason is empty and y and input are 64-byte aligned) and
+// counts the call as accelerated, else false and counts a fallback. The
+// workspace binds to the first device it is used on; invalid arguments or
+// overlapping ranges abort.
+bool native_q4_matmul(NativeQ4Workspace &, int device, void * y, const void * weights,
+                      const void * input, int k, int n, int batch = 1, InputType type = InputType::f32);
 
 // Same layout as the reference (reference k200.h:345-350): matmul submissions
 // on devices 0 and 1, peer copy count and bytes.

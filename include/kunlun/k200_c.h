@@ -23,6 +23,8 @@ extern "C" {
 
 /* Opaque handle that owns one kunlun::Kernel (reference include/kunlun/k200.h:62-88). */
 typedef struct kunlun_kernel kunlun_kernel;
+/* Opaque handle that owns one kunlun::NativeQ4Workspace (reference include/kunlun/k200.h:208-219). */
+typedef struct kunlun_native_q4_workspace kunlun_native_q4_workspace;
 
 /* Copy directions, same values as kunlun::CopyKind (reference include/kunlun/k200.h:18). */
 enum { KUNLUN_HOST_TO_DEVICE = 0, KUNLUN_DEVICE_TO_HOST = 1, KUNLUN_DEVICE_TO_DEVICE = 2 };
@@ -94,6 +96,26 @@ const char *kunlun_swiglu_reason(int width, int rows, int gate_stride, int up_st
 int kunlun_swiglu(kunlun_kernel *kernel, int device, void *y, size_t y_bytes, const void *gate,
                   size_t gate_bytes, const void *up, size_t up_bytes, int width, int rows,
                   int gate_stride, int up_stride, int output_stride, int type);
+
+/* Native Q4 layout (reference include/kunlun/k200.h:127-131): 1/0 for
+ * native_q4_layout_supported, bytes of the layout (0 when unsupported), host
+ * repack (1 on success, 0 for a bad shape, short buffer or overlap), and
+ * pack + upload completed before returning (invalid arguments abort). */
+int kunlun_native_q4_layout_supported(int k, int n);
+size_t kunlun_native_q4_size(int k, int n);
+int kunlun_pack_native_q4(void *destination, size_t bytes, const void *q4, int k, int n);
+void kunlun_upload_native_q4(int device, void *weights, const void *q4, int k, int n);
+/* native_q4_reason() (reference include/kunlun/k200.h:203); type is a KUNLUN_INPUT_* value. */
+const char *kunlun_native_q4_reason(int k, int n, int batch, int type);
+kunlun_native_q4_workspace *kunlun_native_q4_workspace_create(void);
+void kunlun_native_q4_workspace_destroy(kunlun_native_q4_workspace *workspace);
+/* NativeQ4Workspace::statistics(): out = {accelerated, fallback,
+ * hbm_workspace_bytes, l3_workspace_bytes}. */
+void kunlun_native_q4_statistics(const kunlun_native_q4_workspace *workspace, size_t out[4]);
+/* native_q4_matmul() (reference include/kunlun/k200.h:223-224): completes
+ * before returning; 1 where the reference takes its accelerated route, else 0. */
+int kunlun_native_q4_matmul(kunlun_native_q4_workspace *workspace, int device, void *y, const void *weights,
+                            const void *input, int k, int n, int batch, int type);
 
 /* statistics() (reference include/kunlun/k200.h:345-349) as four counters:
  * out[0..1] = matmul submissions on devices 0 and 1, out[2] = peer copies,

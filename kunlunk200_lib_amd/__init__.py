@@ -69,6 +69,16 @@ C_FUNCTIONS = [
                                _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     ("kunlun_matmul_swiglu", None, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int,
                                     _c_int, _c_int]),
+    ("kunlun_native_q4_layout_supported", _c_int, [_c_int, _c_int]),
+    ("kunlun_native_q4_size", _c_size, [_c_int, _c_int]),
+    ("kunlun_pack_native_q4", _c_int, [_c_void_p, _c_size, _c_void_p, _c_int, _c_int]),
+    ("kunlun_upload_native_q4", None, [_c_int, _c_void_p, _c_void_p, _c_int, _c_int]),
+    ("kunlun_native_q4_reason", ctypes.c_char_p, [_c_int, _c_int, _c_int, _c_int]),
+    ("kunlun_native_q4_workspace_create", _c_void_p, []),
+    ("kunlun_native_q4_workspace_destroy", None, [_c_void_p]),
+    ("kunlun_native_q4_statistics", None, [_c_void_p, ctypes.POINTER(_c_size)]),
+    ("kunlun_native_q4_matmul", _c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
+                                         _c_int]),
 ]
 
 
@@ -334,6 +344,78 @@ def matmul_swiglu(kernel: Kernel, device: int, y, w_gate, w_up, x, k: int, n: in
     the reference runs two matmul calls and swiglu)."""
     load().kunlun_matmul_swiglu(kernel.handle, int(device), _ptr(y), _ptr(w_gate), _ptr(w_up), _ptr(x), int(k),
                                 int(n), int(batch), int(type))
+
+
+def native_q4_layout_supported(k: int, n: int) -> bool:
+    """reference k200.h:128"""
+    return bool(load().kunlun_native_q4_layout_supported(int(k), int(n)))
+
+
+def native_q4_size(k: int, n: int) -> int:
+    """Bytes of the native Q4 layout, 0 when unsupported (reference k200.h:129)."""
+    return load().kunlun_native_q4_size(int(k), int(n))
+
+
+def pack_native_q4(destination, nbytes: int, q4, k: int, n: int) -> bool:
+    """Host repack of Q4_0 rows into the native layout (reference k200.h:130).
+    destination and q4 are host arrays or addresses."""
+    return bool(load().kunlun_pack_native_q4(_ptr(destination), int(nbytes), _ptr(q4), int(k), int(n)))
+
+
+def pack_native_q4_array(q4: np.ndarray, k: int, n: int) -> np.ndarray:
+    """pack_native_q4 into a new uint8 array of native_q4_size(k, n) bytes."""
+    q4 = np.ascontiguousarray(q4, dtype=np.uint8)
+    if q4.size < n * (k // 32) * 18:
+        raise ValueError("pack_native_q4_array: fewer than n rows of Q4_0 blocks")
+    out = np.empty(native_q4_size(k, n), np.uint8)
+    require(out.size > 0 and pack_native_q4(out, out.size, q4, k, n))
+    return out
+
+
+def upload_native_q4(device: int, weights, q4: np.ndarray, k: int, n: int) -> None:
+    """Pack on the host and copy to device memory; completes before returning (reference k200.h:131)."""
+    q4 = np.ascontiguousarray(q4, dtype=np.uint8)
+    if q4.size < n * (k // 32) * 18:
+        raise ValueError("upload_native_q4: fewer than n rows of Q4_0 blocks")
+    load().kunlun_upload_native_q4(int(device), _ptr(weights), q4.ctypes.data, int(k), int(n))
+
+
+def native_q4_reason(k: int, n: int, batch: int, type: InputType = InputType.f32) -> str:
+    """"" when the reference takes its accelerated route (reference k200.h:203)."""
+    return load().kunlun_native_q4_reason(int(k), int(n), int(batch), int(type)).decode()
+
+
+class NativeQ4Workspace:
+    """Per-call state owner for native_q4_matmul, bound to one device (reference k200.h:208-219)."""
+
+    def __init__(self):
+        self.handle = load().kunlun_native_q4_workspace_create()
+        require(bool(self.handle))
+
+    def close(self) -> None:
+        if self.handle:
+            load().kunlun_native_q4_workspace_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def statistics(self) -> dict:
+        out = (_c_size * 4)()
+        load().kunlun_native_q4_statistics(self.handle, out)
+        return {"accelerated": out[0], "fallback": out[1], "hbm_workspace_bytes": out[2],
+                "l3_workspace_bytes": out[3]}
+
+
+def native_q4_matmul(workspace: NativeQ4Workspace, device: int, y, weights, x, k: int, n: int, batch: int = 1,
+                     type: InputType = InputType.f32) -> bool:
+    """Y[batch,n] = X W^T over the native layout, completed before returning;
+    True where the reference takes its accelerated route (reference k200.h:223-224)."""
+    return bool(load().kunlun_native_q4_matmul(workspace.handle, int(device), _ptr(y), _ptr(weights), _ptr(x),
+                                               int(k), int(n), int(batch), int(type)))
 
 
 def statistics() -> dict:

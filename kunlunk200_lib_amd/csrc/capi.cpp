@@ -9,6 +9,17 @@ struct kunlun_kernel {
     const char * route = nullptr;
 };
 
+struct kunlun_native_q4_workspace {
+    kunlun::NativeQ4Workspace workspace;
+};
+
+namespace {
+kunlun::InputType input_type(int type) {
+    kunlun::require(type == KUNLUN_INPUT_F32 || type == KUNLUN_INPUT_F16);
+    return type == KUNLUN_INPUT_F16 ? kunlun::InputType::f16 : kunlun::InputType::f32;
+}
+} // namespace
+
 extern "C" {
 
 void kunlun_lock(void) { kunlun::runtime_mutex().lock(); }
@@ -51,6 +62,38 @@ void kunlun_matmul(kunlun_kernel * kernel, int device, void * y, const void * w,
     kunlun::matmul(kernel->kernel, device, y, w, x, k, n, batch, static_cast<kunlun::WeightType>(type), scales,
                    maxima, tile);
     kernel->route = kunlun::detail::route_of_last_matmul();
+}
+
+int kunlun_native_q4_layout_supported(int k, int n) { return kunlun::native_q4_layout_supported(k, n) ? 1 : 0; }
+size_t kunlun_native_q4_size(int k, int n) { return kunlun::native_q4_size(k, n); }
+int kunlun_pack_native_q4(void * destination, size_t bytes, const void * q4, int k, int n) {
+    return kunlun::pack_native_q4(destination, bytes, q4, k, n) ? 1 : 0;
+}
+void kunlun_upload_native_q4(int device, void * weights, const void * q4, int k, int n) {
+    kunlun::upload_native_q4(device, weights, q4, k, n);
+}
+const char * kunlun_native_q4_reason(int k, int n, int batch, int type) {
+    if (type != KUNLUN_INPUT_F32 && type != KUNLUN_INPUT_F16) {
+        if (!kunlun::native_q4_layout_supported(k, n)) return "K/N/layout capacity";
+        return "input type";
+    }
+    return kunlun::native_q4_reason(k, n, batch, input_type(type));
+}
+kunlun_native_q4_workspace * kunlun_native_q4_workspace_create(void) { return new kunlun_native_q4_workspace(); }
+void kunlun_native_q4_workspace_destroy(kunlun_native_q4_workspace * workspace) { delete workspace; }
+void kunlun_native_q4_statistics(const kunlun_native_q4_workspace * workspace, size_t out[4]) {
+    kunlun::require(workspace != nullptr && out != nullptr);
+    const kunlun::NativeQ4Statistics s = workspace->workspace.statistics();
+    out[0] = s.accelerated;
+    out[1] = s.fallback;
+    out[2] = s.hbm_workspace_bytes;
+    out[3] = s.l3_workspace_bytes;
+}
+int kunlun_native_q4_matmul(kunlun_native_q4_workspace * workspace, int device, void * y, const void * weights,
+                            const void * input, int k, int n, int batch, int type) {
+    kunlun::require(workspace != nullptr);
+    return kunlun::native_q4_matmul(workspace->workspace, device, y, weights, input, k, n, batch,
+                                    input_type(type)) ? 1 : 0;
 }
 
 void kunlun_statistics(size_t out[4]) {

@@ -85,6 +85,38 @@ __device__ __forceinline__ u32x4_a4 load_u32x4(const uint32_t *p) {
     return *reinterpret_cast<const u32x4_a4 *>(p);
 }
 
+// Eight activations as signed fixed point X_t = rint(v[t] * to_fixed) (round
+// to nearest even via the 1.5 * 2^23 magic constant, one FMA; |X_t| <= 2^22
+// when every |v[t]| < 2^e and to_fixed = 2^(22-e)), written as six balanced
+// base-16 digits in [-8, 7]: Z = (X + 0x888888) ^ 0x888888 holds them as 4-bit
+// two's-complement nibbles (as_uint(fma) - 0x4b400000 + 0x888888 ==
+// as_uint(fma) + 0xb5488888). Digit dword l holds digit l of X_t in nibble t,
+// so for signed nibbles w_t: sum_t w_t X_t = sum_l 16^l sdot8(w, dig[l]).
+__device__ __forceinline__ void fixed_point_digits(const float (&v)[8], float to_fixed, uint32_t (&dig)[6]) {
+    uint32_t z[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) z[t] = (__float_as_uint(fmaf(v[t], to_fixed, 12582912.0f)) + 0xb5488888u) ^ 0x888888u;
+    // 8 x 6 nibble transpose. E[s] byte c = (z[2s].n(2c), z[2s+1].n(2c)),
+    // O[s] byte c = (.. n(2c+1) ..); v_perm_b32(hi, lo, sel): selector byte
+    // 0-3 picks a lo byte, 4-7 a hi byte, 0x0c gives 0.
+    uint32_t ev[4], od[4];
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2) {
+        ev[s2] = (z[2 * s2] & 0x0f0f0f0fu) | ((z[2 * s2 + 1] << 4) & 0xf0f0f0f0u);
+        od[s2] = ((z[2 * s2] >> 4) & 0x0f0f0f0fu) | (z[2 * s2 + 1] & 0xf0f0f0f0u);
+    }
+    const uint32_t e01 = __builtin_amdgcn_perm(ev[1], ev[0], 0x05010400u);   // E0.b0 E1.b0 E0.b1 E1.b1
+    const uint32_t e23 = __builtin_amdgcn_perm(ev[3], ev[2], 0x05010400u);
+    dig[0] = __builtin_amdgcn_perm(e23, e01, 0x05040100u);
+    dig[2] = __builtin_amdgcn_perm(e23, e01, 0x07060302u);
+    dig[4] = __builtin_amdgcn_perm(ev[1], ev[0], 0x0c0c0602u) | __builtin_amdgcn_perm(ev[3], ev[2], 0x06020c0cu);
+    const uint32_t o01 = __builtin_amdgcn_perm(od[1], od[0], 0x05010400u);
+    const uint32_t o23 = __builtin_amdgcn_perm(od[3], od[2], 0x05010400u);
+    dig[1] = __builtin_amdgcn_perm(o23, o01, 0x05040100u);
+    dig[3] = __builtin_amdgcn_perm(o23, o01, 0x07060302u);
+    dig[5] = __builtin_amdgcn_perm(od[1], od[0], 0x0c0c0602u) | __builtin_amdgcn_perm(od[3], od[2], 0x06020c0cu);
+}
+
 // SiLU(g) * u in F32 with the reference's non-finite rules (reference
 // kernels/kunlun-swiglu.xpu:27-39): finite inputs give (g / (1 + e^-g)) * u;
 // otherwise NaN when g or u is NaN or g is -Inf, +-Inf with the product sign

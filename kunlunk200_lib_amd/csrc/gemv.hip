@@ -441,36 +441,8 @@ __global__ __launch_bounds__(64 * WAVES) void q4_gemv_dot8(const uint8_t *__rest
         // 2^(e-1) <= m < 2^e (e = 0 for m == 0); e is kept >= -100 so that
         // 2^(22-e) stays finite (blocks below 2^-100 lose relative precision only).
         const int e = max(__builtin_amdgcn_frexp_expf(m), -100);
-        const float to_fixed = ldexpf(1.0f, 22 - e);
-        // X = rint(v * 2^(22-e)) via the 1.5*2^23 magic constant (one FMA,
-        // round to nearest even), then Z = (X + 0x888888) ^ 0x888888:
-        // as_uint(fma) - 0x4b400000 + 0x888888 == as_uint(fma) + 0xb5488888.
-        uint32_t z[8];
-#pragma unroll
-        for (int t = 0; t < 8; ++t)
-            z[t] = (__float_as_uint(fmaf(v[t], to_fixed, 12582912.0f)) + 0xb5488888u) ^ 0x888888u;
-        // 8 x 6 nibble transpose: digit dword l holds nibble l of z[0..7].
-        // E[s] byte c = (z[2s].n(2c), z[2s+1].n(2c)), O[s] byte c = (.. n(2c+1) ..)
-        uint32_t ev[4], od[4];
-#pragma unroll
-        for (int s2 = 0; s2 < 4; ++s2) {
-            ev[s2] = (z[2 * s2] & 0x0f0f0f0fu) | ((z[2 * s2 + 1] << 4) & 0xf0f0f0f0u);
-            od[s2] = ((z[2 * s2] >> 4) & 0x0f0f0f0fu) | (z[2 * s2 + 1] & 0xf0f0f0f0u);
-        }
         uint32_t dig[6];
-        {
-            // v_perm_b32(hi, lo, sel): selector byte 0-3 picks lo byte, 4-7 hi byte, 0x0c gives 0
-            const uint32_t e01 = __builtin_amdgcn_perm(ev[1], ev[0], 0x05010400u);   // E0.b0 E1.b0 E0.b1 E1.b1
-            const uint32_t e23 = __builtin_amdgcn_perm(ev[3], ev[2], 0x05010400u);
-            dig[0] = __builtin_amdgcn_perm(e23, e01, 0x05040100u);
-            dig[2] = __builtin_amdgcn_perm(e23, e01, 0x07060302u);
-            dig[4] = __builtin_amdgcn_perm(ev[1], ev[0], 0x0c0c0602u) | __builtin_amdgcn_perm(ev[3], ev[2], 0x06020c0cu);
-            const uint32_t o01 = __builtin_amdgcn_perm(od[1], od[0], 0x05010400u);
-            const uint32_t o23 = __builtin_amdgcn_perm(od[3], od[2], 0x05010400u);
-            dig[1] = __builtin_amdgcn_perm(o23, o01, 0x05040100u);
-            dig[3] = __builtin_amdgcn_perm(o23, o01, 0x07060302u);
-            dig[5] = __builtin_amdgcn_perm(od[1], od[0], 0x0c0c0602u) | __builtin_amdgcn_perm(od[3], od[2], 0x06020c0cu);
-        }
+        kk::fixed_point_digits(v, ldexpf(1.0f, 22 - e), dig);
         if (idx < groups) {
             const int b = (B > 1 && idx >= blocks * 4) ? 1 : 0;
             const int rem = idx - b * blocks * 4;

@@ -50,6 +50,13 @@ int kk_dense_mfma_gemv(int type, const void *w, const float *x, float *y, int k,
 int kk_elementwise(float *y, const float *a, const float *b, int count, int width, int b_count, int op,
                    float parameter, hipStream_t stream);
 
+// Native Q4 layout (256-byte aligned): offset of the FP16 scales, and the
+// exact GEMV Y[batch,n] = X[batch,k] W^T with X F32 (x_f16 = 0, 4-byte
+// aligned) or F16 (x_f16 = 1, 2-byte aligned), Y F32 (4-byte aligned).
+size_t kk_native_q4_payload_bytes(int k, int n);
+int kk_native_q4_gemv(const void *weights, const void *x, int x_f16, float *y, int k, int n, int batch,
+                      hipStream_t stream);
+
 // Bytes of device workspace kk_i8_quantize needs for `count` activations.
 size_t kk_i8_workspace_bytes(int k, int batch);
 // Two-pass per-tensor INT8 quantization of X[batch,k] into `workspace`

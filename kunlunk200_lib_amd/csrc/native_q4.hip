@@ -1,0 +1,262 @@
+// GEMV over the native Q4 layout (reference src/q4-layout.cpp:15-37,
+// src/k200.cpp:554-617) on gfx950.
+//
+// Layout: for N32 tile t and K32 block b, 512 bytes at (t * blocks + b) * 512
+// hold byte [pair j][lane r] = signed nibbles of row 32t + r, K 32b + 2j (low)
+// and 32b + 2j + 1 (high); after the 256-byte aligned payload, 32 FP16 block
+// scales per tile-block at (t * blocks + b) * 32 + r. Rows past N are zero.
+//
+// Arithmetic is exact up to the activation representation: each 32-value
+// activation block is a 23-bit signed fixed point with a power-of-two block
+// scale s_b (kk::fixed_point_digits), so sum_j q_j X_j is an exact int32 from
+// 24 v_dot8_i32_i4 per row and block, and y_r += float(S) * (d_rb * s_b) in F32.
+//
+// Work split: one workgroup per N32 tile, its waves take the tile's items of
+// eight K32 blocks in turn. In an item, lane l owns block 8i + l/8 and rows
+// 4(l%8) .. 4(l%8)+3: it loads the 16 pair dwords of those rows (stride 32
+// bytes; the 8 lanes of a block read 32 contiguous bytes per pair, the 16
+// loads cover the block's 512 bytes) and turns each group of four pair dwords
+// into four row dwords of 8 consecutive K values with a 4 x 4 byte transpose
+// (8 v_perm_b32). Rows are reduced over lanes, then over waves in a fixed
+// order: results are bitwise reproducible.
+#include "device_common.h"
+#include "launch.h"
+
+#include <algorithm>
+
+namespace {
+
+constexpr int kNqWaves = 8;
+constexpr int kNqThreads = 64 * kNqWaves;
+constexpr int kNqDepth = 2;                 // items in flight per wave
+constexpr int kNqItemBlocks = 8;            // K32 blocks per item (64 lanes / 8 lanes per block)
+constexpr int kNqMaxColumns = 4;            // batch columns per launch
+constexpr size_t kNqLdsLimit = 64 * 1024;
+
+size_t lds_bytes(int blocks, int columns) {
+    // per column and block: 24 digit dwords and one scale; per wave and
+    // column: 32 row partials
+    return static_cast<size_t>(columns) * blocks * (96 + 4) + static_cast<size_t>(kNqWaves) * columns * 32 * 4;
+}
+
+template <int B>
+__global__ __launch_bounds__(kNqThreads) void native_q4_gemv(const uint8_t *__restrict__ w,
+                                                            const uint16_t *__restrict__ scales,
+                                                            const void *__restrict__ x, int x_f16,
+                                                            float *__restrict__ y, int k, int n) {
+    extern __shared__ uint4 lds4[];
+    const int blocks = k >> 5;
+    const int items = (blocks + kNqItemBlocks - 1) / kNqItemBlocks;
+    const int tile = blockIdx.x;
+    uint4 *digits = lds4;                                                                      // [B][blocks][6]
+    float *block_scale = reinterpret_cast<float *>(lds4 + static_cast<size_t>(B) * blocks * 6);  // [B][blocks]
+    float *partial = block_scale + B * blocks;                                                 // [waves][B][32]
+
+    const int lane = threadIdx.x & (kk::kWave - 1);
+    const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+    const int c = lane & 7;                       // rows 4c .. 4c+3 of the tile
+    const size_t tile_block0 = static_cast<size_t>(tile) * blocks;
+
+    auto load_item = [&](int s, uint32_t (&buf)[18]) {
+        const int it = min(wid + kNqWaves * s, items - 1);
+        const int blk = min(it * kNqItemBlocks + (lane >> 3), blocks - 1);
+        const uint8_t *src = w + (tile_block0 + blk) * 512 + 4 * c;
+#pragma unroll
+        for (int p = 0; p < 16; ++p) buf[p] = *reinterpret_cast<const uint32_t *>(src + 32 * p);
+        const uint2 sc = *reinterpret_cast<const uint2 *>(scales + (tile_block0 + blk) * 32 + 4 * c);
+        buf[16] = sc.x;
+        buf[17] = sc.y;
+    };
+
+    // 1. activation loads: thread (b, block, q) owns values 8q .. 8q+7 of a block
+    const int groups = B * blocks * 4;
+    const int passes = (groups + kNqThreads - 1) / kNqThreads;
+    // 2. the first weight items go out before the activations are converted
+    const int my_items = wid < items ? (items - wid + kNqWaves - 1) / kNqWaves : 0;
+    uint32_t ring[kNqDepth][18];
+#pragma unroll
+    for (int d = 0; d < kNqDepth; ++d) load_item(d, ring[d]);
+
+    // 3. activations -> block scale and six digit dwords per 8 values
+    for (int pass = 0; pass < passes; ++pass) {
+        const int idx = pass * kNqThreads + static_cast<int>(threadIdx.x);
+        const int g = min(idx, groups - 1);
+        const int b = g / (blocks * 4);
+        const int rem = g - b * blocks * 4;
+        const size_t base = static_cast<size_t>(b) * k + static_cast<size_t>(rem) * 8;
+        float v[8];
+        if (x_f16) {
+            const uint16_t *xh = static_cast<const uint16_t *>(x) + base;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) v[t] = kk::half_bits_to_float(xh[t]);
+        } else {
+            const float *xf = static_cast<const float *>(x) + base;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) v[t] = xf[t];
+        }
+        float m = 0.0f, bad = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const float a = fabsf(v[t]);
+            bad = (a <= 3.402823466e38f) ? bad : 1.0f;
+            m = fmaxf(m, a);
+        }
+        // the four threads of a block are the lanes of one quad
+        m = fmaxf(m, kk::dpp_move<0xb1>(m));
+        m = fmaxf(m, kk::dpp_move<0x4e>(m));
+        bad = fmaxf(bad, kk::dpp_move<0xb1>(bad));
+        bad = fmaxf(bad, kk::dpp_move<0x4e>(bad));
+        // 2^(e-1) <= m < 2^e; e >= -100 keeps 2^(22-e) finite
+        const int e = max(__builtin_amdgcn_frexp_expf(m), -100);
+        uint32_t dig[6];
+        kk::fixed_point_digits(v, ldexpf(1.0f, 22 - e), dig);
+        if (idx < groups) {
+            uint32_t *dst = reinterpret_cast<uint32_t *>(digits) + static_cast<size_t>(b * blocks) * 24 + rem * 6;
+#pragma unroll
+            for (int l = 0; l < 6; ++l) dst[l] = dig[l];
+            if ((rem & 3) == 0)
+                block_scale[b * blocks + (rem >> 2)] = bad != 0.0f ? __builtin_nanf("") : ldexpf(1.0f, e - 22);
+        }
+    }
+    __syncthreads();
+
+    // 4. items: 4 rows x one K32 block per lane
+    float acc[B][4];
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[b][r] = 0.0f;
+
+    auto compute_item = [&](int s, const uint32_t (&buf)[18]) {
+        const int blk_raw = (wid + kNqWaves * s) * kNqItemBlocks + (lane >> 3);
+        const bool live = blk_raw < blocks;
+        const int blk = min(blk_raw, blocks - 1);
+        float d[4];
+        d[0] = kk::half_bits_to_float(buf[16] & 0xffffu);
+        d[1] = kk::half_bits_to_float(buf[16] >> 16);
+        d[2] = kk::half_bits_to_float(buf[17] & 0xffffu);
+        d[3] = kk::half_bits_to_float(buf[17] >> 16);
+        // row dwords: o[r][q] nibble t = row 4c+r, K 8q+t (4 x 4 byte transposes)
+        uint32_t o[4][4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t a = buf[4 * q], bb = buf[4 * q + 1], cc = buf[4 * q + 2], dd = buf[4 * q + 3];
+            const uint32_t ab_lo = __builtin_amdgcn_perm(bb, a, 0x05010400u);    // a0 b0 a1 b1
+            const uint32_t ab_hi = __builtin_amdgcn_perm(bb, a, 0x07030602u);    // a2 b2 a3 b3
+            const uint32_t cd_lo = __builtin_amdgcn_perm(dd, cc, 0x05010400u);
+            const uint32_t cd_hi = __builtin_amdgcn_perm(dd, cc, 0x07030602u);
+            o[0][q] = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x05040100u);          // a0 b0 c0 d0
+            o[1][q] = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x07060302u);          // a1 b1 c1 d1
+            o[2][q] = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x05040100u);
+            o[3][q] = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x07060302u);
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const uint4 *dsrc = digits + (static_cast<size_t>(b) * blocks + blk) * 6;
+            uint32_t dg[24];
+#pragma unroll
+            for (int g = 0; g < 6; ++g) {
+                const uint4 v4 = dsrc[g];
+                dg[4 * g] = v4.x;
+                dg[4 * g + 1] = v4.y;
+                dg[4 * g + 2] = v4.z;
+                dg[4 * g + 3] = v4.w;
+            }
+            const float sb = block_scale[b * blocks + blk];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                int t[6];
+#pragma unroll
+                for (int l = 0; l < 6; ++l) {
+                    t[l] = 0;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        t[l] = __builtin_amdgcn_sdot8(static_cast<int>(o[r][q]), static_cast<int>(dg[q * 6 + l]),
+                                                      t[l], false);
+                }
+                int sum = t[5];
+#pragma unroll
+                for (int l = 4; l >= 0; --l) sum = (sum << 4) + t[l];
+                acc[b][r] = fmaf(static_cast<float>(sum), live ? d[r] * sb : 0.0f, acc[b][r]);
+            }
+        }
+    };
+
+    for (int base = 0; base < my_items; base += kNqDepth) {
+#pragma unroll
+        for (int dpt = 0; dpt < kNqDepth; ++dpt) {
+            const int s = base + dpt;
+            if (s < my_items) {
+                compute_item(s, ring[dpt]);
+                if (s + kNqDepth < my_items) load_item(s + kNqDepth, ring[dpt]);
+            }
+        }
+    }
+
+    // 5. rows: sum the 8 lanes of each row group (fixed xor order), then the waves
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float v = acc[b][r];
+            v += __shfl_xor(v, 8, kk::kWave);
+            v += __shfl_xor(v, 16, kk::kWave);
+            v += __shfl_xor(v, 32, kk::kWave);
+            if (lane < 8) partial[(wid * B + b) * 32 + 4 * c + r] = v;
+        }
+    __syncthreads();
+    if (static_cast<int>(threadIdx.x) < 32 * B) {
+        const int b = threadIdx.x >> 5, row = threadIdx.x & 31;
+        float v = 0.0f;
+#pragma unroll
+        for (int wv = 0; wv < kNqWaves; ++wv) v += partial[(wv * B + b) * 32 + row];
+        const int gr = tile * 32 + row;
+        if (gr < n) y[static_cast<size_t>(b) * n + gr] = v;
+    }
+}
+
+template <int B>
+hipError_t launch_columns(const uint8_t *w, const uint16_t *scales, const void *x, int x_f16, float *y, int k,
+                          int n, hipStream_t stream) {
+    const int tiles = (n + 31) / 32;
+    const size_t lds = lds_bytes(k >> 5, B);
+    hipLaunchKernelGGL(native_q4_gemv<B>, dim3(tiles), dim3(kNqThreads), lds, stream, w, scales, x, x_f16, y, k, n);
+    return hipGetLastError();
+}
+
+} // namespace
+
+extern "C" size_t kk_native_q4_payload_bytes(int k, int n) {
+    const size_t rows = (static_cast<size_t>(n) + 31) & ~static_cast<size_t>(31);
+    return (rows * k / 2 + 255) & ~static_cast<size_t>(255);
+}
+
+extern "C" int kk_native_q4_gemv(const void *weights, const void *x, int x_f16, float *y, int k, int n, int batch,
+                                 hipStream_t stream) {
+    if (!weights || !x || !y || k <= 0 || k % 32 != 0 || k > 16384 || n <= 0 || batch <= 0)
+        return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(weights) & 255) != 0) return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(x) & (x_f16 ? 1 : 3)) != 0 || (reinterpret_cast<uintptr_t>(y) & 3) != 0)
+        return hipErrorInvalidValue;
+    const uint8_t *w = static_cast<const uint8_t *>(weights);
+    const uint16_t *scales = reinterpret_cast<const uint16_t *>(w + kk_native_q4_payload_bytes(k, n));
+    const int blocks = k >> 5;
+    int fit = 1;
+    while (fit < kNqMaxColumns && lds_bytes(blocks, fit + 1) <= kNqLdsLimit) ++fit;
+    if (lds_bytes(blocks, 1) > kNqLdsLimit) return hipErrorInvalidValue;
+    const size_t x_bytes = x_f16 ? 2 : 4;
+    for (int c0 = 0; c0 < batch; c0 += fit) {
+        const int cols = std::min(fit, batch - c0);
+        const void *xc = static_cast<const uint8_t *>(x) + static_cast<size_t>(c0) * k * x_bytes;
+        float *yc = y + static_cast<size_t>(c0) * n;
+        hipError_t status;
+        switch (cols) {
+        case 1: status = launch_columns<1>(w, scales, xc, x_f16, yc, k, n, stream); break;
+        case 2: status = launch_columns<2>(w, scales, xc, x_f16, yc, k, n, stream); break;
+        case 3: status = launch_columns<3>(w, scales, xc, x_f16, yc, k, n, stream); break;
+        default: status = launch_columns<4>(w, scales, xc, x_f16, yc, k, n, stream); break;
+        }
+        if (status != hipSuccess) return status;
+    }
+    return hipSuccess;
+}

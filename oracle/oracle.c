@@ -486,3 +486,65 @@ void orc_elementwise(float *y, const float *a, const float *b, int n, int width,
         y[e] = out;
     }
 }
+
+/* Native Q4 layout (reference src/q4-layout.cpp:7-37). Bytes: rows = n padded
+ * to 32; payload = aligned256(rows * k / 2); scales = aligned256(rows * k / 16). */
+static size_t orc_align256(size_t bytes) { return (bytes + 255u) & ~(size_t)255u; }
+
+size_t orc_native_q4_size(int k, int n) {
+    if (k <= 0 || k > 16384 || k % 32 != 0 || n <= 0 || n > 90000000 / k) return 0;
+    size_t rows = ((size_t)n + 31u) & ~(size_t)31u;
+    return orc_align256(rows * (size_t)k / 2) + orc_align256(rows * (size_t)(k / 32) * 2);
+}
+
+/* Element e (0..31) of a Q4_0 block as the signed value q - 8: byte 2 + e % 16,
+ * low nibble for e < 16, high nibble otherwise (reference q4-layout.cpp:29-30). */
+static int orc_q4_signed(const uint8_t *block, int e) {
+    int shift = e < 16 ? 0 : 4;
+    return ((block[2 + (e % 16)] >> shift) & 15) - 8;
+}
+
+/* For row r and block b: the FP16 scale goes to the scale region at
+ * ((r / 32) * (k / 32) + b) * 32 + r % 32 (two bytes each), and byte
+ * ((r / 32) * (k / 32) + b) * 512 + j * 32 + r % 32 holds elements 2j (low
+ * nibble) and 2j + 1 (high) as 4-bit two's complement
+ * (reference q4-layout.cpp:24-35). Everything else is zero. */
+void orc_pack_native_q4(const uint8_t *q4, int k, int n, uint8_t *out) {
+    size_t total = orc_native_q4_size(k, n);
+    size_t rows = ((size_t)n + 31u) & ~(size_t)31u;
+    size_t payload = orc_align256(rows * (size_t)k / 2);
+    int blocks = k / 32;
+    memset(out, 0, total);
+    for (int r = 0; r < n; ++r) {
+        for (int b = 0; b < blocks; ++b) {
+            const uint8_t *block = q4 + ((size_t)r * blocks + b) * 18;
+            size_t tb = (size_t)(r / 32) * blocks + b;
+            out[payload + (tb * 32 + r % 32) * 2] = block[0];
+            out[payload + (tb * 32 + r % 32) * 2 + 1] = block[1];
+            for (int j = 0; j < 16; ++j) {
+                int lo = orc_q4_signed(block, 2 * j), hi = orc_q4_signed(block, 2 * j + 1);
+                out[tb * 512 + (size_t)j * 32 + r % 32] = (uint8_t)((lo & 15) | ((hi & 15) << 4));
+            }
+        }
+    }
+}
+
+/* Inverse view: F32 weights [n, k] of a native layout, w = signed4 * fp16 scale. */
+void orc_native_q4_decode(const uint8_t *native, int k, int n, float *w) {
+    size_t rows = ((size_t)n + 31u) & ~(size_t)31u;
+    size_t payload = orc_align256(rows * (size_t)k / 2);
+    int blocks = k / 32;
+    for (int r = 0; r < n; ++r) {
+        for (int b = 0; b < blocks; ++b) {
+            size_t tb = (size_t)(r / 32) * blocks + b;
+            uint16_t h = (uint16_t)(native[payload + (tb * 32 + r % 32) * 2] |
+                                    (native[payload + (tb * 32 + r % 32) * 2 + 1] << 8));
+            float d = orc_half_to_float(h);
+            for (int e = 0; e < 32; ++e) {
+                int byte = native[tb * 512 + (size_t)(e / 2) * 32 + r % 32];
+                int v = (e % 2 ? byte >> 4 : byte) & 15;
+                w[(size_t)r * k + (size_t)b * 32 + e] = (float)(v >= 8 ? v - 16 : v) * d;
+            }
+        }
+    }
+}

@@ -39,6 +39,12 @@
  *                            of the FP64 closed form, constant rows exactly
  *                            (c / |c| = sign), and the reference
  *                            library-bench gold (max_abs < 1e-4).
+ *   orc_native_q4_size     - the reference's published 4096 x 4096 figure
+ *                            (9,437,184 bytes) and the closed form;
+ *   orc_pack_native_q4,
+ *   orc_native_q4_decode   - the reference bench's inverse-mapping check of
+ *                            every nibble and scale, and decode(pack(q4))
+ *                            equal to orc_q4_decode(q4) bit for bit.
  */
 #ifndef KUNLUN_ORACLE_H
 #define KUNLUN_ORACLE_H
@@ -84,6 +90,10 @@ float orc_swiglu_value(float g, float u);
 void orc_swiglu(const void *gate, const void *up, void *y, int width, int rows, int gate_stride,
                 int up_stride, int output_stride, int bytes);
 void orc_elementwise(float *y, const float *a, const float *b, int n, int width, int bn, int op, float parameter);
+
+size_t orc_native_q4_size(int k, int n);
+void orc_pack_native_q4(const uint8_t *q4, int k, int n, uint8_t *out);
+void orc_native_q4_decode(const uint8_t *native, int k, int n, float *w);
 
 #ifdef __cplusplus
 }

@@ -52,6 +52,9 @@ class Oracle:
             "orc_swiglu_value": (ctypes.c_float, [ctypes.c_float, ctypes.c_float]),
             "orc_swiglu": (None, [P, P, P, I, I, I, I, I, I]),
             "orc_elementwise": (None, [P, P, P, I, I, I, I, ctypes.c_float]),
+            "orc_native_q4_size": (ctypes.c_size_t, [I, I]),
+            "orc_pack_native_q4": (None, [P, I, I, P]),
+            "orc_native_q4_decode": (None, [P, I, I, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -211,6 +214,23 @@ class Oracle:
         assert y.dtype == np.float32 and y.flags.c_contiguous and y.size == a.size
         self.lib.orc_elementwise(_p(y), _p(a), _p(b), a.size, int(width), b.size, int(op), float(parameter))
         return y
+
+    def native_q4_size(self, k: int, n: int) -> int:
+        return self.lib.orc_native_q4_size(k, n)
+
+    def pack_native_q4(self, q4: np.ndarray, k: int, n: int) -> np.ndarray:
+        q4 = np.ascontiguousarray(q4, dtype=np.uint8)
+        assert q4.size >= n * (k // 32) * 18
+        out = np.empty(self.native_q4_size(k, n), np.uint8)
+        self.lib.orc_pack_native_q4(_p(q4), k, n, _p(out))
+        return out
+
+    def native_q4_decode(self, native: np.ndarray, k: int, n: int) -> np.ndarray:
+        native = np.ascontiguousarray(native, dtype=np.uint8)
+        assert native.size >= self.native_q4_size(k, n)
+        w = np.empty((n, k), np.float32)
+        self.lib.orc_native_q4_decode(_p(native), k, n, _p(w))
+        return w
 
     def rowwise_i8_matmul(self, w: np.ndarray, x: np.ndarray) -> np.ndarray:
         """Whole reference rowwise_i8 path: weight upload quantization, two-pass

@@ -38,3 +38,11 @@ def gpu():
     count = kl.device_count()
     assert count >= 1, "gpu-marked test needs a HIP device"
     return kl
+
+
+@pytest.fixture(scope="session")
+def kl():
+    """The product library, loaded (no device needed)."""
+    import kunlunk200_lib_amd as kl
+    kl.load()
+    return kl

@@ -16,13 +16,6 @@ C_HEADER = os.path.join(ROOT, "include", "kunlun", "k200_c.h")
 CXX_HEADER = os.path.join(ROOT, "include", "kunlun", "k200.h")
 
 
-@pytest.fixture(scope="module")
-def kl():
-    import kunlunk200_lib_amd as kl
-    kl.load()
-    return kl
-
-
 def _c_names():
     text = open(C_HEADER).read()
     return sorted(set(re.findall(r"\b(kunlun_[a-z0-9_]+)\s*\(", text)))
