@@ -262,6 +262,105 @@ def small_batch_leg(kernel, events, stream, device: int, reps: int) -> dict:
     return out
 
 
+NATIVE_SHAPES = ((4096, 4096), (4096, 11008), (11008, 4096))   # reference docs/native-q4.md:62-71
+NATIVE_REFERENCE_MS = {(4096, 4096): 0.338455, (4096, 11008): 0.712449, (11008, 4096): 0.843438}
+
+
+def native_leg(events, stream, device: int, reps: int) -> dict:
+    """native_q4_matmul at the reference's published shapes, batch 1, F32 X, over
+    rotating weight copies. Each call completes before returning (as the
+    reference's does), so `us` is the time per call including its
+    synchronization; GB/s = layout bytes + 4k + 4n over that time."""
+    out = {}
+    rng = np.random.Generator(np.random.PCG64(33))
+    ws = kl.NativeQ4Workspace()
+    for k, n in NATIVE_SHAPES:
+        nbytes = kl.native_q4_size(k, n)
+        q4 = kl.quantize_q4_0(rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+        first = kl.Buffer(device, nbytes)
+        kl.upload_native_q4(device, first.data, q4, k, n)
+        bufs = [first]
+        for _ in range(max(2, -(-ROTATE_BYTES // nbytes)) - 1):
+            b = kl.Buffer(device, nbytes)
+            with kl.runtime_mutex():
+                kl.select(device)
+                kl.check(kl.copy(b.data, first.data, nbytes, kl.CopyKind.device_to_device))
+                kl.check(kl.wait())
+            bufs.append(b)
+        xb = kl.Buffer(device, 4 * k)
+        xb.upload(rng.standard_normal(k, dtype=np.float32))
+        yb = kl.Buffer(device, 4 * n)
+        with kl.runtime_mutex():
+            for i in range(5):
+                kl.native_q4_matmul(ws, device, yb.data, bufs[i % len(bufs)].data, xb.data, k, n)
+            start, stop = events.create(), events.create()
+            events.record(start, stream)
+            t0 = time.perf_counter()
+            for i in range(reps):
+                kl.native_q4_matmul(ws, device, yb.data, bufs[i % len(bufs)].data, xb.data, k, n)
+            wall_us = (time.perf_counter() - t0) * 1e6 / reps
+            events.record(stop, stream)
+            kl.select(device)
+            kl.check(kl.wait())
+            ms = events.elapsed_ms(start, stop) / reps
+        total = nbytes + 4 * k + 4 * n
+        out[f"k{k}_n{n}"] = {"us": round(ms * 1e3, 3), "host_wall_us": round(wall_us, 3),
+                             "gbps": round(total / (ms * 1e-3) / 1e9, 1),
+                             "hbm_frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                             "reference_k200_ms": NATIVE_REFERENCE_MS[(k, n)]}
+        for b in bufs + [xb, yb]:
+            b.close()
+    return out
+
+
+COMMON_SHAPES = ((4096, 11008, 1), (4096, 4096, 1), (11008, 4096, 1), (4096, 11008, 128), (4096, 4096, 128))
+
+
+def common_leg(events, stream, device: int, reps: int) -> dict:
+    """common_q4_matmul (common Q4 ABI v1) at the reference's main shapes, M = 1
+    (two-component A8 GEMV) and M = 128 (Row A8 GEMM), F32 X, over rotating
+    weight copies. Calls complete before returning; `us` is per call. GB/s =
+    layout bytes + 4mk + 4mn over that time; TOP/s = 2mkn / time for M > 1."""
+    out = {}
+    rng = np.random.Generator(np.random.PCG64(44))
+    ws = kl.CommonQ4Workspace()
+    for k, n, m in COMMON_SHAPES:
+        q4 = kl.quantize_q4_0(rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+        nbytes = kl.common_q4_size(k, n)
+        weights = []
+        for _ in range(max(2, -(-ROTATE_BYTES // nbytes))):
+            w = kl.CommonQ4Weight(device, k, n)
+            w.upload(q4)                         # a handle is usable once uploaded
+            weights.append(w)
+        xb = kl.Buffer(device, 4 * m * k)
+        xb.upload(rng.standard_normal((m, k), dtype=np.float32))
+        yb = kl.Buffer(device, 4 * m * n)
+        with kl.runtime_mutex():
+            for i in range(3):
+                kl.common_q4_matmul(ws, device, yb.data, weights[i % len(weights)], xb.data, m)
+            start, stop = events.create(), events.create()
+            events.record(start, stream)
+            t0 = time.perf_counter()
+            for i in range(reps):
+                kl.common_q4_matmul(ws, device, yb.data, weights[i % len(weights)], xb.data, m)
+            wall_us = (time.perf_counter() - t0) * 1e6 / reps
+            events.record(stop, stream)
+            kl.select(device)
+            kl.check(kl.wait())
+            ms = events.elapsed_ms(start, stop) / reps
+        total = nbytes + 4 * m * k + 4 * m * n
+        entry = {"us": round(ms * 1e3, 3), "host_wall_us": round(wall_us, 3),
+                 "gbps": round(total / (ms * 1e-3) / 1e9, 1)}
+        if m > 1:
+            entry["tops"] = round(2.0 * m * k * n / (ms * 1e-3) / 1e12, 1)
+        out[f"k{k}_n{n}_m{m}"] = entry
+        for w in weights:
+            w.close()
+        xb.close()
+        yb.close()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -272,7 +371,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gemm-reps", type=int, default=50, help="timed batch-512 GEMM calls per shape (0: skip)")
     ap.add_argument("--small-reps", type=int, default=100, help="timed calls per small-batch config (0: skip)")
-    ap.add_argument("--only", choices=[name for name, _, _ in LAYER] + ["gemm", "copy", "small"],
+    ap.add_argument("--native-reps", type=int, default=100, help="timed native_q4_matmul calls per shape (0: skip)")
+    ap.add_argument("--common-reps", type=int, default=50, help="timed common_q4_matmul calls per shape (0: skip)")
+    ap.add_argument("--only", choices=[name for name, _, _ in LAYER] + ["gemm", "copy", "small", "native", "common"],
                     help="profiling aid: time only this GEMV's launch loop, the GEMM leg, or (copy) a "
                          f"{COPY_BYTES >> 20} MiB device-to-device copy that calibrates the traffic counters")
     args = ap.parse_args()
@@ -293,6 +394,12 @@ def main() -> int:
     if args.only == "small":
         print(json.dumps({"small_batch": small_batch_leg(kernel, events, stream, device, args.small_reps)}),
               flush=True)
+        return 0
+    if args.only == "common":
+        print(json.dumps({"common_q4": common_leg(events, stream, device, args.common_reps)}), flush=True)
+        return 0
+    if args.only == "native":
+        print(json.dumps({"native_q4": native_leg(events, stream, device, args.native_reps)}), flush=True)
         return 0
     if args.only == "copy":
         print(json.dumps({"copy": copy_leg(events, stream, device)}), flush=True)
@@ -384,6 +491,8 @@ def main() -> int:
 
     gemm = gemm_leg(kernel, events, stream, device, args.gemm_reps) if args.gemm_reps > 0 else None
     small = small_batch_leg(kernel, events, stream, device, args.small_reps) if args.small_reps > 0 else None
+    native = native_leg(events, stream, device, args.native_reps) if args.native_reps > 0 else None
+    common = common_leg(events, stream, device, args.common_reps) if args.common_reps > 0 else None
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     result = {
         "metric": METRIC,
@@ -424,6 +533,8 @@ def main() -> int:
         "per_shape": per_shape,
         "gemm_b512": gemm,
         "small_batch": small,
+        "native_q4": native,
+        "common_q4": common,
     }
     print(json.dumps(result), flush=True)
     for bufs in copies.values():

@@ -2,10 +2,10 @@
 //
 // This header keeps the declarations, argument meaning, defaults and class
 // layouts of the matmul subset of the reference library's public header
-// (reference include/kunlun/k200.h:10-37, 40-41, 62-107, 127-132, 185-224, 345-350)
+// (reference include/kunlun/k200.h:10-37, 40-41, 62-107, 127-132, 185-335, 345-350)
 // so a consumer of that subset rebuilds against this library unchanged.
 // Declarations of the reference that are not on the matmul path (attention,
-// Q6_K, the common Q4 ABI, KV caches) are not
+// Q6_K, KV caches, row gathers) are not
 // declared here. matmul_swiglu has no reference counterpart (see below).
 //
 // Device numbering: the reference drives the two processing dies of one
@@ -197,6 +197,152 @@ private:
 // overlapping ranges abort.
 bool native_q4_matmul(NativeQ4Workspace &, int device, void * y, const void * weights,
                       const void * input, int k, int n, int batch = 1, InputType type = InputType::f32);
+
+// ---------------------------------------------------------------------------
+// Common Q4 ABI v1 (reference k200.h:226-335): the persistent weight format
+// K200_Q4_0_MICRO32_BANK16_KMAJOR (layout 1, scale order 1) of an [n,k] Q4_0
+// matrix, padded to Kp = k rounded up to 512 (k < 512) or 256 and Np = n
+// rounded up to 256. For output column c and K block b, the 16 bytes of
+// signed nibble pairs (K 2p low, 2p+1 high) sit at
+// ((c/32) * Kp/32 + b) * 512 + (c%16) * 32 + ((c%32)/16) * 16; the FP16 scales
+// follow at scale_offset = Np*Kp/2 as [b][Np]. Payload Np*Kp*9/16 bytes.
+struct CommonQ4Info {
+    uint32_t abi_version, quant_type, layout, scale_order;
+    int k, n, kp, np, device;
+    size_t scale_offset, payload_bytes;
+};
+bool common_q4_supported(int k, int n);               // 0 < k <= 16384, 0 < n <= 32000
+size_t common_q4_size(int k, int n);                  // payload bytes, 0 when unsupported
+
+struct CommonQ4ActivationStatistics {
+    size_t prepare_calls, quantized_chunks, quant_kernel_launches;
+    size_t prepared_matmuls, prepared_chunks, invalidations, rejected_calls;
+    size_t hbm_activation_bytes;
+    uint64_t quantization_ns, preparation_ns;
+};
+struct CommonQ4ActivationChunk {
+    const void * values; const void * scales;
+    int first, rows, padded_rows, kp, components;
+    size_t values_bytes, scales_bytes;
+};
+class CommonQ4ActivationLease;
+class CommonQ4Workspace;
+
+struct CommonQ4WeightStatistics { size_t uploads, upload_bytes; double pack_ms, upload_ms; };
+class CommonQ4Weight {
+public:
+    // Borrowed storage must be 256-byte aligned, hold common_q4_size bytes and
+    // outlive this handle and its calls; null storage allocates it here.
+    CommonQ4Weight(int device, int k, int n, void * storage = nullptr, size_t bytes = 0);
+    ~CommonQ4Weight();
+    CommonQ4Weight(const CommonQ4Weight &) = delete;
+    CommonQ4Weight & operator=(const CommonQ4Weight &) = delete;
+    CommonQ4Info info() const;
+    CommonQ4WeightStatistics statistics() const;
+    void * data() const;
+    // Packs n rows of ceil(k/32) Q4_0 blocks on the host and uploads them;
+    // completes before returning.
+    void upload(const void * q4, size_t bytes);
+    struct Impl;
+private:
+    Impl * impl_;
+    friend bool common_q4_matmul_pair(CommonQ4Workspace &, int, void *, void *, const CommonQ4Weight &,
+                                      const CommonQ4Weight &, const CommonQ4ActivationLease &, uint64_t);
+    friend void common_q4_matmul(CommonQ4Workspace &, int, void *, const CommonQ4Weight &, const void *, int,
+                                 InputType);
+    friend bool common_q4_matmul_shared(CommonQ4Workspace &, int, void *, const CommonQ4Weight &,
+                                        const CommonQ4ActivationLease &, uint64_t);
+};
+struct CommonQ4Statistics {
+    // Calls by route, as the reference counts them: GEMV (M = 1, two-component
+    // A8), then M > 1 chunks by padded rows (8, 32, 64 with Kp <= 8192, 128
+    // with Kp <= 4096, 64 above, 128 above), then the exact M = 1 route.
+    size_t paths[8], calls, chunks;
+    size_t hbm_workspace_bytes, l3_workspace_bytes, slice_bytes;
+};
+// Counters of the reference's SD engine schedules; always zero here.
+struct CommonQ4MacStatistics {
+    size_t baseline_sd_calls, stream_sd_calls, shape_fallbacks, resident_l1d_bytes;
+};
+// Device view of the last call's quantized activations (components 0: none).
+// components 2 (M = 1): code of K index j at values[(j/32)*64 + j%32], the
+// residual code at values[2*kp + (j/32)*64 + j%32], F32 scales[0] and [1].
+// components 1 (M > 1): row r's codes at values[r*kp + j], scale scales[r*16].
+struct CommonQ4Quantization { const void * values; const void * scales; int rows, kp, components; };
+struct CommonQ4PairStatistics { size_t calls, declined, l3_partial_bytes; };
+enum class CommonQ4PairStatus { NotAttempted, Success, Disabled, InvalidInput, Configuration, WeightAbi, Lease, Alias,
+                                Workspace };
+class CommonQ4Workspace {
+public:
+    CommonQ4Workspace();
+    ~CommonQ4Workspace();
+    CommonQ4Workspace(const CommonQ4Workspace &) = delete;
+    CommonQ4Workspace & operator=(const CommonQ4Workspace &) = delete;
+    CommonQ4Statistics statistics() const;
+    CommonQ4ActivationStatistics activation_statistics() const;
+    CommonQ4MacStatistics mac_statistics() const;
+    // Borrowed device buffers, valid until the next call or workspace destruction.
+    CommonQ4Quantization quantization() const;
+    struct Impl;
+private:
+    Impl * impl_;
+    friend CommonQ4PairStatistics common_q4_pair_statistics(const CommonQ4Workspace &);
+    friend CommonQ4PairStatus common_q4_pair_last_status(const CommonQ4Workspace &);
+    friend bool common_q4_matmul_pair(CommonQ4Workspace &, int, void *, void *, const CommonQ4Weight &,
+                                      const CommonQ4Weight &, const CommonQ4ActivationLease &, uint64_t);
+    friend void common_q4_matmul(CommonQ4Workspace &, int, void *, const CommonQ4Weight &, const void *, int,
+                                 InputType);
+    friend bool common_q4_prepare(CommonQ4Workspace &, int, const void *, int, int, InputType, uint64_t,
+                                  CommonQ4ActivationLease &);
+    friend bool common_q4_matmul_shared(CommonQ4Workspace &, int, void *, const CommonQ4Weight &,
+                                        const CommonQ4ActivationLease &, uint64_t);
+};
+// Y[m,n] = X[m,k] W^T, X F32 or F16 contiguous, Y F32; completes before
+// returning (reference k200.h:300-302). M = 1 quantizes X per tensor into two
+// int8 components (the exact F32 product when Np * Kp > 2^27, as the
+// reference's exact route); M > 1 quantizes each row to int8 (Row A8). The
+// original weight scales are exact. Invalid arguments, another device's
+// weight, overlap or misalignment abort before any launch.
+void common_q4_matmul(CommonQ4Workspace &, int device, void * y, const CommonQ4Weight &,
+                      const void * input, int m, InputType type = InputType::f32);
+
+// A quantized snapshot of X for later common_q4_matmul_shared and
+// common_q4_matmul_pair calls (reference k200.h:306-322). The owner passes a
+// new nonzero generation after writing X; any other workspace call retires it.
+class CommonQ4ActivationLease {
+public:
+    CommonQ4ActivationLease();
+    ~CommonQ4ActivationLease();
+    CommonQ4ActivationLease(const CommonQ4ActivationLease &) = delete;
+    CommonQ4ActivationLease & operator=(const CommonQ4ActivationLease &) = delete;
+    void reset();
+    bool matches(int device, int k, int rows, InputType, uint64_t generation) const;
+    size_t chunks() const;
+    CommonQ4ActivationChunk chunk(size_t index) const;
+    struct Impl;
+private:
+    Impl * impl_;
+    friend bool common_q4_matmul_pair(CommonQ4Workspace &, int, void *, void *, const CommonQ4Weight &,
+                                      const CommonQ4Weight &, const CommonQ4ActivationLease &, uint64_t);
+    friend bool common_q4_prepare(CommonQ4Workspace &, int, const void *, int, int, InputType, uint64_t,
+                                  CommonQ4ActivationLease &);
+    friend bool common_q4_matmul_shared(CommonQ4Workspace &, int, void *, const CommonQ4Weight &,
+                                        const CommonQ4ActivationLease &, uint64_t);
+};
+// False (and a rejected call counted) for an unsupported descriptor; no launch.
+bool common_q4_prepare(CommonQ4Workspace &, int device, const void * input, int k, int rows,
+                       InputType, uint64_t generation, CommonQ4ActivationLease &);
+// False means no output was written (stale lease, wrong weight or overlap).
+bool common_q4_matmul_shared(CommonQ4Workspace &, int device, void * y, const CommonQ4Weight &,
+                             const CommonQ4ActivationLease &, uint64_t generation);
+// Gate/up pair over one prepared M = 1 F32 lease (reference k200.h:381-383,
+// src/q4-pair.inc:9-80):
+// y0 = X W0^T, y1 = X W1^T for the shapes the reference accepts (K4096 x
+// N11008, K2048 x N5632, unpadded); false with a status otherwise.
+bool common_q4_matmul_pair(CommonQ4Workspace &, int device, void * y0, void * y1, const CommonQ4Weight & w0,
+                           const CommonQ4Weight & w1, const CommonQ4ActivationLease &, uint64_t generation);
+CommonQ4PairStatistics common_q4_pair_statistics(const CommonQ4Workspace &);
+CommonQ4PairStatus common_q4_pair_last_status(const CommonQ4Workspace &);
 
 // Same layout as the reference (reference k200.h:345-350): matmul submissions
 // on devices 0 and 1, peer copy count and bytes.

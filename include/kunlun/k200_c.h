@@ -25,6 +25,17 @@ extern "C" {
 typedef struct kunlun_kernel kunlun_kernel;
 /* Opaque handle that owns one kunlun::NativeQ4Workspace (reference include/kunlun/k200.h:208-219). */
 typedef struct kunlun_native_q4_workspace kunlun_native_q4_workspace;
+/* Opaque handles owning kunlun::CommonQ4Weight, CommonQ4Workspace and
+ * CommonQ4ActivationLease (reference include/kunlun/k200.h:249-326). */
+typedef struct kunlun_common_q4_weight kunlun_common_q4_weight;
+typedef struct kunlun_common_q4_workspace kunlun_common_q4_workspace;
+typedef struct kunlun_common_q4_lease kunlun_common_q4_lease;
+/* kunlun::CommonQ4Info, same fields and types (reference include/kunlun/k200.h:227-231). */
+typedef struct {
+    uint32_t abi_version, quant_type, layout, scale_order;
+    int k, n, kp, np, device;
+    size_t scale_offset, payload_bytes;
+} kunlun_common_q4_info;
 
 /* Copy directions, same values as kunlun::CopyKind (reference include/kunlun/k200.h:18). */
 enum { KUNLUN_HOST_TO_DEVICE = 0, KUNLUN_DEVICE_TO_HOST = 1, KUNLUN_DEVICE_TO_DEVICE = 2 };
@@ -116,6 +127,56 @@ void kunlun_native_q4_statistics(const kunlun_native_q4_workspace *workspace, si
  * before returning; 1 where the reference takes its accelerated route, else 0. */
 int kunlun_native_q4_matmul(kunlun_native_q4_workspace *workspace, int device, void *y, const void *weights,
                             const void *input, int k, int n, int batch, int type);
+
+/* Common Q4 ABI v1 (reference include/kunlun/k200.h:226-335, 381-383). Each
+ * function forwards to the C++ entry of the same name; type is a
+ * KUNLUN_INPUT_* value. */
+int kunlun_common_q4_supported(int k, int n);
+size_t kunlun_common_q4_size(int k, int n);
+/* CommonQ4Weight(device, k, n, storage, bytes); storage NULL allocates. */
+kunlun_common_q4_weight *kunlun_common_q4_weight_create(int device, int k, int n, void *storage, size_t bytes);
+void kunlun_common_q4_weight_destroy(kunlun_common_q4_weight *weight);
+void kunlun_common_q4_weight_info(const kunlun_common_q4_weight *weight, kunlun_common_q4_info *out);
+void *kunlun_common_q4_weight_data(const kunlun_common_q4_weight *weight);
+void kunlun_common_q4_weight_upload(kunlun_common_q4_weight *weight, const void *q4, size_t bytes);
+/* counts = {uploads, upload_bytes}, ms = {pack_ms, upload_ms}. */
+void kunlun_common_q4_weight_statistics(const kunlun_common_q4_weight *weight, size_t counts[2], double ms[2]);
+kunlun_common_q4_workspace *kunlun_common_q4_workspace_create(void);
+void kunlun_common_q4_workspace_destroy(kunlun_common_q4_workspace *workspace);
+/* out = {paths[0..7], calls, chunks, hbm_workspace_bytes, l3_workspace_bytes, slice_bytes}. */
+void kunlun_common_q4_workspace_statistics(const kunlun_common_q4_workspace *workspace, size_t out[13]);
+/* out = {prepare_calls, quantized_chunks, quant_kernel_launches, prepared_matmuls,
+ * prepared_chunks, invalidations, rejected_calls, hbm_activation_bytes,
+ * quantization_ns, preparation_ns}. */
+void kunlun_common_q4_activation_statistics(const kunlun_common_q4_workspace *workspace, uint64_t out[10]);
+/* out = {baseline_sd_calls, stream_sd_calls, shape_fallbacks, resident_l1d_bytes}. */
+void kunlun_common_q4_mac_statistics(const kunlun_common_q4_workspace *workspace, size_t out[4]);
+/* quantization(): device pointers and {rows, kp, components}. */
+void kunlun_common_q4_quantization(const kunlun_common_q4_workspace *workspace, const void **values,
+                                   const void **scales, int out[3]);
+void kunlun_common_q4_matmul(kunlun_common_q4_workspace *workspace, int device, void *y,
+                             const kunlun_common_q4_weight *weight, const void *input, int m, int type);
+kunlun_common_q4_lease *kunlun_common_q4_lease_create(void);
+void kunlun_common_q4_lease_destroy(kunlun_common_q4_lease *lease);
+void kunlun_common_q4_lease_reset(kunlun_common_q4_lease *lease);
+int kunlun_common_q4_lease_matches(const kunlun_common_q4_lease *lease, int device, int k, int rows, int type,
+                                   uint64_t generation);
+size_t kunlun_common_q4_lease_chunks(const kunlun_common_q4_lease *lease);
+/* chunk(index): device pointers, ints = {first, rows, padded_rows, kp,
+ * components}, bytes = {values_bytes, scales_bytes}. */
+void kunlun_common_q4_lease_chunk(const kunlun_common_q4_lease *lease, size_t index, const void **values,
+                                  const void **scales, int ints[5], size_t bytes[2]);
+int kunlun_common_q4_prepare(kunlun_common_q4_workspace *workspace, int device, const void *input, int k, int rows,
+                             int type, uint64_t generation, kunlun_common_q4_lease *lease);
+int kunlun_common_q4_matmul_shared(kunlun_common_q4_workspace *workspace, int device, void *y,
+                                   const kunlun_common_q4_weight *weight, const kunlun_common_q4_lease *lease,
+                                   uint64_t generation);
+int kunlun_common_q4_matmul_pair(kunlun_common_q4_workspace *workspace, int device, void *y0, void *y1,
+                                 const kunlun_common_q4_weight *w0, const kunlun_common_q4_weight *w1,
+                                 const kunlun_common_q4_lease *lease, uint64_t generation);
+/* out = {calls, declined, l3_partial_bytes}; status as kunlun::CommonQ4PairStatus. */
+void kunlun_common_q4_pair_statistics(const kunlun_common_q4_workspace *workspace, size_t out[3]);
+int kunlun_common_q4_pair_last_status(const kunlun_common_q4_workspace *workspace);
 
 /* statistics() (reference include/kunlun/k200.h:345-349) as four counters:
  * out[0..1] = matmul submissions on devices 0 and 1, out[2] = peer copies,

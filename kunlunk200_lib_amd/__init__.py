@@ -79,6 +79,37 @@ C_FUNCTIONS = [
     ("kunlun_native_q4_statistics", None, [_c_void_p, ctypes.POINTER(_c_size)]),
     ("kunlun_native_q4_matmul", _c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
                                          _c_int]),
+    ("kunlun_common_q4_supported", _c_int, [_c_int, _c_int]),
+    ("kunlun_common_q4_size", _c_size, [_c_int, _c_int]),
+    ("kunlun_common_q4_weight_create", _c_void_p, [_c_int, _c_int, _c_int, _c_void_p, _c_size]),
+    ("kunlun_common_q4_weight_destroy", None, [_c_void_p]),
+    ("kunlun_common_q4_weight_info", None, [_c_void_p, _c_void_p]),
+    ("kunlun_common_q4_weight_data", _c_void_p, [_c_void_p]),
+    ("kunlun_common_q4_weight_upload", None, [_c_void_p, _c_void_p, _c_size]),
+    ("kunlun_common_q4_weight_statistics", None, [_c_void_p, ctypes.POINTER(_c_size), ctypes.POINTER(ctypes.c_double)]),
+    ("kunlun_common_q4_workspace_create", _c_void_p, []),
+    ("kunlun_common_q4_workspace_destroy", None, [_c_void_p]),
+    ("kunlun_common_q4_workspace_statistics", None, [_c_void_p, ctypes.POINTER(_c_size)]),
+    ("kunlun_common_q4_activation_statistics", None, [_c_void_p, ctypes.POINTER(ctypes.c_uint64)]),
+    ("kunlun_common_q4_mac_statistics", None, [_c_void_p, ctypes.POINTER(_c_size)]),
+    ("kunlun_common_q4_quantization", None, [_c_void_p, ctypes.POINTER(_c_void_p), ctypes.POINTER(_c_void_p),
+                                             ctypes.POINTER(_c_int)]),
+    ("kunlun_common_q4_matmul", None, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int]),
+    ("kunlun_common_q4_lease_create", _c_void_p, []),
+    ("kunlun_common_q4_lease_destroy", None, [_c_void_p]),
+    ("kunlun_common_q4_lease_reset", None, [_c_void_p]),
+    ("kunlun_common_q4_lease_matches", _c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_int, ctypes.c_uint64]),
+    ("kunlun_common_q4_lease_chunks", _c_size, [_c_void_p]),
+    ("kunlun_common_q4_lease_chunk", None, [_c_void_p, _c_size, ctypes.POINTER(_c_void_p), ctypes.POINTER(_c_void_p),
+                                            ctypes.POINTER(_c_int), ctypes.POINTER(_c_size)]),
+    ("kunlun_common_q4_prepare", _c_int, [_c_void_p, _c_int, _c_void_p, _c_int, _c_int, _c_int, ctypes.c_uint64,
+                                          _c_void_p]),
+    ("kunlun_common_q4_matmul_shared", _c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p,
+                                                ctypes.c_uint64]),
+    ("kunlun_common_q4_matmul_pair", _c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                              _c_void_p, ctypes.c_uint64]),
+    ("kunlun_common_q4_pair_statistics", None, [_c_void_p, ctypes.POINTER(_c_size)]),
+    ("kunlun_common_q4_pair_last_status", _c_int, [_c_void_p]),
 ]
 
 
@@ -416,6 +447,173 @@ def native_q4_matmul(workspace: NativeQ4Workspace, device: int, y, weights, x, k
     True where the reference takes its accelerated route (reference k200.h:223-224)."""
     return bool(load().kunlun_native_q4_matmul(workspace.handle, int(device), _ptr(y), _ptr(weights), _ptr(x),
                                                int(k), int(n), int(batch), int(type)))
+
+
+def common_q4_supported(k: int, n: int) -> bool:
+    """reference k200.h:232"""
+    return bool(load().kunlun_common_q4_supported(int(k), int(n)))
+
+
+def common_q4_size(k: int, n: int) -> int:
+    """Payload bytes of the common Q4 ABI v1 layout, 0 when unsupported (reference k200.h:233)."""
+    return load().kunlun_common_q4_size(int(k), int(n))
+
+
+class _CommonQ4InfoC(ctypes.Structure):
+    _fields_ = [("abi_version", ctypes.c_uint32), ("quant_type", ctypes.c_uint32), ("layout", ctypes.c_uint32),
+                ("scale_order", ctypes.c_uint32), ("k", _c_int), ("n", _c_int), ("kp", _c_int), ("np", _c_int),
+                ("device", _c_int), ("scale_offset", _c_size), ("payload_bytes", _c_size)]
+
+
+class CommonQ4PairStatus(enum.IntEnum):
+    """reference k200.h:285"""
+    NotAttempted = 0
+    Success = 1
+    Disabled = 2
+    InvalidInput = 3
+    Configuration = 4
+    WeightAbi = 5
+    Lease = 6
+    Alias = 7
+    Workspace = 8
+
+
+class _Handle:
+    _destroy = ""
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            getattr(load(), self._destroy)(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class CommonQ4Weight(_Handle):
+    """Common Q4 ABI v1 weight on one device (reference k200.h:249-268)."""
+    _destroy = "kunlun_common_q4_weight_destroy"
+
+    def __init__(self, device: int, k: int, n: int, storage=None, nbytes: int = 0):
+        self.handle = load().kunlun_common_q4_weight_create(int(device), int(k), int(n), _ptr(storage), int(nbytes))
+        require(bool(self.handle))
+
+    def info(self) -> dict:
+        out = _CommonQ4InfoC()
+        load().kunlun_common_q4_weight_info(self.handle, ctypes.byref(out))
+        return {name: getattr(out, name) for name, _ in out._fields_}
+
+    def data(self) -> int:
+        return load().kunlun_common_q4_weight_data(self.handle)
+
+    def upload(self, q4: np.ndarray) -> None:
+        q4 = np.ascontiguousarray(q4, dtype=np.uint8)
+        load().kunlun_common_q4_weight_upload(self.handle, q4.ctypes.data, q4.nbytes)
+
+    def statistics(self) -> dict:
+        counts, ms = (_c_size * 2)(), (ctypes.c_double * 2)()
+        load().kunlun_common_q4_weight_statistics(self.handle, counts, ms)
+        return {"uploads": counts[0], "upload_bytes": counts[1], "pack_ms": ms[0], "upload_ms": ms[1]}
+
+
+class CommonQ4Workspace(_Handle):
+    """Per-device state of the common Q4 calls (reference k200.h:286-303)."""
+    _destroy = "kunlun_common_q4_workspace_destroy"
+
+    def __init__(self):
+        self.handle = load().kunlun_common_q4_workspace_create()
+        require(bool(self.handle))
+
+    def statistics(self) -> dict:
+        out = (_c_size * 13)()
+        load().kunlun_common_q4_workspace_statistics(self.handle, out)
+        return {"paths": list(out[0:8]), "calls": out[8], "chunks": out[9], "hbm_workspace_bytes": out[10],
+                "l3_workspace_bytes": out[11], "slice_bytes": out[12]}
+
+    def activation_statistics(self) -> dict:
+        out = (ctypes.c_uint64 * 10)()
+        load().kunlun_common_q4_activation_statistics(self.handle, out)
+        names = ("prepare_calls", "quantized_chunks", "quant_kernel_launches", "prepared_matmuls", "prepared_chunks",
+                 "invalidations", "rejected_calls", "hbm_activation_bytes", "quantization_ns", "preparation_ns")
+        return dict(zip(names, list(out)))
+
+    def mac_statistics(self) -> dict:
+        out = (_c_size * 4)()
+        load().kunlun_common_q4_mac_statistics(self.handle, out)
+        return dict(zip(("baseline_sd_calls", "stream_sd_calls", "shape_fallbacks", "resident_l1d_bytes"), list(out)))
+
+    def quantization(self) -> dict:
+        values, scales, ints = _c_void_p(), _c_void_p(), (_c_int * 3)()
+        load().kunlun_common_q4_quantization(self.handle, ctypes.byref(values), ctypes.byref(scales), ints)
+        return {"values": values.value or 0, "scales": scales.value or 0, "rows": ints[0], "kp": ints[1],
+                "components": ints[2]}
+
+
+class CommonQ4ActivationLease(_Handle):
+    """Quantized activation snapshot (reference k200.h:306-322)."""
+    _destroy = "kunlun_common_q4_lease_destroy"
+
+    def __init__(self):
+        self.handle = load().kunlun_common_q4_lease_create()
+        require(bool(self.handle))
+
+    def reset(self) -> None:
+        load().kunlun_common_q4_lease_reset(self.handle)
+
+    def matches(self, device: int, k: int, rows: int, type: InputType, generation: int) -> bool:
+        return bool(load().kunlun_common_q4_lease_matches(self.handle, int(device), int(k), int(rows), int(type),
+                                                          int(generation)))
+
+    def chunks(self) -> int:
+        return load().kunlun_common_q4_lease_chunks(self.handle)
+
+    def chunk(self, index: int) -> dict:
+        values, scales, ints, nbytes = _c_void_p(), _c_void_p(), (_c_int * 5)(), (_c_size * 2)()
+        load().kunlun_common_q4_lease_chunk(self.handle, int(index), ctypes.byref(values), ctypes.byref(scales),
+                                            ints, nbytes)
+        return {"values": values.value or 0, "scales": scales.value or 0, "first": ints[0], "rows": ints[1],
+                "padded_rows": ints[2], "kp": ints[3], "components": ints[4], "values_bytes": nbytes[0],
+                "scales_bytes": nbytes[1]}
+
+
+def common_q4_matmul(workspace: CommonQ4Workspace, device: int, y, weight: CommonQ4Weight, x, m: int,
+                     type: InputType = InputType.f32) -> None:
+    """Y[m,n] = X W^T, completed before returning (reference k200.h:300-302)."""
+    load().kunlun_common_q4_matmul(workspace.handle, int(device), _ptr(y), weight.handle, _ptr(x), int(m), int(type))
+
+
+def common_q4_prepare(workspace: CommonQ4Workspace, device: int, x, k: int, rows: int, type: InputType,
+                      generation: int, lease: CommonQ4ActivationLease) -> bool:
+    """reference k200.h:327-328"""
+    return bool(load().kunlun_common_q4_prepare(workspace.handle, int(device), _ptr(x), int(k), int(rows), int(type),
+                                                int(generation), lease.handle))
+
+
+def common_q4_matmul_shared(workspace: CommonQ4Workspace, device: int, y, weight: CommonQ4Weight,
+                            lease: CommonQ4ActivationLease, generation: int) -> bool:
+    """reference k200.h:331-332"""
+    return bool(load().kunlun_common_q4_matmul_shared(workspace.handle, int(device), _ptr(y), weight.handle,
+                                                      lease.handle, int(generation)))
+
+
+def common_q4_matmul_pair(workspace: CommonQ4Workspace, device: int, y0, y1, w0: CommonQ4Weight,
+                          w1: CommonQ4Weight, lease: CommonQ4ActivationLease, generation: int) -> bool:
+    """reference k200.h:381"""
+    return bool(load().kunlun_common_q4_matmul_pair(workspace.handle, int(device), _ptr(y0), _ptr(y1), w0.handle,
+                                                    w1.handle, lease.handle, int(generation)))
+
+
+def common_q4_pair_statistics(workspace: CommonQ4Workspace) -> dict:
+    out = (_c_size * 3)()
+    load().kunlun_common_q4_pair_statistics(workspace.handle, out)
+    return {"calls": out[0], "declined": out[1], "l3_partial_bytes": out[2]}
+
+
+def common_q4_pair_last_status(workspace: CommonQ4Workspace) -> CommonQ4PairStatus:
+    return CommonQ4PairStatus(load().kunlun_common_q4_pair_last_status(workspace.handle))
 
 
 def statistics() -> dict:

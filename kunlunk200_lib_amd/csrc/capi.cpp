@@ -13,6 +13,18 @@ struct kunlun_native_q4_workspace {
     kunlun::NativeQ4Workspace workspace;
 };
 
+struct kunlun_common_q4_weight {
+    kunlun::CommonQ4Weight weight;
+    kunlun_common_q4_weight(int device, int k, int n, void * storage, size_t bytes)
+        : weight(device, k, n, storage, bytes) {}
+};
+struct kunlun_common_q4_workspace {
+    kunlun::CommonQ4Workspace workspace;
+};
+struct kunlun_common_q4_lease {
+    kunlun::CommonQ4ActivationLease lease;
+};
+
 namespace {
 kunlun::InputType input_type(int type) {
     kunlun::require(type == KUNLUN_INPUT_F32 || type == KUNLUN_INPUT_F16);
@@ -94,6 +106,142 @@ int kunlun_native_q4_matmul(kunlun_native_q4_workspace * workspace, int device, 
     kunlun::require(workspace != nullptr);
     return kunlun::native_q4_matmul(workspace->workspace, device, y, weights, input, k, n, batch,
                                     input_type(type)) ? 1 : 0;
+}
+
+int kunlun_common_q4_supported(int k, int n) { return kunlun::common_q4_supported(k, n) ? 1 : 0; }
+size_t kunlun_common_q4_size(int k, int n) { return kunlun::common_q4_size(k, n); }
+kunlun_common_q4_weight * kunlun_common_q4_weight_create(int device, int k, int n, void * storage, size_t bytes) {
+    return new kunlun_common_q4_weight(device, k, n, storage, bytes);
+}
+void kunlun_common_q4_weight_destroy(kunlun_common_q4_weight * weight) { delete weight; }
+void kunlun_common_q4_weight_info(const kunlun_common_q4_weight * weight, kunlun_common_q4_info * out) {
+    kunlun::require(weight && out);
+    const kunlun::CommonQ4Info a = weight->weight.info();
+    *out = {a.abi_version, a.quant_type, a.layout, a.scale_order, a.k, a.n, a.kp, a.np, a.device, a.scale_offset,
+            a.payload_bytes};
+}
+void * kunlun_common_q4_weight_data(const kunlun_common_q4_weight * weight) {
+    kunlun::require(weight != nullptr);
+    return weight->weight.data();
+}
+void kunlun_common_q4_weight_upload(kunlun_common_q4_weight * weight, const void * q4, size_t bytes) {
+    kunlun::require(weight != nullptr);
+    weight->weight.upload(q4, bytes);
+}
+void kunlun_common_q4_weight_statistics(const kunlun_common_q4_weight * weight, size_t counts[2], double ms[2]) {
+    kunlun::require(weight && counts && ms);
+    const kunlun::CommonQ4WeightStatistics s = weight->weight.statistics();
+    counts[0] = s.uploads;
+    counts[1] = s.upload_bytes;
+    ms[0] = s.pack_ms;
+    ms[1] = s.upload_ms;
+}
+kunlun_common_q4_workspace * kunlun_common_q4_workspace_create(void) { return new kunlun_common_q4_workspace(); }
+void kunlun_common_q4_workspace_destroy(kunlun_common_q4_workspace * workspace) { delete workspace; }
+void kunlun_common_q4_workspace_statistics(const kunlun_common_q4_workspace * workspace, size_t out[13]) {
+    kunlun::require(workspace && out);
+    const kunlun::CommonQ4Statistics s = workspace->workspace.statistics();
+    for (int i = 0; i < 8; ++i) out[i] = s.paths[i];
+    out[8] = s.calls;
+    out[9] = s.chunks;
+    out[10] = s.hbm_workspace_bytes;
+    out[11] = s.l3_workspace_bytes;
+    out[12] = s.slice_bytes;
+}
+void kunlun_common_q4_activation_statistics(const kunlun_common_q4_workspace * workspace, uint64_t out[10]) {
+    kunlun::require(workspace && out);
+    const kunlun::CommonQ4ActivationStatistics s = workspace->workspace.activation_statistics();
+    const uint64_t v[10] = {s.prepare_calls, s.quantized_chunks, s.quant_kernel_launches, s.prepared_matmuls,
+                            s.prepared_chunks, s.invalidations, s.rejected_calls, s.hbm_activation_bytes,
+                            s.quantization_ns, s.preparation_ns};
+    for (int i = 0; i < 10; ++i) out[i] = v[i];
+}
+void kunlun_common_q4_mac_statistics(const kunlun_common_q4_workspace * workspace, size_t out[4]) {
+    kunlun::require(workspace && out);
+    const kunlun::CommonQ4MacStatistics s = workspace->workspace.mac_statistics();
+    out[0] = s.baseline_sd_calls;
+    out[1] = s.stream_sd_calls;
+    out[2] = s.shape_fallbacks;
+    out[3] = s.resident_l1d_bytes;
+}
+void kunlun_common_q4_quantization(const kunlun_common_q4_workspace * workspace, const void ** values,
+                                   const void ** scales, int out[3]) {
+    kunlun::require(workspace && values && scales && out);
+    const kunlun::CommonQ4Quantization q = workspace->workspace.quantization();
+    *values = q.values;
+    *scales = q.scales;
+    out[0] = q.rows;
+    out[1] = q.kp;
+    out[2] = q.components;
+}
+void kunlun_common_q4_matmul(kunlun_common_q4_workspace * workspace, int device, void * y,
+                             const kunlun_common_q4_weight * weight, const void * input, int m, int type) {
+    kunlun::require(workspace && weight);
+    kunlun::common_q4_matmul(workspace->workspace, device, y, weight->weight, input, m, input_type(type));
+}
+kunlun_common_q4_lease * kunlun_common_q4_lease_create(void) { return new kunlun_common_q4_lease(); }
+void kunlun_common_q4_lease_destroy(kunlun_common_q4_lease * lease) { delete lease; }
+void kunlun_common_q4_lease_reset(kunlun_common_q4_lease * lease) {
+    kunlun::require(lease != nullptr);
+    lease->lease.reset();
+}
+int kunlun_common_q4_lease_matches(const kunlun_common_q4_lease * lease, int device, int k, int rows, int type,
+                                   uint64_t generation) {
+    kunlun::require(lease != nullptr);
+    if (type != KUNLUN_INPUT_F32 && type != KUNLUN_INPUT_F16) return 0;
+    return lease->lease.matches(device, k, rows, input_type(type), generation) ? 1 : 0;
+}
+size_t kunlun_common_q4_lease_chunks(const kunlun_common_q4_lease * lease) {
+    kunlun::require(lease != nullptr);
+    return lease->lease.chunks();
+}
+void kunlun_common_q4_lease_chunk(const kunlun_common_q4_lease * lease, size_t index, const void ** values,
+                                  const void ** scales, int ints[5], size_t bytes[2]) {
+    kunlun::require(lease && values && scales && ints && bytes);
+    const kunlun::CommonQ4ActivationChunk c = lease->lease.chunk(index);
+    *values = c.values;
+    *scales = c.scales;
+    ints[0] = c.first;
+    ints[1] = c.rows;
+    ints[2] = c.padded_rows;
+    ints[3] = c.kp;
+    ints[4] = c.components;
+    bytes[0] = c.values_bytes;
+    bytes[1] = c.scales_bytes;
+}
+int kunlun_common_q4_prepare(kunlun_common_q4_workspace * workspace, int device, const void * input, int k,
+                             int rows, int type, uint64_t generation, kunlun_common_q4_lease * lease) {
+    kunlun::require(workspace && lease);
+    const kunlun::InputType t = type == KUNLUN_INPUT_F16 ? kunlun::InputType::f16
+                                : type == KUNLUN_INPUT_F32 ? kunlun::InputType::f32
+                                                           : static_cast<kunlun::InputType>(type);
+    return kunlun::common_q4_prepare(workspace->workspace, device, input, k, rows, t, generation, lease->lease) ? 1
+                                                                                                                 : 0;
+}
+int kunlun_common_q4_matmul_shared(kunlun_common_q4_workspace * workspace, int device, void * y,
+                                   const kunlun_common_q4_weight * weight, const kunlun_common_q4_lease * lease,
+                                   uint64_t generation) {
+    kunlun::require(workspace && weight && lease);
+    return kunlun::common_q4_matmul_shared(workspace->workspace, device, y, weight->weight, lease->lease,
+                                           generation) ? 1 : 0;
+}
+int kunlun_common_q4_matmul_pair(kunlun_common_q4_workspace * workspace, int device, void * y0, void * y1,
+                                 const kunlun_common_q4_weight * w0, const kunlun_common_q4_weight * w1,
+                                 const kunlun_common_q4_lease * lease, uint64_t generation) {
+    kunlun::require(workspace && w0 && w1 && lease);
+    return kunlun::common_q4_matmul_pair(workspace->workspace, device, y0, y1, w0->weight, w1->weight, lease->lease,
+                                         generation) ? 1 : 0;
+}
+void kunlun_common_q4_pair_statistics(const kunlun_common_q4_workspace * workspace, size_t out[3]) {
+    kunlun::require(workspace && out);
+    const kunlun::CommonQ4PairStatistics s = kunlun::common_q4_pair_statistics(workspace->workspace);
+    out[0] = s.calls;
+    out[1] = s.declined;
+    out[2] = s.l3_partial_bytes;
+}
+int kunlun_common_q4_pair_last_status(const kunlun_common_q4_workspace * workspace) {
+    kunlun::require(workspace != nullptr);
+    return static_cast<int>(kunlun::common_q4_pair_last_status(workspace->workspace));
 }
 
 void kunlun_statistics(size_t out[4]) {

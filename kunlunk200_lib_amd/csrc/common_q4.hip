@@ -1,0 +1,483 @@
+// Common Q4 ABI v1 kernels (reference src/q4-common.inc, src/q4-activation.inc,
+// src/q4-pair.inc; persistent layout src/q4-common-pack.h:16-31) on gfx950.
+//
+// Weight layout (layout 1 "Micro32Bank", scale order 1 "KMajor"): for output
+// column c and K32 block b the 16 bytes of signed nibble pairs (K 2p low,
+// 2p + 1 high) of that column's block are contiguous at
+// ((c/32) * (Kp/32) + b) * 512 + (c%16) * 32 + ((c%32)/16) * 16, so one 16-byte
+// load gives a lane 32 K values of one column in natural order; the FP16
+// scales are [b][Np] after the weights.
+//
+// Activations are quantized as the reference does (reference
+// kernels/kunlun-common-{max,main,residual}-exact.xpu, quant-row-serial):
+//   M = 1: per tensor, two int8 components: max0 = max|x| (1 if 0),
+//          q0 = rnd(x * (127/max0)), r = x - q0 * (max0/127), q1 the same on r;
+//   M > 1: per row, one component q = rnd(x * (127/max_row)).
+// rnd rounds half away from zero and clamps to [-127, 127]. Products with the
+// weights are exact int32 block sums (v_dot4_i32_i8 / v_mfma_i32_16x16x32_i8
+// on weights widened to 16*q), then y = sum_b d_b * (S0 s0 + S1 s1) in F32.
+#include "device_common.h"
+#include "launch.h"
+
+#include <algorithm>
+
+namespace {
+
+constexpr int kCqWaves = 8;
+constexpr int kCqThreads = 64 * kCqWaves;
+constexpr int kCqDepth = 4;            // GEMV items (block pairs) in flight per wave
+constexpr int kQuantThreads = 1024;    // single-workgroup per-tensor quantization
+constexpr int kRowThreads = 256;       // Row A8: one workgroup per row
+
+typedef int int32x4 __attribute__((ext_vector_type(4)));
+
+// Max of |x| bit patterns over the workgroup (NaN above Inf, as the
+// reference's integer max); every thread gets the result.
+template <int Threads>
+__device__ uint32_t block_max_bits(uint32_t v, uint32_t *scratch) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), offset, kk::kWave)));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+    __syncthreads();
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < Threads / 64; ++i) m = max(m, scratch[i]);
+    return m;
+}
+
+__device__ __forceinline__ float load_value(const void *x, int x_f16, size_t i) {
+    return x_f16 ? kk::half_bits_to_float(static_cast<const uint16_t *>(x)[i]) : static_cast<const float *>(x)[i];
+}
+
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+    return (static_cast<uint32_t>(a) & 255u) | ((static_cast<uint32_t>(b) & 255u) << 8) |
+           ((static_cast<uint32_t>(c) & 255u) << 16) | (static_cast<uint32_t>(d) << 24);
+}
+
+// ---------------------------------------------------------------------------
+// M = 1: two-component per-tensor quantization into the reference's view:
+// main code of K j at values[(j/32)*64 + j%32], residual at values[2kp + ...],
+// the other 32 bytes of each 64-byte group and values[4kp .. 4kp+1024) zero;
+// params = {max0/127, max1/127, max0, max1, 0 ...} (16 floats).
+// One workgroup; thread t owns groups of 8 values g = t + 1024 i.
+__global__ __launch_bounds__(kQuantThreads) void common_quant_pair(const void *__restrict__ x, int x_f16, int k,
+                                                                  int kp, int8_t *__restrict__ values,
+                                                                  float *__restrict__ params) {
+#pragma clang fp contract(off)
+    __shared__ uint32_t scratch[kQuantThreads / 64];
+    constexpr int kMaxGroups = 2;              // kp <= 16384 = 2 * 1024 * 8
+    const int groups = kp / 8;
+    float v[kMaxGroups][8];
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxGroups; ++i) {
+        const int g = threadIdx.x + kQuantThreads * i;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int j = 8 * g + t;
+            v[i][t] = (g < groups && j < k) ? load_value(x, x_f16, j) : 0.0f;
+            m = max(m, __float_as_uint(v[i][t]) & 0x7fffffffu);
+        }
+    }
+    m = block_max_bits<kQuantThreads>(m, scratch);
+    const float max0 = m ? __uint_as_float(m) : 1.0f;
+    const float s0 = max0 / 127.0f, inv0 = 127.0f / max0;
+    int q0[kMaxGroups][8];
+    uint32_t m1 = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxGroups; ++i)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const float scaled = v[i][t] * inv0;
+            q0[i][t] = kk::round_clamp(scaled, 127);
+            const float back = static_cast<float>(q0[i][t]) * s0;
+            v[i][t] = v[i][t] - back;                       // residual
+            m1 = max(m1, __float_as_uint(v[i][t]) & 0x7fffffffu);
+        }
+    m1 = block_max_bits<kQuantThreads>(m1, scratch);
+    const float max1 = m1 ? __uint_as_float(m1) : 1.0f;
+    const float s1 = max1 / 127.0f, inv1 = 127.0f / max1;
+#pragma unroll
+    for (int i = 0; i < kMaxGroups; ++i) {
+        const int g = threadIdx.x + kQuantThreads * i;
+        if (g >= groups) continue;
+        int q1[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) q1[t] = kk::round_clamp(v[i][t] * inv1, 127);
+        const size_t at = static_cast<size_t>(g / 4) * 64 + (g % 4) * 8;
+        uint32_t *main = reinterpret_cast<uint32_t *>(values + at);
+        uint32_t *resid = reinterpret_cast<uint32_t *>(values + 2 * static_cast<size_t>(kp) + at);
+        main[0] = pack4(q0[i][0], q0[i][1], q0[i][2], q0[i][3]);
+        main[1] = pack4(q0[i][4], q0[i][5], q0[i][6], q0[i][7]);
+        main[8] = 0;                          // bytes at + 32 .. + 40: the group's gap
+        main[9] = 0;
+        resid[0] = pack4(q1[0], q1[1], q1[2], q1[3]);
+        resid[1] = pack4(q1[4], q1[5], q1[6], q1[7]);
+        resid[8] = 0;
+        resid[9] = 0;
+    }
+    if (threadIdx.x < 256) reinterpret_cast<uint32_t *>(values + 4 * static_cast<size_t>(kp))[threadIdx.x] = 0;
+    if (threadIdx.x < 16) {
+        const float p[4] = {s0, s1, max0, max1};
+        params[threadIdx.x] = threadIdx.x < 4 ? p[threadIdx.x] : 0.0f;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// M > 1: Row A8. Workgroup r quantizes row r of X (rows >= `rows` are the
+// zero padding rows: scale 1/127, codes 0) into values[r*kp ..] and writes the
+// row scale to all 16 floats of params[r*16 ..].
+__global__ __launch_bounds__(kRowThreads) void common_quant_rows(const void *__restrict__ x, int x_f16, int k,
+                                                                int kp, int rows, int8_t *__restrict__ values,
+                                                                float *__restrict__ params) {
+#pragma clang fp contract(off)
+    __shared__ uint32_t scratch[kRowThreads / 64];
+    const int row = blockIdx.x;
+    const bool real = row < rows;
+    const size_t base = static_cast<size_t>(row) * k;
+    uint32_t m = 0;
+    for (int j = threadIdx.x; j < k && real; j += kRowThreads)
+        m = max(m, __float_as_uint(load_value(x, x_f16, base + j)) & 0x7fffffffu);
+    m = block_max_bits<kRowThreads>(m, scratch);
+    const float mx = m ? __uint_as_float(m) : 1.0f;
+    const float scale = mx / 127.0f, inv = 127.0f / mx;
+    // four values per thread per step, written as one dword
+    uint32_t *out = reinterpret_cast<uint32_t *>(values + static_cast<size_t>(row) * kp);
+    for (int d = threadIdx.x; d < kp / 4; d += kRowThreads) {
+        int q[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int j = 4 * d + t;
+            const float v = (real && j < k) ? load_value(x, x_f16, base + j) : 0.0f;
+            q[t] = kk::round_clamp(v * inv, 127);
+        }
+        out[d] = pack4(q[0], q[1], q[2], q[3]);
+    }
+    if (threadIdx.x < 16) params[row * 16 + threadIdx.x] = scale;
+}
+
+// ---------------------------------------------------------------------------
+// M = 1 GEMV over one or two weights (the gate/up pair shares the
+// activations). Workgroup = one N32 tile of one weight; its 8 waves take block
+// pairs in turn. In an item (blocks 2i, 2i+1) lane l loads the 16 bytes of
+// column 16 (c%2) + c/2 (c = l%32) of block 2i + l/32: the wave reads 1 KB
+// contiguous. A8 (EXACT false): activation per block in LDS as 16 dwords
+// [component][even K, odd K][4]; the weight dword w gives 16*q of the even K
+// as (w << 4) & 0xf0f0f0f0 and of the odd K as w & 0xf0f0f0f0, so
+// v_dot4_i32_i8 yields 16 * sum q x_q exactly. EXACT: the activations are
+// 23-bit block fixed point digits (kk::fixed_point_digits) and v_dot8_i32_i4
+// takes the weight dwords as they are (natural K order).
+struct GemvMatrix {
+    const uint8_t *w;
+    float *y;
+};
+
+template <bool EXACT>
+__global__ __launch_bounds__(kCqThreads) void common_gemv(GemvMatrix m0, GemvMatrix m1, int tiles_per_matrix,
+                                                         const void *__restrict__ act, int x_f16,
+                                                         const float *__restrict__ params, int k, int kp, int n,
+                                                         int np) {
+    extern __shared__ uint4 lds4[];
+    const int which = blockIdx.x / tiles_per_matrix;
+    const int tile = blockIdx.x - which * tiles_per_matrix;
+    const GemvMatrix mat = which ? m1 : m0;
+    const int blocks = kp >> 5;
+    const int pairs = blocks >> 1;
+    const uint16_t *scales = reinterpret_cast<const uint16_t *>(mat.w + static_cast<size_t>(np) * kp / 2);
+    constexpr int kBlockWords = EXACT ? 24 : 16;
+    uint32_t *act_lds = reinterpret_cast<uint32_t *>(lds4);                       // [blocks][kBlockWords]
+    float *block_scale = reinterpret_cast<float *>(act_lds + static_cast<size_t>(blocks) * kBlockWords);  // EXACT
+    float *partial = block_scale + (EXACT ? blocks : 0);                         // [waves][32]
+
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+    const int chunk = lane & 31;
+    const int col = tile * 32 + 16 * (chunk & 1) + (chunk >> 1);
+    const size_t tile_block0 = static_cast<size_t>(tile) * blocks;
+
+    // 1. activation loads (before the weights: the memory counter is in order)
+    constexpr int kMaxPasses = 4;              // kp / 8 <= 2048 groups = 4 x 512 threads
+    const int groups = kp / 8;
+    uint32_t raw[kMaxPasses][4];
+    float xv[kMaxPasses][8];
+#pragma unroll
+    for (int pass = 0; pass < kMaxPasses; ++pass) {
+        const int g = min(pass * kCqThreads + static_cast<int>(threadIdx.x), groups - 1);
+        if (EXACT) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const int j = 8 * g + t;
+                xv[pass][t] = j < k ? load_value(act, x_f16, j) : 0.0f;
+            }
+        } else {
+            const int8_t *codes = static_cast<const int8_t *>(act);
+            const size_t at = static_cast<size_t>(g / 4) * 64 + (g % 4) * 8;
+            const uint2 a = *reinterpret_cast<const uint2 *>(codes + at);
+            const uint2 b = *reinterpret_cast<const uint2 *>(codes + 2 * static_cast<size_t>(kp) + at);
+            raw[pass][0] = a.x;
+            raw[pass][1] = a.y;
+            raw[pass][2] = b.x;
+            raw[pass][3] = b.y;
+        }
+    }
+    float s0 = 0.0f, s1 = 0.0f;
+    if (!EXACT) {
+        s0 = params[0] * 0.0625f;              // the weights enter as 16 * q
+        s1 = params[1] * 0.0625f;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. the first weight items
+    auto load_item = [&](int s, uint32_t (&buf)[5]) {
+        const int it = min(wid + kCqWaves * s, pairs - 1);
+        const int blk = 2 * it + (lane >> 5);
+        const uint4 v = *reinterpret_cast<const uint4 *>(mat.w + (tile_block0 + blk) * 512 + chunk * 16);
+        buf[0] = v.x;
+        buf[1] = v.y;
+        buf[2] = v.z;
+        buf[3] = v.w;
+        buf[4] = scales[static_cast<size_t>(blk) * np + min(col, np - 1)];
+    };
+    const int my_items = wid < pairs ? (pairs - wid + kCqWaves - 1) / kCqWaves : 0;
+    uint32_t ring[kCqDepth][5];
+#pragma unroll
+    for (int d = 0; d < kCqDepth; ++d) {
+        load_item(d, ring[d]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // 3. activations -> LDS
+#pragma unroll
+    for (int pass = 0; pass < kMaxPasses; ++pass) {
+        const int idx = pass * kCqThreads + static_cast<int>(threadIdx.x);
+        const int g = min(idx, groups - 1);
+        if (EXACT) {
+            float m = 0.0f, bad = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const float a = fabsf(xv[pass][t]);
+                bad = (a <= 3.402823466e38f) ? bad : 1.0f;
+                m = fmaxf(m, a);
+            }
+            m = fmaxf(m, kk::dpp_move<0xb1>(m));        // the 4 groups of a block: one quad
+            m = fmaxf(m, kk::dpp_move<0x4e>(m));
+            bad = fmaxf(bad, kk::dpp_move<0xb1>(bad));
+            bad = fmaxf(bad, kk::dpp_move<0x4e>(bad));
+            const int e = max(__builtin_amdgcn_frexp_expf(m), -100);
+            uint32_t dig[6];
+            kk::fixed_point_digits(xv[pass], ldexpf(1.0f, 22 - e), dig);
+            if (idx < groups) {
+#pragma unroll
+                for (int l = 0; l < 6; ++l) act_lds[(g / 4) * 24 + (g % 4) * 6 + l] = dig[l];
+                if ((g & 3) == 0) block_scale[g / 4] = bad != 0.0f ? __builtin_nanf("") : ldexpf(1.0f, e - 22);
+            }
+        } else if (idx < groups) {
+            // even K: bytes 0, 2 of each dword; odd K: bytes 1, 3
+            uint32_t *dst = act_lds + (g / 4) * 16 + (g % 4);
+            dst[0] = __builtin_amdgcn_perm(raw[pass][1], raw[pass][0], 0x06040200u);
+            dst[4] = __builtin_amdgcn_perm(raw[pass][1], raw[pass][0], 0x07050301u);
+            dst[8] = __builtin_amdgcn_perm(raw[pass][3], raw[pass][2], 0x06040200u);
+            dst[12] = __builtin_amdgcn_perm(raw[pass][3], raw[pass][2], 0x07050301u);
+        }
+    }
+    __syncthreads();
+
+    // 4. items
+    float acc = 0.0f;
+    auto compute_item = [&](int s, const uint32_t (&buf)[5]) {
+        const int blk = 2 * (wid + kCqWaves * s) + (lane >> 5);
+        const float d = col < n ? kk::half_bits_to_float(buf[4]) : 0.0f;
+        if (EXACT) {
+            const uint4 *src = reinterpret_cast<const uint4 *>(act_lds + static_cast<size_t>(blk) * 24);
+            uint32_t dg[24];
+#pragma unroll
+            for (int g = 0; g < 6; ++g) {
+                const uint4 v4 = src[g];
+                dg[4 * g] = v4.x;
+                dg[4 * g + 1] = v4.y;
+                dg[4 * g + 2] = v4.z;
+                dg[4 * g + 3] = v4.w;
+            }
+            int t[6];
+#pragma unroll
+            for (int l = 0; l < 6; ++l) {
+                t[l] = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    t[l] = __builtin_amdgcn_sdot8(static_cast<int>(buf[i]), static_cast<int>(dg[i * 6 + l]), t[l], false);
+            }
+            int sum = t[5];
+#pragma unroll
+            for (int l = 4; l >= 0; --l) sum = (sum << 4) + t[l];
+            acc = fmaf(static_cast<float>(sum), col < n ? d * block_scale[blk] : 0.0f, acc);
+        } else {
+            const uint4 *src = reinterpret_cast<const uint4 *>(act_lds + static_cast<size_t>(blk) * 16);
+            const uint4 e0 = src[0], o0 = src[1], e1 = src[2], o1 = src[3];
+            const uint32_t a0e[4] = {e0.x, e0.y, e0.z, e0.w}, a0o[4] = {o0.x, o0.y, o0.z, o0.w};
+            const uint32_t a1e[4] = {e1.x, e1.y, e1.z, e1.w}, a1o[4] = {o1.x, o1.y, o1.z, o1.w};
+            int p0 = 0, p1 = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int ev = static_cast<int>((buf[i] << 4) & 0xf0f0f0f0u);
+                const int od = static_cast<int>(buf[i] & 0xf0f0f0f0u);
+                p0 = __builtin_amdgcn_sdot4(ev, static_cast<int>(a0e[i]), p0, false);
+                p0 = __builtin_amdgcn_sdot4(od, static_cast<int>(a0o[i]), p0, false);
+                p1 = __builtin_amdgcn_sdot4(ev, static_cast<int>(a1e[i]), p1, false);
+                p1 = __builtin_amdgcn_sdot4(od, static_cast<int>(a1o[i]), p1, false);
+            }
+            const float t = fmaf(static_cast<float>(p0), s0, static_cast<float>(p1) * s1);
+            acc = fmaf(d, t, acc);
+        }
+    };
+    for (int base = 0; base < my_items; base += kCqDepth) {
+#pragma unroll
+        for (int dpt = 0; dpt < kCqDepth; ++dpt) {
+            const int s = base + dpt;
+            if (s < my_items) {
+                compute_item(s, ring[dpt]);
+                if (s + kCqDepth < my_items) load_item(s + kCqDepth, ring[dpt]);
+            }
+        }
+    }
+
+    // 5. column sums: the two block halves of the wave, then the waves in order
+    acc += __shfl_xor(acc, 32, kk::kWave);
+    if (lane < 32) partial[wid * 32 + chunk] = acc;
+    __syncthreads();
+    if (threadIdx.x < 32) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kCqWaves; ++w) v += partial[w * 32 + threadIdx.x];
+        const int c = tile * 32 + 16 * (threadIdx.x & 1) + (threadIdx.x >> 1);
+        if (c < n) mat.y[c] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// M > 1 GEMM on v_mfma_i32_16x16x32_i8 (one K32 block per MFMA, so each
+// block's int32 sums get their own FP16 scale). Workgroup = one N32 tile (two
+// 16-column groups) x up to 128 rows: wave w owns rows 32w .. 32w+31 (two
+// 16-row tiles). Operand layout (wave64): A[l%16][8(l/16) .. +8),
+// B[8(l/16) .. +8)[l%16], D[4(l/16) + r][l%16]. B lane l: column 16g + l%16
+// of the tile, K dword l/16 of the block, widened to 8 int8 = 16 * q.
+__global__ __launch_bounds__(256) void common_gemm(const uint8_t *__restrict__ w, const int8_t *__restrict__ codes,
+                                                  const float *__restrict__ row_scales, float *__restrict__ y,
+                                                  int rows, int defined_rows, int kp, int n, int np) {
+    const int lane = threadIdx.x & 63;
+    const int wid = threadIdx.x >> 6;
+    const int tile = blockIdx.x;
+    const int row0 = 32 * wid;
+    if (row0 >= defined_rows) return;           // no barrier in this kernel
+    const int blocks = kp >> 5;
+    const uint16_t *scales = reinterpret_cast<const uint16_t *>(w + static_cast<size_t>(np) * kp / 2);
+    const int q = lane >> 4, c16 = lane & 15;
+    const size_t tile_block0 = static_cast<size_t>(tile) * blocks;
+    const int col[2] = {tile * 32 + c16, tile * 32 + 16 + c16};
+
+    float acc[2][2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.0f;
+
+    auto widen = [](uint32_t wd) -> long {
+        const uint32_t ev = (wd << 4) & 0xf0f0f0f0u, od = wd & 0xf0f0f0f0u;
+        const uint32_t lo = __builtin_amdgcn_perm(od, ev, 0x05010400u);   // K 0..3
+        const uint32_t hi = __builtin_amdgcn_perm(od, ev, 0x07030602u);   // K 4..7
+        return static_cast<long>((static_cast<unsigned long>(hi) << 32) | lo);
+    };
+    const int32x4 zero = {0, 0, 0, 0};
+    for (int b = 0; b < blocks; ++b) {
+        const uint8_t *tb = w + (tile_block0 + b) * 512;
+        const uint32_t w0 = *reinterpret_cast<const uint32_t *>(tb + c16 * 32 + 4 * q);
+        const uint32_t w1 = *reinterpret_cast<const uint32_t *>(tb + c16 * 32 + 16 + 4 * q);
+        const float d0 = kk::half_bits_to_float(scales[static_cast<size_t>(b) * np + col[0]]) * 0.0625f;
+        const float d1 = kk::half_bits_to_float(scales[static_cast<size_t>(b) * np + col[1]]) * 0.0625f;
+        long a[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            a[i] = *reinterpret_cast<const long *>(codes + static_cast<size_t>(row0 + 16 * i + c16) * kp + 32 * b + 8 * q);
+        const long b0 = widen(w0), b1 = widen(w1);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int32x4 p0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], b0, zero, 0, 0, 0);
+            const int32x4 p1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], b1, zero, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                acc[i][0][r] = fmaf(static_cast<float>(p0[r]), d0, acc[i][0][r]);
+                acc[i][1][r] = fmaf(static_cast<float>(p1[r]), d1, acc[i][1][r]);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = row0 + 16 * i + 4 * q + r;
+            if (row >= rows) continue;
+            const float s = row_scales[row * 16];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                if (col[j] < n) y[static_cast<size_t>(row) * n + col[j]] = acc[i][j][r] * s;
+        }
+}
+
+} // namespace
+
+extern "C" int kk_common_quant_pair(const void *x, int x_f16, int k, int kp, void *values, void *params,
+                                    hipStream_t stream) {
+    if (!x || !values || !params || k <= 0 || kp < k || kp % 256 != 0 || kp > 16384) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(common_quant_pair, dim3(1), dim3(kQuantThreads), 0, stream, x, x_f16, k, kp,
+                       static_cast<int8_t *>(values), static_cast<float *>(params));
+    return hipGetLastError();
+}
+
+extern "C" int kk_common_quant_rows(const void *x, int x_f16, int k, int kp, int rows, int defined_rows,
+                                    void *values, void *params, hipStream_t stream) {
+    if (!x || !values || !params || k <= 0 || kp < k || kp % 256 != 0 || rows <= 0 || defined_rows < rows ||
+        defined_rows % 32 != 0)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(common_quant_rows, dim3(defined_rows), dim3(kRowThreads), 0, stream, x, x_f16, k, kp, rows,
+                       static_cast<int8_t *>(values), static_cast<float *>(params));
+    return hipGetLastError();
+}
+
+extern "C" size_t kk_common_gemv_lds_bytes(int kp, int exact) {
+    const size_t blocks = static_cast<size_t>(kp) / 32;
+    return blocks * (exact ? 24 * 4 + 4 : 16 * 4) + static_cast<size_t>(kCqWaves) * 32 * 4;
+}
+
+extern "C" int kk_common_gemv(const void *w0, float *y0, const void *w1, float *y1, const void *act, int exact,
+                              int x_f16, const void *params, int k, int kp, int n, int np, hipStream_t stream) {
+    if (!w0 || !y0 || !act || (!exact && !params) || kp % 256 != 0 || kp > 16384 || np % 256 != 0 || n > np ||
+        k > kp || (reinterpret_cast<uintptr_t>(w0) & 255) != 0 || (w1 && (reinterpret_cast<uintptr_t>(w1) & 255)))
+        return hipErrorInvalidValue;
+    const int tiles = (n + 31) / 32;
+    const int count = w1 ? 2 : 1;
+    const size_t lds = kk_common_gemv_lds_bytes(kp, exact);
+    const GemvMatrix m0{static_cast<const uint8_t *>(w0), y0};
+    const GemvMatrix m1{static_cast<const uint8_t *>(w1 ? w1 : w0), w1 ? y1 : y0};
+    if (exact)
+        hipLaunchKernelGGL(common_gemv<true>, dim3(tiles * count), dim3(kCqThreads), lds, stream, m0, m1, tiles, act,
+                           x_f16, static_cast<const float *>(params), k, kp, n, np);
+    else
+        hipLaunchKernelGGL(common_gemv<false>, dim3(tiles * count), dim3(kCqThreads), lds, stream, m0, m1, tiles, act,
+                           x_f16, static_cast<const float *>(params), k, kp, n, np);
+    return hipGetLastError();
+}
+
+extern "C" int kk_common_gemm(const void *w, const void *codes, const void *row_scales, float *y, int rows,
+                              int defined_rows, int kp, int n, int np, hipStream_t stream) {
+    if (!w || !codes || !row_scales || !y || rows <= 0 || rows > 128 || defined_rows < rows ||
+        defined_rows % 32 != 0 || defined_rows > 128 || kp % 256 != 0 || np % 256 != 0 || n > np ||
+        (reinterpret_cast<uintptr_t>(w) & 255) != 0 || (reinterpret_cast<uintptr_t>(codes) & 7) != 0)
+        return hipErrorInvalidValue;
+    const int tiles = (n + 31) / 32;
+    hipLaunchKernelGGL(common_gemm, dim3(tiles), dim3(256), 0, stream, static_cast<const uint8_t *>(w),
+                       static_cast<const int8_t *>(codes), static_cast<const float *>(row_scales), y, rows,
+                       defined_rows, kp, n, np);
+    return hipGetLastError();
+}

@@ -57,6 +57,24 @@ size_t kk_native_q4_payload_bytes(int k, int n);
 int kk_native_q4_gemv(const void *weights, const void *x, int x_f16, float *y, int k, int n, int batch,
                       hipStream_t stream);
 
+// Common Q4 ABI v1 (layout 1, scale order 1; weights 256-byte aligned).
+// M = 1 per-tensor two-component int8 quantization of X[k] (F32 or F16) into
+// the view buffer `values` (4*kp + 1024 bytes) and `params` (16 floats).
+int kk_common_quant_pair(const void *x, int x_f16, int k, int kp, void *values, void *params, hipStream_t stream);
+// M > 1 per-row int8 quantization of `rows` rows (zero rows up to
+// defined_rows, a multiple of 32): values [defined_rows][kp], params [defined_rows][16].
+int kk_common_quant_rows(const void *x, int x_f16, int k, int kp, int rows, int defined_rows, void *values,
+                         void *params, hipStream_t stream);
+// M = 1 GEMV over one weight (w1 null) or two sharing the activations.
+// exact = 0: act = the quantized view, params its scales; exact = 1: act = X.
+size_t kk_common_gemv_lds_bytes(int kp, int exact);
+int kk_common_gemv(const void *w0, float *y0, const void *w1, float *y1, const void *act, int exact, int x_f16,
+                   const void *params, int k, int kp, int n, int np, hipStream_t stream);
+// M > 1 (rows <= 128) GEMM on quantized rows (codes [defined_rows][kp], row
+// scales at row_scales[r*16]).
+int kk_common_gemm(const void *w, const void *codes, const void *row_scales, float *y, int rows, int defined_rows,
+                   int kp, int n, int np, hipStream_t stream);
+
 // Bytes of device workspace kk_i8_quantize needs for `count` activations.
 size_t kk_i8_workspace_bytes(int k, int batch);
 // Two-pass per-tensor INT8 quantization of X[batch,k] into `workspace`

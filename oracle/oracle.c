@@ -548,3 +548,134 @@ void orc_native_q4_decode(const uint8_t *native, int k, int n, float *w) {
         }
     }
 }
+
+/* Common Q4 ABI v1 (reference src/q4-common-pack.h:16-31, docs/q4-common-ABI.json):
+ * Kp = k rounded up to 512 (k < 512) or 256, Np = n rounded up to 256,
+ * weights Np*Kp/2 bytes then FP16 scales Np*Kp/16 bytes. */
+static int orc_round_up(int v, int a) { return (v + a - 1) / a * a; }
+static void orc_common_dims(int k, int n, int *kp, int *np, size_t *scale_offset) {
+    *kp = orc_round_up(k, k < 512 ? 512 : 256);
+    *np = orc_round_up(n, 256);
+    *scale_offset = (size_t)*kp * (size_t)*np / 2;
+}
+
+size_t orc_common_q4_size(int k, int n) {
+    if (k < 1 || k > 16384 || n < 1 || n > 32000) return 0;
+    int kp, np;
+    size_t off;
+    orc_common_dims(k, n, &kp, &np, &off);
+    return off + (size_t)kp * (size_t)np / 16;
+}
+
+/* Layout 1 ("Micro32Bank", reference q4-common-pack.h:23-29): column c, K
+ * pair index pr -> kb = pr/16, p = pr%16, word row = (c%32/16)*8 + p/2,
+ * bank = c%16, byte = (tile + kb)*512 + (bank*16 + row)*2 + p%2 with
+ * tile = (c/32)*(Kp/32). Scale order 1 (KMajor, q4-common-pack.h:31):
+ * scale_offset + (kb*Np + c)*2. */
+static size_t orc_common_weight_index(int kp, int c, int pr) {
+    int kb = pr / 16, p = pr % 16, row = (c % 32 / 16) * 8 + p / 2, bank = c % 16;
+    size_t tile = (size_t)(c / 32) * (size_t)(kp / 32);
+    return (tile + (size_t)kb) * 512 + (size_t)(bank * 16 + row) * 2 + (size_t)(p % 2);
+}
+static size_t orc_common_scale_index(size_t scale_offset, int np, int c, int kb) {
+    return scale_offset + ((size_t)kb * (size_t)np + (size_t)c) * 2;
+}
+
+/* Pack n rows of ceil(k/32) Q4_0 blocks (reference q4-common-pack.h:32-44):
+ * every byte not written is zero. */
+void orc_common_q4_pack(const uint8_t *q4, int k, int n, uint8_t *out) {
+    int kp, np;
+    size_t off;
+    orc_common_dims(k, n, &kp, &np, &off);
+    int blocks = (k + 31) / 32;
+    memset(out, 0, orc_common_q4_size(k, n));
+    for (int c = 0; c < n; ++c) {
+        for (int b = 0; b < blocks; ++b) {
+            const uint8_t *src = q4 + ((size_t)c * blocks + b) * 18;
+            size_t si = orc_common_scale_index(off, np, c, b);
+            out[si] = src[0];
+            out[si + 1] = src[1];
+            for (int p = 0; p < 16; ++p) {
+                int lo = orc_q4_signed(src, 2 * p), hi = orc_q4_signed(src, 2 * p + 1);
+                out[orc_common_weight_index(kp, c, b * 16 + p)] = (uint8_t)((lo & 15) | ((hi & 15) << 4));
+            }
+        }
+    }
+}
+
+/* F32 weights [n, k] of a packed region: signed nibble * FP16 scale. */
+void orc_common_q4_decode(const uint8_t *packed, int k, int n, float *w) {
+    int kp, np;
+    size_t off;
+    orc_common_dims(k, n, &kp, &np, &off);
+    for (int c = 0; c < n; ++c) {
+        for (int j = 0; j < k; ++j) {
+            int v = packed[orc_common_weight_index(kp, c, j / 2)] >> (j % 2 * 4) & 15;
+            size_t si = orc_common_scale_index(off, np, c, j / 32);
+            float d = orc_half_to_float((uint16_t)(packed[si] | (packed[si + 1] << 8)));
+            w[(size_t)c * k + j] = (float)(v >= 8 ? v - 16 : v) * d;
+        }
+    }
+}
+
+/* M = 1 activation view (reference kernels/kunlun-common-max-exact.xpu,
+ * -main-exact.xpu, -residual-exact.xpu): the two-component per-tensor
+ * quantization of X padded with zeros to Kp (orc_i8_activation's rule), main
+ * code of K j at values[(j/32)*64 + j%32], residual at values[2*Kp + same],
+ * every other byte of values[0 .. 4*Kp + 1024) zero; params =
+ * {max0/127, max1/127, max0, max1, 0 x 12}. -1 for a non-finite input. */
+int orc_common_quant_pair(const float *x, int k, int8_t *values, float *params) {
+    int kp, np;
+    size_t off;
+    orc_common_dims(k, 1, &kp, &np, &off);
+    float *padded = (float *)calloc((size_t)kp, sizeof(float));
+    int8_t *q0 = (int8_t *)malloc((size_t)kp), *q1 = (int8_t *)malloc((size_t)kp);
+    float max0, max1;
+    int rc = -2;
+    if (padded && q0 && q1) {
+        memcpy(padded, x, (size_t)k * sizeof(float));
+        rc = orc_i8_activation(padded, (size_t)kp, q0, q1, &max0, &max1);
+    }
+    if (rc == 0) {
+        memset(values, 0, (size_t)4 * kp + 1024);
+        for (int j = 0; j < kp; ++j) {
+            size_t i = (size_t)(j / 32) * 64 + (size_t)(j % 32);
+            values[i] = q0[j];
+            values[(size_t)2 * kp + i] = q1[j];
+        }
+        for (int i = 0; i < 16; ++i) params[i] = 0.0f;
+        params[0] = max0 / 127.0f;
+        params[1] = max1 / 127.0f;
+        params[2] = max0;
+        params[3] = max1;
+    }
+    free(padded);
+    free(q0);
+    free(q1);
+    return rc;
+}
+
+/* M > 1 Row A8 (reference common-q4/.../quant-row-serial-fused.xpu): row r of
+ * `rows` rows of X [rows, k] (rows up to `defined` are zero) -> max = max|x|
+ * (1 if 0), codes rnd(x * (127/max)) at values[r*Kp + j] (zero for j >= k),
+ * scale max/127 in all 16 floats of params[r*16 ..]. */
+void orc_common_quant_rows(const float *x, int k, int rows, int defined, int8_t *values, float *params) {
+    int kp, np;
+    size_t off;
+    orc_common_dims(k, 1, &kp, &np, &off);
+    for (int r = 0; r < defined; ++r) {
+        float mx = 0.0f;
+        for (int j = 0; j < k && r < rows; ++j) {
+            float a = fabsf(x[(size_t)r * k + j]);
+            if (a > mx) mx = a;
+        }
+        if (mx == 0.0f) mx = 1.0f;
+        float inv = 127.0f / mx, scale = mx / 127.0f;
+        for (int j = 0; j < kp; ++j) {
+            float v = (r < rows && j < k) ? x[(size_t)r * k + j] : 0.0f;
+            float scaled = v * inv;
+            values[(size_t)r * kp + j] = (int8_t)orc_round_clamp(scaled, 127);
+        }
+        for (int i = 0; i < 16; ++i) params[r * 16 + i] = scale;
+    }
+}

@@ -45,6 +45,20 @@
  *   orc_native_q4_decode   - the reference bench's inverse-mapping check of
  *                            every nibble and scale, and decode(pack(q4))
  *                            equal to orc_q4_decode(q4) bit for bit.
+ *   orc_common_q4_size,
+ *   orc_common_q4_pack,
+ *   orc_common_q4_decode   - the reference layout test's properties (the
+ *                            weight map is a bijection onto the payload,
+ *                            4.5 padded bits per weight) and decode(pack(q4))
+ *                            equal to orc_q4_decode(q4) bit for bit, over
+ *                            every FP16 scale pattern;
+ *   orc_common_quant_pair  - codes equal orc_i8_activation's on the padded
+ *                            input (pinned against the reference header);
+ *                            view layout checked against the reference
+ *                            bench's index formula;
+ *   orc_common_quant_rows  - the reference bench's CPU row rule
+ *                            (bench/common-q4-bench.cpp:43-45) restated in
+ *                            numpy, and scale * code within scale/2 of x.
  */
 #ifndef KUNLUN_ORACLE_H
 #define KUNLUN_ORACLE_H
@@ -94,6 +108,12 @@ void orc_elementwise(float *y, const float *a, const float *b, int n, int width,
 size_t orc_native_q4_size(int k, int n);
 void orc_pack_native_q4(const uint8_t *q4, int k, int n, uint8_t *out);
 void orc_native_q4_decode(const uint8_t *native, int k, int n, float *w);
+
+size_t orc_common_q4_size(int k, int n);
+void orc_common_q4_pack(const uint8_t *q4, int k, int n, uint8_t *out);
+void orc_common_q4_decode(const uint8_t *packed, int k, int n, float *w);
+int orc_common_quant_pair(const float *x, int k, int8_t *values, float *params);
+void orc_common_quant_rows(const float *x, int k, int rows, int defined, int8_t *values, float *params);
 
 #ifdef __cplusplus
 }

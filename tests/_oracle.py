@@ -55,6 +55,11 @@ class Oracle:
             "orc_native_q4_size": (ctypes.c_size_t, [I, I]),
             "orc_pack_native_q4": (None, [P, I, I, P]),
             "orc_native_q4_decode": (None, [P, I, I, P]),
+            "orc_common_q4_size": (ctypes.c_size_t, [I, I]),
+            "orc_common_q4_pack": (None, [P, I, I, P]),
+            "orc_common_q4_decode": (None, [P, I, I, P]),
+            "orc_common_quant_pair": (I, [P, I, P, P]),
+            "orc_common_quant_rows": (None, [P, I, I, I, P, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -231,6 +236,46 @@ class Oracle:
         w = np.empty((n, k), np.float32)
         self.lib.orc_native_q4_decode(_p(native), k, n, _p(w))
         return w
+
+    @staticmethod
+    def common_dims(k: int, n: int):
+        kp = -(-k // (512 if k < 512 else 256)) * (512 if k < 512 else 256)
+        np_ = -(-n // 256) * 256
+        return kp, np_
+
+    def common_q4_size(self, k: int, n: int) -> int:
+        return self.lib.orc_common_q4_size(k, n)
+
+    def common_q4_pack(self, q4: np.ndarray, k: int, n: int) -> np.ndarray:
+        q4 = np.ascontiguousarray(q4, dtype=np.uint8)
+        assert q4.size == n * (-(-k // 32)) * 18
+        out = np.empty(self.common_q4_size(k, n), np.uint8)
+        self.lib.orc_common_q4_pack(_p(q4), k, n, _p(out))
+        return out
+
+    def common_q4_decode(self, packed: np.ndarray, k: int, n: int) -> np.ndarray:
+        packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        w = np.empty((n, k), np.float32)
+        self.lib.orc_common_q4_decode(_p(packed), k, n, _p(w))
+        return w
+
+    def common_quant_pair(self, x: np.ndarray, k: int):
+        """(values [4kp+1024] int8, params [16] f32) or None for non-finite x."""
+        x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+        kp, _ = self.common_dims(k, 1)
+        values = np.empty(4 * kp + 1024, np.int8)
+        params = np.empty(16, np.float32)
+        if self.lib.orc_common_quant_pair(_p(x), k, _p(values), _p(params)) != 0:
+            return None
+        return values, params
+
+    def common_quant_rows(self, x: np.ndarray, k: int, rows: int, defined: int):
+        x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+        kp, _ = self.common_dims(k, 1)
+        values = np.empty(defined * kp, np.int8)
+        params = np.empty(defined * 16, np.float32)
+        self.lib.orc_common_quant_rows(_p(x), k, rows, defined, _p(values), _p(params))
+        return values, params
 
     def rowwise_i8_matmul(self, w: np.ndarray, x: np.ndarray) -> np.ndarray:
         """Whole reference rowwise_i8 path: weight upload quantization, two-pass

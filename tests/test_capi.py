@@ -42,8 +42,11 @@ def test_every_cxx_function_is_exported(kl):
     names = set(re.findall(r"^\s*[\w:&<>\s\*]+?\b([a-z_][a-z0-9_]*)\s*\(", body, re.M))
     names -= {"if", "return", "sizeof", "data", "size"}
     symbols = _dynamic_symbols(kl.LIBRARY_PATH)
-    missing = [n for n in sorted(names) if f"kunlun::{n}(" not in symbols]
+    # free functions as kunlun::name(, member functions as kunlun::Class::name(
+    missing = [n for n in sorted(names) if not re.search(rf"kunlun::(\w+::)?{n}\(", symbols)]
     assert not missing
+    for cls in ("NativeQ4Workspace", "CommonQ4Weight", "CommonQ4Workspace", "CommonQ4ActivationLease"):
+        assert f"kunlun::{cls}::~{cls}()" in symbols
     for special in ("kunlun::Buffer::Buffer(int, unsigned long)", "kunlun::Buffer::~Buffer()",
                     "kunlun::Kernel::Kernel()", "kunlun::Kernel::~Kernel()"):
         assert special in symbols
