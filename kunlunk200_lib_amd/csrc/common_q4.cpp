@@ -69,6 +69,8 @@ struct ActivationStorage {
     size_t quant_bytes = 0;
     void * scale = nullptr;
     size_t scale_bytes = 0;
+    void * tiled = nullptr;             // M > 1 codes in the GEMM's operand order
+    size_t tiled_bytes = 0;
     uint64_t epoch = 0;
     bool valid = false;
     bool profile = false;
@@ -84,6 +86,7 @@ struct ActivationStorage {
             check(wait());
             release(device, quant, quant_bytes);
             release(device, scale, scale_bytes);
+            release(device, tiled, tiled_bytes);
         }
     }
 };
@@ -201,6 +204,7 @@ struct CommonQ4ActivationLease::Impl {
     const void * input = nullptr;
     size_t input_bytes = 0;
     std::vector<CommonQ4ActivationChunk> chunks;
+    std::vector<const void *> tiled;       // per chunk: M > 1 codes in the GEMM's operand order
 };
 
 struct CommonQ4Workspace::Impl {
@@ -226,7 +230,7 @@ CommonQ4Statistics CommonQ4Workspace::statistics() const {
     CommonQ4Statistics a = impl_->stats;
     const ActivationStorage & st = *impl_->activation;
     a.hbm_workspace_bytes = 0;
-    for (size_t b : {st.quant_bytes, st.scale_bytes})
+    for (size_t b : {st.quant_bytes, st.scale_bytes, st.tiled_bytes})
         if (b) a.hbm_workspace_bytes += std::max<size_t>(b, 256);
     a.l3_workspace_bytes = 0;
     a.slice_bytes = 0;
@@ -238,7 +242,7 @@ CommonQ4ActivationStatistics CommonQ4Workspace::activation_statistics() const {
     const ActivationStorage & st = *impl_->activation;
     CommonQ4ActivationStatistics a = st.stats;
     a.hbm_activation_bytes = 0;
-    for (size_t b : {st.quant_bytes, st.scale_bytes})
+    for (size_t b : {st.quant_bytes, st.scale_bytes, st.tiled_bytes})
         if (b) a.hbm_activation_bytes += std::max<size_t>(b, 256);
     return a;
 }
@@ -263,6 +267,7 @@ void CommonQ4ActivationLease::reset() {
     if (a.storage && a.storage->valid && a.epoch == a.storage->epoch) invalidate(*a.storage);
     a.storage.reset();
     a.chunks.clear();
+    a.tiled.clear();
     a.epoch = a.generation = 0;
 }
 bool CommonQ4ActivationLease::matches(int id, int k, int m, InputType type, uint64_t generation) const {
@@ -298,7 +303,7 @@ bool exact_route(const CommonQ4Info & a) { return (size_t)a.np * a.kp > kExactRo
 
 // Quantizes one chunk of rows into (values, scales); returns launches made.
 void quantize_chunk(CommonQ4Workspace::Impl & s, hipStream_t stream, const void * x, int x_f16, const CommonQ4Info & a,
-                    int m, int rows, int padded, void * values, void * scales) {
+                    int m, int rows, int padded, void * values, void * scales, void * tiled) {
     ActivationStorage & st = *s.activation;
     const uint64_t t0 = st.profile ? now_ns() : 0;
     if (m == 1)
@@ -306,7 +311,7 @@ void quantize_chunk(CommonQ4Workspace::Impl & s, hipStream_t stream, const void 
                           "kk_common_quant_pair");
     else
         detail::check_hip((hipError_t)kk_common_quant_rows(x, x_f16, a.k, a.kp, rows, round_up(padded, 32), values,
-                                                           scales, stream),
+                                                           scales, tiled, stream),
                           "kk_common_quant_rows");
     if (st.profile) {
         detail::check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
@@ -332,32 +337,42 @@ bool execute(CommonQ4Workspace::Impl & s, int id, void * y, const CommonQ4Info &
         float * out = static_cast<float *>(y) + (size_t)first * a.n;
         const CommonQ4ActivationChunk * chunk = prepared ? &prepared->chunks[index++] : nullptr;
         if (m == 1 && exact_route(a)) {
-            detail::check_hip((hipError_t)kk_common_gemv(w, out, nullptr, nullptr, x, 1, x_f16, nullptr, a.k, a.kp,
-                                                         a.n, a.np, ctx.stream),
+            detail::check_hip((hipError_t)kk_common_gemv(w, out, nullptr, nullptr, x, 2, x_f16, nullptr, nullptr, a.k,
+                                                         a.kp, a.n, a.np, ctx.stream),
                               "kk_common_gemv");
             s.last_components = 0;
             ++s.stats.paths[7];
         } else {
             const void * values;
             const void * scales;
+            const void * tiled = nullptr;
             if (chunk) {
                 values = chunk->values;
                 scales = chunk->scales;
+                tiled = prepared->tiled[index - 1];
             } else {
                 reserve(st, id, st.quant, st.quant_bytes, m == 1 ? (size_t)4 * a.kp + 1024 : (size_t)128 * a.kp + 1024);
                 reserve(st, id, st.scale, st.scale_bytes, m == 1 ? 64 : 128 * 64);
-                quantize_chunk(s, ctx.stream, x, x_f16, a, m, rows, padded, st.quant, st.scale);
+                if (m != 1) reserve(st, id, st.tiled, st.tiled_bytes, (size_t)128 * a.kp);
+                // M = 1 quantizes inside the GEMV (every workgroup for itself,
+                // workgroup 0 writes the view); M > 1 runs the row kernel first
+                if (m != 1) quantize_chunk(s, ctx.stream, x, x_f16, a, m, rows, padded, st.quant, st.scale, st.tiled);
+                else ++st.stats.quantized_chunks;
                 values = st.quant;
                 scales = st.scale;
+                tiled = st.tiled;
             }
             if (m == 1) {
-                detail::check_hip((hipError_t)kk_common_gemv(w, out, nullptr, nullptr, values, 0, 0, scales, a.k, a.kp,
-                                                             a.n, a.np, ctx.stream),
+                const bool fused = chunk == nullptr;
+                detail::check_hip((hipError_t)kk_common_gemv(w, out, nullptr, nullptr, fused ? x : values, fused ? 1 : 0,
+                                                             x_f16, const_cast<void *>(scales),
+                                                             const_cast<void *>(values), a.k, a.kp, a.n, a.np,
+                                                             ctx.stream),
                                   "kk_common_gemv");
                 s.last_components = 2;
                 ++s.stats.paths[0];
             } else {
-                detail::check_hip((hipError_t)kk_common_gemm(w, values, scales, out, rows, round_up(padded, 32), a.kp,
+                detail::check_hip((hipError_t)kk_common_gemm(w, tiled, scales, out, rows, round_up(padded, 32), a.kp,
                                                              a.n, a.np, ctx.stream),
                                   "kk_common_gemm");
                 s.last_components = 1;
@@ -437,6 +452,7 @@ bool common_q4_prepare(CommonQ4Workspace & work, int id, const void * input, int
     detail::DeviceContext & ctx = detail::context(id);
     reserve(st, id, st.quant, st.quant_bytes, chunks * qstride);
     reserve(st, id, st.scale, st.scale_bytes, chunks * sstride);
+    if (m != 1) reserve(st, id, st.tiled, st.tiled_bytes, chunks * 128 * (size_t)a.kp);
     CommonQ4ActivationLease::Impl & l = *lease.impl_;
     l.storage = s.activation;
     l.epoch = st.epoch;
@@ -453,7 +469,9 @@ bool common_q4_prepare(CommonQ4Workspace & work, int id, const void * input, int
         const void * x = static_cast<const char *>(input) + (size_t)first * k * bytes;
         void * q = static_cast<char *>(st.quant) + index * qstride;
         void * sc = static_cast<char *>(st.scale) + index * sstride;
-        quantize_chunk(s, ctx.stream, x, bytes == 2, a, m, rows, padded, q, sc);
+        void * tl = m == 1 ? nullptr : static_cast<char *>(st.tiled) + index * 128 * (size_t)a.kp;
+        quantize_chunk(s, ctx.stream, x, bytes == 2, a, m, rows, padded, q, sc, tl);
+        l.tiled.push_back(tl);
         const int defined = m == 1 ? 1 : round_up(padded, 32);
         l.chunks.push_back({q, sc, first, rows, padded, a.kp, m == 1 ? 2 : 1,
                             m == 1 ? qstride : (size_t)defined * a.kp, m == 1 ? sstride : (size_t)defined * 64});
@@ -551,8 +569,9 @@ bool common_q4_matmul_pair(CommonQ4Workspace & work, int id, void * y0, void * y
     if ((size_t)a.n * (a.k / 32) * 4 > 8u * 1024 * 1024) return reject(CommonQ4PairStatus::Workspace);
     detail::DeviceContext & ctx = detail::context(id);
     detail::check_hip((hipError_t)kk_common_gemv(w0.storage, static_cast<float *>(y0), w1.storage,
-                                                 static_cast<float *>(y1), chunk.values, 0, 0, chunk.scales, a.k,
-                                                 a.kp, a.n, a.np, ctx.stream),
+                                                 static_cast<float *>(y1), chunk.values, 0, 0,
+                                                 const_cast<void *>(chunk.scales), nullptr, a.k, a.kp, a.n, a.np,
+                                                 ctx.stream),
                       "kk_common_gemv");
     detail::check_hip(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize");
     s.last_values = chunk.values;

@@ -55,6 +55,67 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
            ((static_cast<uint32_t>(c) & 255u) << 16) | (static_cast<uint32_t>(d) << 24);
 }
 
+// Two-component per-tensor quantization of the values a workgroup holds
+// (v[i][t] for its groups; values past k are zero): on return v holds the
+// residuals' codes' inputs replaced by the codes themselves in q0/q1, and
+// s[] = {max0/127, max1/127, max0, max1}. Every thread of the workgroup calls it.
+template <int Threads, int Groups>
+__device__ void quantize_pair(float (&v)[Groups][8], int (&q0)[Groups][8], int (&q1)[Groups][8], float (&s)[4],
+                              uint32_t *scratch) {
+#pragma clang fp contract(off)
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < Groups; ++i)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) m = max(m, __float_as_uint(v[i][t]) & 0x7fffffffu);
+    m = block_max_bits<Threads>(m, scratch);
+    const float max0 = m ? __uint_as_float(m) : 1.0f;
+    const float s0 = max0 / 127.0f, inv0 = 127.0f / max0;
+    uint32_t m1 = 0;
+#pragma unroll
+    for (int i = 0; i < Groups; ++i)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const float scaled = v[i][t] * inv0;
+            q0[i][t] = kk::round_clamp(scaled, 127);
+            const float back = static_cast<float>(q0[i][t]) * s0;
+            v[i][t] = v[i][t] - back;                       // residual
+            m1 = max(m1, __float_as_uint(v[i][t]) & 0x7fffffffu);
+        }
+    m1 = block_max_bits<Threads>(m1, scratch);
+    const float max1 = m1 ? __uint_as_float(m1) : 1.0f;
+    const float s1 = max1 / 127.0f, inv1 = 127.0f / max1;
+#pragma unroll
+    for (int i = 0; i < Groups; ++i)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) q1[i][t] = kk::round_clamp(v[i][t] * inv1, 127);
+    s[0] = s0;
+    s[1] = s1;
+    s[2] = max0;
+    s[3] = max1;
+}
+
+// Writes group g's codes to the view (main at (g/4)*64 + (g%4)*8, residual
+// 2kp further, the group's gap bytes zero).
+__device__ __forceinline__ void write_view_group(int8_t *values, int kp, int g, const int (&a)[8], const int (&b)[8]) {
+    const size_t at = static_cast<size_t>(g / 4) * 64 + (g % 4) * 8;
+    uint32_t *main = reinterpret_cast<uint32_t *>(values + at);
+    uint32_t *resid = reinterpret_cast<uint32_t *>(values + 2 * static_cast<size_t>(kp) + at);
+    main[0] = pack4(a[0], a[1], a[2], a[3]);
+    main[1] = pack4(a[4], a[5], a[6], a[7]);
+    main[8] = 0;                          // bytes at + 32 .. + 40: the group's gap
+    main[9] = 0;
+    resid[0] = pack4(b[0], b[1], b[2], b[3]);
+    resid[1] = pack4(b[4], b[5], b[6], b[7]);
+    resid[8] = 0;
+    resid[9] = 0;
+}
+
+__device__ __forceinline__ void write_view_tail(int8_t *values, int kp, float *params, const float (&s)[4]) {
+    if (threadIdx.x < 256) reinterpret_cast<uint32_t *>(values + 4 * static_cast<size_t>(kp))[threadIdx.x] = 0;
+    if (threadIdx.x < 16) params[threadIdx.x] = threadIdx.x < 4 ? s[threadIdx.x] : 0.0f;
+}
+
 // ---------------------------------------------------------------------------
 // M = 1: two-component per-tensor quantization into the reference's view:
 // main code of K j at values[(j/32)*64 + j%32], residual at values[2kp + ...],
@@ -69,7 +130,6 @@ __global__ __launch_bounds__(kQuantThreads) void common_quant_pair(const void *_
     constexpr int kMaxGroups = 2;              // kp <= 16384 = 2 * 1024 * 8
     const int groups = kp / 8;
     float v[kMaxGroups][8];
-    uint32_t m = 0;
 #pragma unroll
     for (int i = 0; i < kMaxGroups; ++i) {
         const int g = threadIdx.x + kQuantThreads * i;
@@ -77,60 +137,35 @@ __global__ __launch_bounds__(kQuantThreads) void common_quant_pair(const void *_
         for (int t = 0; t < 8; ++t) {
             const int j = 8 * g + t;
             v[i][t] = (g < groups && j < k) ? load_value(x, x_f16, j) : 0.0f;
-            m = max(m, __float_as_uint(v[i][t]) & 0x7fffffffu);
         }
     }
-    m = block_max_bits<kQuantThreads>(m, scratch);
-    const float max0 = m ? __uint_as_float(m) : 1.0f;
-    const float s0 = max0 / 127.0f, inv0 = 127.0f / max0;
-    int q0[kMaxGroups][8];
-    uint32_t m1 = 0;
-#pragma unroll
-    for (int i = 0; i < kMaxGroups; ++i)
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const float scaled = v[i][t] * inv0;
-            q0[i][t] = kk::round_clamp(scaled, 127);
-            const float back = static_cast<float>(q0[i][t]) * s0;
-            v[i][t] = v[i][t] - back;                       // residual
-            m1 = max(m1, __float_as_uint(v[i][t]) & 0x7fffffffu);
-        }
-    m1 = block_max_bits<kQuantThreads>(m1, scratch);
-    const float max1 = m1 ? __uint_as_float(m1) : 1.0f;
-    const float s1 = max1 / 127.0f, inv1 = 127.0f / max1;
+    int q0[kMaxGroups][8], q1[kMaxGroups][8];
+    float sc[4];
+    quantize_pair<kQuantThreads, kMaxGroups>(v, q0, q1, sc, scratch);
 #pragma unroll
     for (int i = 0; i < kMaxGroups; ++i) {
         const int g = threadIdx.x + kQuantThreads * i;
-        if (g >= groups) continue;
-        int q1[8];
-#pragma unroll
-        for (int t = 0; t < 8; ++t) q1[t] = kk::round_clamp(v[i][t] * inv1, 127);
-        const size_t at = static_cast<size_t>(g / 4) * 64 + (g % 4) * 8;
-        uint32_t *main = reinterpret_cast<uint32_t *>(values + at);
-        uint32_t *resid = reinterpret_cast<uint32_t *>(values + 2 * static_cast<size_t>(kp) + at);
-        main[0] = pack4(q0[i][0], q0[i][1], q0[i][2], q0[i][3]);
-        main[1] = pack4(q0[i][4], q0[i][5], q0[i][6], q0[i][7]);
-        main[8] = 0;                          // bytes at + 32 .. + 40: the group's gap
-        main[9] = 0;
-        resid[0] = pack4(q1[0], q1[1], q1[2], q1[3]);
-        resid[1] = pack4(q1[4], q1[5], q1[6], q1[7]);
-        resid[8] = 0;
-        resid[9] = 0;
+        if (g < groups) write_view_group(values, kp, g, q0[i], q1[i]);
     }
-    if (threadIdx.x < 256) reinterpret_cast<uint32_t *>(values + 4 * static_cast<size_t>(kp))[threadIdx.x] = 0;
-    if (threadIdx.x < 16) {
-        const float p[4] = {s0, s1, max0, max1};
-        params[threadIdx.x] = threadIdx.x < 4 ? p[threadIdx.x] : 0.0f;
-    }
+    write_view_tail(values, kp, params, sc);
 }
 
 // ---------------------------------------------------------------------------
 // M > 1: Row A8. Workgroup r quantizes row r of X (rows >= `rows` are the
 // zero padding rows: scale 1/127, codes 0) into values[r*kp ..] and writes the
-// row scale to all 16 floats of params[r*16 ..].
+// row scale to all 16 floats of params[r*16 ..]. The same codes also go to
+// `tiled` in the GEMM's A-operand order, two blocks per lane: row r, K j at
+// (((r/16) * (kp/64) + j/64) * 64 + r%16 + 16 * (j%32/8)) * 16 + (j/32 % 2) * 8 + j%8,
+// so one wave reads a 16-row x 64-K operand pair as 1 KB contiguous.
+__device__ __forceinline__ size_t tiled_offset(int r, int j, int blocks) {
+    return ((static_cast<size_t>(r / 16) * (blocks / 2) + j / 64) * 64 + r % 16 + 16 * ((j % 32) / 8)) * 16 +
+           ((j / 32) % 2) * 8 + j % 8;
+}
+
 __global__ __launch_bounds__(kRowThreads) void common_quant_rows(const void *__restrict__ x, int x_f16, int k,
                                                                 int kp, int rows, int8_t *__restrict__ values,
-                                                                float *__restrict__ params) {
+                                                                float *__restrict__ params,
+                                                                int8_t *__restrict__ tiled) {
 #pragma clang fp contract(off)
     __shared__ uint32_t scratch[kRowThreads / 64];
     const int row = blockIdx.x;
@@ -152,7 +187,9 @@ __global__ __launch_bounds__(kRowThreads) void common_quant_rows(const void *__r
             const float v = (real && j < k) ? load_value(x, x_f16, base + j) : 0.0f;
             q[t] = kk::round_clamp(v * inv, 127);
         }
-        out[d] = pack4(q[0], q[1], q[2], q[3]);
+        const uint32_t word = pack4(q[0], q[1], q[2], q[3]);
+        out[d] = word;
+        *reinterpret_cast<uint32_t *>(tiled + tiled_offset(row, 4 * d, kp / 32)) = word;
     }
     if (threadIdx.x < 16) params[row * 16 + threadIdx.x] = scale;
 }
@@ -173,12 +210,22 @@ struct GemvMatrix {
     float *y;
 };
 
-template <bool EXACT>
+// MODE: kPrepared (act = the quantized view, params its scales), kQuantize
+// (act = X: every workgroup quantizes X itself, workgroup 0 also writes the
+// view to view_values / view_params), kExact (act = X).
+constexpr int kPrepared = 0, kQuantize = 1, kExact = 2;
+
+template <int MODE>
 __global__ __launch_bounds__(kCqThreads) void common_gemv(GemvMatrix m0, GemvMatrix m1, int tiles_per_matrix,
                                                          const void *__restrict__ act, int x_f16,
-                                                         const float *__restrict__ params, int k, int kp, int n,
+                                                         const float *__restrict__ params,
+                                                         int8_t *__restrict__ view_values,
+                                                         float *__restrict__ view_params, int k, int kp, int n,
                                                          int np) {
+    constexpr bool EXACT = MODE == kExact;
+    constexpr bool RAW_X = MODE != kPrepared;
     extern __shared__ uint4 lds4[];
+    __shared__ uint32_t scratch[kCqWaves];
     const int which = blockIdx.x / tiles_per_matrix;
     const int tile = blockIdx.x - which * tiles_per_matrix;
     const GemvMatrix mat = which ? m1 : m0;
@@ -204,7 +251,7 @@ __global__ __launch_bounds__(kCqThreads) void common_gemv(GemvMatrix m0, GemvMat
 #pragma unroll
     for (int pass = 0; pass < kMaxPasses; ++pass) {
         const int g = min(pass * kCqThreads + static_cast<int>(threadIdx.x), groups - 1);
-        if (EXACT) {
+        if (RAW_X) {
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
                 const int j = 8 * g + t;
@@ -222,7 +269,7 @@ __global__ __launch_bounds__(kCqThreads) void common_gemv(GemvMatrix m0, GemvMat
         }
     }
     float s0 = 0.0f, s1 = 0.0f;
-    if (!EXACT) {
+    if (MODE == kPrepared) {
         s0 = params[0] * 0.0625f;              // the weights enter as 16 * q
         s1 = params[1] * 0.0625f;
     }
@@ -239,7 +286,10 @@ __global__ __launch_bounds__(kCqThreads) void common_gemv(GemvMatrix m0, GemvMat
         buf[3] = v.w;
         buf[4] = scales[static_cast<size_t>(blk) * np + min(col, np - 1)];
     };
-    const int my_items = wid < pairs ? (pairs - wid + kCqWaves - 1) / kCqWaves : 0;
+    // every wave runs the same padded count of items; items past the end load
+    // a valid address and add zero
+    const int iters = (pairs + kCqWaves - 1) / kCqWaves;
+    const int iters_padded = (iters + kCqDepth - 1) / kCqDepth * kCqDepth;
     uint32_t ring[kCqDepth][5];
 #pragma unroll
     for (int d = 0; d < kCqDepth; ++d) {
@@ -248,6 +298,26 @@ __global__ __launch_bounds__(kCqThreads) void common_gemv(GemvMatrix m0, GemvMat
     }
 
     // 3. activations -> LDS
+    if (MODE == kQuantize) {
+        // clamped duplicate groups hold copies of the last group: no effect on the maxima
+        int q0[kMaxPasses][8], q1[kMaxPasses][8];
+        float sc[4];
+        quantize_pair<kCqThreads, kMaxPasses>(xv, q0, q1, sc, scratch);
+        s0 = sc[0] * 0.0625f;
+        s1 = sc[1] * 0.0625f;
+#pragma unroll
+        for (int pass = 0; pass < kMaxPasses; ++pass) {
+            const int g = pass * kCqThreads + static_cast<int>(threadIdx.x);
+            if (g < groups) {
+                raw[pass][0] = pack4(q0[pass][0], q0[pass][1], q0[pass][2], q0[pass][3]);
+                raw[pass][1] = pack4(q0[pass][4], q0[pass][5], q0[pass][6], q0[pass][7]);
+                raw[pass][2] = pack4(q1[pass][0], q1[pass][1], q1[pass][2], q1[pass][3]);
+                raw[pass][3] = pack4(q1[pass][4], q1[pass][5], q1[pass][6], q1[pass][7]);
+                if (blockIdx.x == 0) write_view_group(view_values, kp, g, q0[pass], q1[pass]);
+            }
+        }
+        if (blockIdx.x == 0) write_view_tail(view_values, kp, view_params, sc);
+    }
 #pragma unroll
     for (int pass = 0; pass < kMaxPasses; ++pass) {
         const int idx = pass * kCqThreads + static_cast<int>(threadIdx.x);
@@ -286,8 +356,10 @@ __global__ __launch_bounds__(kCqThreads) void common_gemv(GemvMatrix m0, GemvMat
     // 4. items
     float acc = 0.0f;
     auto compute_item = [&](int s, const uint32_t (&buf)[5]) {
-        const int blk = 2 * (wid + kCqWaves * s) + (lane >> 5);
-        const float d = col < n ? kk::half_bits_to_float(buf[4]) : 0.0f;
+        const int it = wid + kCqWaves * s;
+        const bool live = it < pairs && col < n;
+        const int blk = 2 * min(it, pairs - 1) + (lane >> 5);
+        const float d = live ? kk::half_bits_to_float(buf[4]) : 0.0f;
         if (EXACT) {
             const uint4 *src = reinterpret_cast<const uint4 *>(act_lds + static_cast<size_t>(blk) * 24);
             uint32_t dg[24];
@@ -310,7 +382,7 @@ __global__ __launch_bounds__(kCqThreads) void common_gemv(GemvMatrix m0, GemvMat
             int sum = t[5];
 #pragma unroll
             for (int l = 4; l >= 0; --l) sum = (sum << 4) + t[l];
-            acc = fmaf(static_cast<float>(sum), col < n ? d * block_scale[blk] : 0.0f, acc);
+            acc = fmaf(static_cast<float>(sum), live ? d * block_scale[blk] : 0.0f, acc);
         } else {
             const uint4 *src = reinterpret_cast<const uint4 *>(act_lds + static_cast<size_t>(blk) * 16);
             const uint4 e0 = src[0], o0 = src[1], e1 = src[2], o1 = src[3];
@@ -330,14 +402,12 @@ __global__ __launch_bounds__(kCqThreads) void common_gemv(GemvMatrix m0, GemvMat
             acc = fmaf(d, t, acc);
         }
     };
-    for (int base = 0; base < my_items; base += kCqDepth) {
+    for (int base = 0; base < iters_padded; base += kCqDepth) {
 #pragma unroll
         for (int dpt = 0; dpt < kCqDepth; ++dpt) {
-            const int s = base + dpt;
-            if (s < my_items) {
-                compute_item(s, ring[dpt]);
-                if (s + kCqDepth < my_items) load_item(s + kCqDepth, ring[dpt]);
-            }
+            compute_item(base + dpt, ring[dpt]);
+            load_item(base + dpt + kCqDepth, ring[dpt]);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 
@@ -356,24 +426,82 @@ __global__ __launch_bounds__(kCqThreads) void common_gemv(GemvMatrix m0, GemvMat
 
 // ---------------------------------------------------------------------------
 // M > 1 GEMM on v_mfma_i32_16x16x32_i8 (one K32 block per MFMA, so each
-// block's int32 sums get their own FP16 scale). Workgroup = one N32 tile (two
-// 16-column groups) x up to 128 rows: wave w owns rows 32w .. 32w+31 (two
-// 16-row tiles). Operand layout (wave64): A[l%16][8(l/16) .. +8),
-// B[8(l/16) .. +8)[l%16], D[4(l/16) + r][l%16]. B lane l: column 16g + l%16
-// of the tile, K dword l/16 of the block, widened to 8 int8 = 16 * q.
-__global__ __launch_bounds__(256) void common_gemm(const uint8_t *__restrict__ w, const int8_t *__restrict__ codes,
-                                                  const float *__restrict__ row_scales, float *__restrict__ y,
-                                                  int rows, int defined_rows, int kp, int n, int np) {
+// block's int32 sums get their own FP16 scale). A workgroup is one N32 tile x
+// up to 128 rows: wave w owns rows 32w .. 32w+31 (two 16-row tiles).
+//
+// Data path (wide loads only; narrow per-lane loads cost one L1 tag access
+// per few lanes and starve this kernel): per stage of 8 blocks the tile's 4 KB
+// of weights and 512 B of scales are copied into LDS by the 4 waves
+// (global_load_lds, 16 B per lane, 2 copies per wave), two stages ahead into
+// a ring of 3 buffers; each wave loads its activation operands with one
+// dwordx4 per lane per row tile and block pair (the tiled order of
+// common_quant_rows), one stage ahead. MFMA operand layout (wave64):
+// A[l%16][8(l/16) .. +8), B[8(l/16) .. +8)[l%16], D[4(l/16) + r][l%16]; B
+// lane l: column 16g + l%16 of the tile, K dword l/16 of the block, widened
+// to 8 int8 = 16 * q.
+constexpr int kGemmChunk = 8;                    // blocks per stage
+constexpr int kGemmBufs = 3;                     // LDS stage buffers
+constexpr int kGemmStageBytes = kGemmChunk * 512 + kGemmChunk * 64;
+
+__device__ __forceinline__ void gemm_lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+}
+
+// KS = 2 doubles the waves: wave 4h + g takes row group g over K half h
+// (its own staging ring); the halves' sums meet in LDS and are added in a
+// fixed order.
+template <int KS>
+__global__ __launch_bounds__(256 * KS) void common_gemm(const uint8_t *__restrict__ w, const int8_t *__restrict__ tiled,
+                                                       const float *__restrict__ row_scales, float *__restrict__ y,
+                                                       int rows, int defined_rows, int kp, int n, int np) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds_all[KS * kGemmBufs * kGemmStageBytes];
     const int lane = threadIdx.x & 63;
-    const int wid = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+    const int wid = wave & 3, half = wave >> 2;
+    uint8_t *const stage_lds = lds_all + half * kGemmBufs * kGemmStageBytes;
     const int tile = blockIdx.x;
     const int row0 = 32 * wid;
-    if (row0 >= defined_rows) return;           // no barrier in this kernel
+    const bool active = row0 < defined_rows;
     const int blocks = kp >> 5;
-    const uint16_t *scales = reinterpret_cast<const uint16_t *>(w + static_cast<size_t>(np) * kp / 2);
+    const int chunks = blocks / kGemmChunk / KS;   // per K half (kp % (256 * KS) == 0)
+    const int chunk0 = half * chunks;
+    const int pairs = blocks / 2;
+    const uint8_t *scales = w + static_cast<size_t>(np) * kp / 2;
     const int q = lane >> 4, c16 = lane & 15;
-    const size_t tile_block0 = static_cast<size_t>(tile) * blocks;
-    const int col[2] = {tile * 32 + c16, tile * 32 + 16 + c16};
+
+    // copies of stage c into buffer c % 3: wave w takes blocks 2w, 2w+1 (1 KB
+    // of weights) and their scales (lanes 0..7: block 2w + lane/4, 16 B each)
+    auto copy_stage = [&](int c) {
+        const int cc = chunk0 + min(c, chunks - 1);        // past the end: a copy nobody reads
+        uint8_t *buf = stage_lds + (c % kGemmBufs) * kGemmStageBytes;
+        const int b0 = cc * kGemmChunk + 2 * wid;
+        __builtin_amdgcn_global_load_lds(w + (static_cast<size_t>(tile) * blocks + b0) * 512 + lane * 16,
+                                         buf + wid * 1024, 16, 0, 0);
+        const int sl = min(lane, 7);                       // lanes 8.. repeat lane 7's copy
+        const uint8_t *ssrc = scales + (static_cast<size_t>(b0 + sl / 4) * np + tile * 32) * 2 + (sl % 4) * 16;
+        if (lane < 8) __builtin_amdgcn_global_load_lds(ssrc, buf + kGemmChunk * 512 + wid * 128, 16, 0, 0);
+    };
+    // activation operands of stage c: [row tile][block pair] as uint4
+    const int8_t *abase = tiled + (static_cast<size_t>(row0 / 16) * pairs * 64 + lane) * 16;
+    auto load_a = [&](int c, uint4 (&a)[2][kGemmChunk / 2]) {
+        const int cc = chunk0 + min(c, chunks - 1);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int p = 0; p < kGemmChunk / 2; ++p)
+                a[i][p] = *reinterpret_cast<const uint4 *>(abase + (static_cast<size_t>(i) * pairs +
+                                                                    cc * (kGemmChunk / 2) + p) * 64 * 16);
+    };
+    auto widen = [](uint32_t wd) -> long {
+        const uint32_t ev = (wd << 4) & 0xf0f0f0f0u, od = wd & 0xf0f0f0f0u;
+        const uint32_t lo = __builtin_amdgcn_perm(od, ev, 0x05010400u);   // K 0..3
+        const uint32_t hi = __builtin_amdgcn_perm(od, ev, 0x07030602u);   // K 4..7
+        return static_cast<long>((static_cast<unsigned long>(hi) << 32) | lo);
+    };
 
     float acc[2][2][4];
 #pragma unroll
@@ -382,36 +510,79 @@ __global__ __launch_bounds__(256) void common_gemm(const uint8_t *__restrict__ w
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.0f;
-
-    auto widen = [](uint32_t wd) -> long {
-        const uint32_t ev = (wd << 4) & 0xf0f0f0f0u, od = wd & 0xf0f0f0f0u;
-        const uint32_t lo = __builtin_amdgcn_perm(od, ev, 0x05010400u);   // K 0..3
-        const uint32_t hi = __builtin_amdgcn_perm(od, ev, 0x07030602u);   // K 4..7
-        return static_cast<long>((static_cast<unsigned long>(hi) << 32) | lo);
-    };
     const int32x4 zero = {0, 0, 0, 0};
-    for (int b = 0; b < blocks; ++b) {
-        const uint8_t *tb = w + (tile_block0 + b) * 512;
-        const uint32_t w0 = *reinterpret_cast<const uint32_t *>(tb + c16 * 32 + 4 * q);
-        const uint32_t w1 = *reinterpret_cast<const uint32_t *>(tb + c16 * 32 + 16 + 4 * q);
-        const float d0 = kk::half_bits_to_float(scales[static_cast<size_t>(b) * np + col[0]]) * 0.0625f;
-        const float d1 = kk::half_bits_to_float(scales[static_cast<size_t>(b) * np + col[1]]) * 0.0625f;
-        long a[2];
+
+    uint4 a_cur[2][kGemmChunk / 2], a_next[2][kGemmChunk / 2];
+    // issue order: copies 0, A 0, copies 1; then per step c: A c+1, copies c+2.
+    // At the top of step c only copies c+1 (2 per wave) may still be in flight.
+    copy_stage(0);
+    if (active) load_a(0, a_next);
+    copy_stage(1);
+    for (int c = 0; c < chunks; ++c) {
+        __builtin_amdgcn_s_waitcnt(0x0F70 | 2);            // vmcnt(2): all but copies c+1
+        gemm_lds_barrier();                                // every wave's copies of c landed,
+                                                           // and reads of buffer (c-1)%3 are done
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-            a[i] = *reinterpret_cast<const long *>(codes + static_cast<size_t>(row0 + 16 * i + c16) * kp + 32 * b + 8 * q);
-        const long b0 = widen(w0), b1 = widen(w1);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int32x4 p0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], b0, zero, 0, 0, 0);
-            const int32x4 p1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], b1, zero, 0, 0, 0);
+            for (int p = 0; p < kGemmChunk / 2; ++p) a_cur[i][p] = a_next[i][p];
+        if (active) load_a(c + 1, a_next);
+        copy_stage(c + 2);
+        if (!active) continue;
+        const uint8_t *buf = stage_lds + (c % kGemmBufs) * kGemmStageBytes;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                acc[i][0][r] = fmaf(static_cast<float>(p0[r]), d0, acc[i][0][r]);
-                acc[i][1][r] = fmaf(static_cast<float>(p1[r]), d1, acc[i][1][r]);
+        for (int j = 0; j < kGemmChunk; ++j) {
+            const uint32_t w0 = *reinterpret_cast<const uint32_t *>(buf + j * 512 + c16 * 32 + 4 * q);
+            const uint32_t w1 = *reinterpret_cast<const uint32_t *>(buf + j * 512 + c16 * 32 + 16 + 4 * q);
+            const uint16_t *sc = reinterpret_cast<const uint16_t *>(buf + kGemmChunk * 512 + j * 64);
+            const float d0 = kk::half_bits_to_float(sc[c16]) * 0.0625f;
+            const float d1 = kk::half_bits_to_float(sc[16 + c16]) * 0.0625f;
+            const long b0 = widen(w0), b1 = widen(w1);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint4 v = a_cur[i][j / 2];
+                const long a = (j & 1) ? static_cast<long>((static_cast<unsigned long>(v.w) << 32) | v.z)
+                                       : static_cast<long>((static_cast<unsigned long>(v.y) << 32) | v.x);
+                const int32x4 p0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b0, zero, 0, 0, 0);
+                const int32x4 p1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, zero, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    acc[i][0][r] = fmaf(static_cast<float>(p0[r]), d0, acc[i][0][r]);
+                    acc[i][1][r] = fmaf(static_cast<float>(p1[r]), d1, acc[i][1][r]);
+                }
             }
         }
     }
+    __builtin_amdgcn_s_waitcnt(0);                         // the trailing copies land before exit
+    if (KS > 1) {
+        // half 1 hands its sums to half 0 through the (now idle) staging LDS
+        gemm_lds_barrier();
+        float4 *xfer = reinterpret_cast<float4 *>(lds_all);     // [group][i*2+j][lane]
+        if (half == 1 && active) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    xfer[(wid * 4 + i * 2 + j) * 64 + lane] =
+                        make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+        }
+        __syncthreads();
+        if (half == 1) return;
+        if (active) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const float4 v = xfer[(wid * 4 + i * 2 + j) * 64 + lane];
+                    acc[i][j][0] += v.x;
+                    acc[i][j][1] += v.y;
+                    acc[i][j][2] += v.z;
+                    acc[i][j][3] += v.w;
+                }
+        }
+    }
+    if (!active) return;
+    const int col[2] = {tile * 32 + c16, tile * 32 + 16 + c16};
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -436,12 +607,12 @@ extern "C" int kk_common_quant_pair(const void *x, int x_f16, int k, int kp, voi
 }
 
 extern "C" int kk_common_quant_rows(const void *x, int x_f16, int k, int kp, int rows, int defined_rows,
-                                    void *values, void *params, hipStream_t stream) {
-    if (!x || !values || !params || k <= 0 || kp < k || kp % 256 != 0 || rows <= 0 || defined_rows < rows ||
-        defined_rows % 32 != 0)
+                                    void *values, void *params, void *tiled, hipStream_t stream) {
+    if (!x || !values || !params || !tiled || k <= 0 || kp < k || kp % 256 != 0 || rows <= 0 ||
+        defined_rows < rows || defined_rows % 32 != 0)
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(common_quant_rows, dim3(defined_rows), dim3(kRowThreads), 0, stream, x, x_f16, k, kp, rows,
-                       static_cast<int8_t *>(values), static_cast<float *>(params));
+                       static_cast<int8_t *>(values), static_cast<float *>(params), static_cast<int8_t *>(tiled));
     return hipGetLastError();
 }
 
@@ -450,34 +621,51 @@ extern "C" size_t kk_common_gemv_lds_bytes(int kp, int exact) {
     return blocks * (exact ? 24 * 4 + 4 : 16 * 4) + static_cast<size_t>(kCqWaves) * 32 * 4;
 }
 
-extern "C" int kk_common_gemv(const void *w0, float *y0, const void *w1, float *y1, const void *act, int exact,
-                              int x_f16, const void *params, int k, int kp, int n, int np, hipStream_t stream) {
-    if (!w0 || !y0 || !act || (!exact && !params) || kp % 256 != 0 || kp > 16384 || np % 256 != 0 || n > np ||
-        k > kp || (reinterpret_cast<uintptr_t>(w0) & 255) != 0 || (w1 && (reinterpret_cast<uintptr_t>(w1) & 255)))
+extern "C" int kk_common_gemv(const void *w0, float *y0, const void *w1, float *y1, const void *act, int mode,
+                              int x_f16, void *params, void *view_values, int k, int kp, int n, int np,
+                              hipStream_t stream) {
+    if (!w0 || !y0 || !act || mode < 0 || mode > 2 || (mode != kExact && !params) ||
+        (mode == kQuantize && !view_values) || kp % 256 != 0 || kp > 16384 || np % 256 != 0 || n > np || k > kp ||
+        (reinterpret_cast<uintptr_t>(w0) & 255) != 0 || (w1 && (reinterpret_cast<uintptr_t>(w1) & 255)))
         return hipErrorInvalidValue;
     const int tiles = (n + 31) / 32;
     const int count = w1 ? 2 : 1;
-    const size_t lds = kk_common_gemv_lds_bytes(kp, exact);
+    const size_t lds = kk_common_gemv_lds_bytes(kp, mode == kExact);
     const GemvMatrix m0{static_cast<const uint8_t *>(w0), y0};
     const GemvMatrix m1{static_cast<const uint8_t *>(w1 ? w1 : w0), w1 ? y1 : y0};
-    if (exact)
-        hipLaunchKernelGGL(common_gemv<true>, dim3(tiles * count), dim3(kCqThreads), lds, stream, m0, m1, tiles, act,
-                           x_f16, static_cast<const float *>(params), k, kp, n, np);
+    const dim3 grid(tiles * count), block(kCqThreads);
+    int8_t *vv = static_cast<int8_t *>(view_values);
+    float *pp = static_cast<float *>(params);
+    if (mode == kExact)
+        hipLaunchKernelGGL(common_gemv<kExact>, grid, block, lds, stream, m0, m1, tiles, act, x_f16, pp, vv, pp, k,
+                           kp, n, np);
+    else if (mode == kQuantize)
+        hipLaunchKernelGGL(common_gemv<kQuantize>, grid, block, lds, stream, m0, m1, tiles, act, x_f16, pp, vv, pp,
+                           k, kp, n, np);
     else
-        hipLaunchKernelGGL(common_gemv<false>, dim3(tiles * count), dim3(kCqThreads), lds, stream, m0, m1, tiles, act,
-                           x_f16, static_cast<const float *>(params), k, kp, n, np);
+        hipLaunchKernelGGL(common_gemv<kPrepared>, grid, block, lds, stream, m0, m1, tiles, act, x_f16, pp, vv, pp,
+                           k, kp, n, np);
     return hipGetLastError();
 }
 
-extern "C" int kk_common_gemm(const void *w, const void *codes, const void *row_scales, float *y, int rows,
+extern "C" int kk_common_gemm(const void *w, const void *tiled, const void *row_scales, float *y, int rows,
                               int defined_rows, int kp, int n, int np, hipStream_t stream) {
-    if (!w || !codes || !row_scales || !y || rows <= 0 || rows > 128 || defined_rows < rows ||
+    // kp % 256 == 0 also makes the block count a multiple of the GEMM's ring depth
+    if (!w || !tiled || !row_scales || !y || rows <= 0 || rows > 128 || defined_rows < rows ||
         defined_rows % 32 != 0 || defined_rows > 128 || kp % 256 != 0 || np % 256 != 0 || n > np ||
-        (reinterpret_cast<uintptr_t>(w) & 255) != 0 || (reinterpret_cast<uintptr_t>(codes) & 7) != 0)
+        (reinterpret_cast<uintptr_t>(w) & 255) != 0 || (reinterpret_cast<uintptr_t>(tiled) & 15) != 0)
         return hipErrorInvalidValue;
     const int tiles = (n + 31) / 32;
-    hipLaunchKernelGGL(common_gemm, dim3(tiles), dim3(256), 0, stream, static_cast<const uint8_t *>(w),
-                       static_cast<const int8_t *>(codes), static_cast<const float *>(row_scales), y, rows,
-                       defined_rows, kp, n, np);
+    const uint8_t *wb = static_cast<const uint8_t *>(w);
+    const int8_t *tb = static_cast<const int8_t *>(tiled);
+    const float *rs = static_cast<const float *>(row_scales);
+    // two K halves per tile when Kp splits into whole stages (and the tiles
+    // alone would leave compute units idle)
+    if (kp % 512 == 0 && tiles < 1024)
+        hipLaunchKernelGGL(common_gemm<2>, dim3(tiles), dim3(512), 0, stream, wb, tb, rs, y, rows, defined_rows, kp,
+                           n, np);
+    else
+        hipLaunchKernelGGL(common_gemm<1>, dim3(tiles), dim3(256), 0, stream, wb, tb, rs, y, rows, defined_rows, kp,
+                           n, np);
     return hipGetLastError();
 }

@@ -62,17 +62,21 @@ int kk_native_q4_gemv(const void *weights, const void *x, int x_f16, float *y, i
 // the view buffer `values` (4*kp + 1024 bytes) and `params` (16 floats).
 int kk_common_quant_pair(const void *x, int x_f16, int k, int kp, void *values, void *params, hipStream_t stream);
 // M > 1 per-row int8 quantization of `rows` rows (zero rows up to
-// defined_rows, a multiple of 32): values [defined_rows][kp], params [defined_rows][16].
+// defined_rows, a multiple of 32): values [defined_rows][kp], params
+// [defined_rows][16], and the same codes in the GEMM's operand order in
+// `tiled` (defined_rows * kp bytes).
 int kk_common_quant_rows(const void *x, int x_f16, int k, int kp, int rows, int defined_rows, void *values,
-                         void *params, hipStream_t stream);
+                         void *params, void *tiled, hipStream_t stream);
 // M = 1 GEMV over one weight (w1 null) or two sharing the activations.
-// exact = 0: act = the quantized view, params its scales; exact = 1: act = X.
+// mode 0: act = the quantized view, params its scales; mode 1: act = X,
+// quantized in the kernel, the view written to view_values / params; mode 2:
+// act = X, exact.
 size_t kk_common_gemv_lds_bytes(int kp, int exact);
-int kk_common_gemv(const void *w0, float *y0, const void *w1, float *y1, const void *act, int exact, int x_f16,
-                   const void *params, int k, int kp, int n, int np, hipStream_t stream);
-// M > 1 (rows <= 128) GEMM on quantized rows (codes [defined_rows][kp], row
-// scales at row_scales[r*16]).
-int kk_common_gemm(const void *w, const void *codes, const void *row_scales, float *y, int rows, int defined_rows,
+int kk_common_gemv(const void *w0, float *y0, const void *w1, float *y1, const void *act, int mode, int x_f16,
+                   void *params, void *view_values, int k, int kp, int n, int np, hipStream_t stream);
+// M > 1 (rows <= 128) GEMM on quantized rows (codes in the tiled operand
+// order of kk_common_quant_rows, row scales at row_scales[r*16]).
+int kk_common_gemm(const void *w, const void *tiled, const void *row_scales, float *y, int rows, int defined_rows,
                    int kp, int n, int np, hipStream_t stream);
 
 // Bytes of device workspace kk_i8_quantize needs for `count` activations.

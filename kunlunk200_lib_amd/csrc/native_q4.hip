@@ -101,7 +101,10 @@ __global__ __launch_bounds__(kNqThreads) void native_q4_gemv(const uint8_t *__re
         buf[16] = sc.x;
         buf[17] = sc.y;
     };
-    const int my_items = wid < items ? (items - wid + kNqWaves - 1) / kNqWaves : 0;
+    // every wave runs the same padded count of items; items past the end load
+    // a valid address and add zero
+    const int iters = (items + kNqWaves - 1) / kNqWaves;
+    const int iters_padded = (iters + kNqDepth - 1) / kNqDepth * kNqDepth;
     uint32_t ring[kNqDepth][18];
 #pragma unroll
     for (int d = 0; d < kNqDepth; ++d) {
@@ -150,9 +153,10 @@ __global__ __launch_bounds__(kNqThreads) void native_q4_gemv(const uint8_t *__re
         for (int r = 0; r < 4; ++r) acc[b][r] = 0.0f;
 
     auto compute_item = [&](int s, const uint32_t (&buf)[18]) {
-        const int blk_raw = (wid + kNqWaves * s) * kNqItemBlocks + lane / kNqLanesPerBlock;
-        const bool live = blk_raw < blocks;
-        const int blk = min(blk_raw, blocks - 1);
+        const int it = wid + kNqWaves * s;
+        const int blk_raw = it * kNqItemBlocks + lane / kNqLanesPerBlock;
+        const bool live = it < items && blk_raw < blocks;
+        const int blk = min(min(it, items - 1) * kNqItemBlocks + lane / kNqLanesPerBlock, blocks - 1);
         float d[4];
         d[0] = kk::half_bits_to_float(buf[16] & 0xffffu);
         d[1] = kk::half_bits_to_float(buf[16] >> 16);
@@ -204,14 +208,12 @@ __global__ __launch_bounds__(kNqThreads) void native_q4_gemv(const uint8_t *__re
         }
     };
 
-    for (int base = 0; base < my_items; base += kNqDepth) {
+    for (int base = 0; base < iters_padded; base += kNqDepth) {
 #pragma unroll
         for (int dpt = 0; dpt < kNqDepth; ++dpt) {
-            const int s = base + dpt;
-            if (s < my_items) {
-                compute_item(s, ring[dpt]);
-                if (s + kNqDepth < my_items) load_item(s + kNqDepth, ring[dpt]);
-            }
+            compute_item(base + dpt, ring[dpt]);
+            load_item(base + dpt + kNqDepth, ring[dpt]);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 
