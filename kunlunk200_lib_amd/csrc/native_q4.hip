@@ -101,14 +101,14 @@ __global__ __launch_bounds__(kNqThreads) void native_q4_gemv(const uint8_t *__re
         buf[16] = sc.x;
         buf[17] = sc.y;
     };
-    // every wave runs the same padded count of items; items past the end load
-    // a valid address and add zero
+    // every wave runs the same count of items (the last ones may add zero);
+    // loads beyond that count are skipped by a uniform branch
     const int iters = (items + kNqWaves - 1) / kNqWaves;
     const int iters_padded = (iters + kNqDepth - 1) / kNqDepth * kNqDepth;
     uint32_t ring[kNqDepth][18];
 #pragma unroll
     for (int d = 0; d < kNqDepth; ++d) {
-        load_item(d, ring[d]);
+        if (d < iters) load_item(d, ring[d]);
         __builtin_amdgcn_sched_barrier(0);
     }
 
@@ -211,8 +211,8 @@ __global__ __launch_bounds__(kNqThreads) void native_q4_gemv(const uint8_t *__re
     for (int base = 0; base < iters_padded; base += kNqDepth) {
 #pragma unroll
         for (int dpt = 0; dpt < kNqDepth; ++dpt) {
-            compute_item(base + dpt, ring[dpt]);
-            load_item(base + dpt + kNqDepth, ring[dpt]);
+            if (base + dpt < iters) compute_item(base + dpt, ring[dpt]);   // uniform; no loads inside
+            if (base + dpt + kNqDepth < iters) load_item(base + dpt + kNqDepth, ring[dpt]);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
