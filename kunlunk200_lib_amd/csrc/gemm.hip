@@ -20,6 +20,7 @@
 #include "launch.h"
 
 #include <algorithm>
+#include <cstdio>
 #include <cstdlib>
 
 namespace {
@@ -29,6 +30,7 @@ using kk::kWave;
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float16v __attribute__((ext_vector_type(16)));
+typedef float float4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBM = 128, kBK = 128;            // tile N (64 or 128) is a template parameter
@@ -104,35 +106,83 @@ __global__ __launch_bounds__(kPrepassThreads) void x_to_f16(const float *__restr
 }
 
 // ---------------------------------------------------------------------------
-// Q4_0: half a block (nibble dwords 2*half, 2*half+1 -> 16 values) to fp16
-// (q - 8) * d / 8 in block order; e = the 18 block bytes as 5 dwords.
-__device__ __forceinline__ void decode_q4_half(const uint32_t (&e)[5], int half, bool live, half8 (&out)[2]) {
+// Q4_0 decode to fp16 (q - 8) * d / 8 (the 1/8 keeps |value| <= 65504 for
+// any F16 scale). dd = d / 8 in both halves (zero for a dead block).
+__device__ __forceinline__ half2v q4_scale8(uint32_t bits, bool live) {
     union { uint16_t u; _Float16 h; } du;
-    du.u = static_cast<uint16_t>(e[0] & 0xffffu);
+    du.u = static_cast<uint16_t>(bits & 0xffffu);
     const _Float16 d8 = live ? static_cast<_Float16>(du.h * static_cast<_Float16>(0.125f)) : static_cast<_Float16>(0.0f);
-    const half2v dd = {d8, d8};
+    return half2v{d8, d8};
+}
+
+// Nibble dword i of a block (bytes 4i .. 4i+3) -> the 8 values at block
+// positions 8i .. 8i+7 in block order.
+__device__ __forceinline__ half8 decode_q4_dword(uint32_t n, half2v dd) {
     const half2v off_lo = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
     const half2v sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
     const half2v off_hi = {static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
+    const uint32_t t = n >> 8;
+    union { uint32_t u; half2v h; } p0, p1, p2, p3;
+    p0.u = (n & 0x000f000fu) | 0x64006400u;   // 1024 + q(4i),    1024 + q(4i+2)
+    p1.u = (t & 0x000f000fu) | 0x64006400u;   // 1024 + q(4i+1),  1024 + q(4i+3)
+    p2.u = (n & 0x00f000f0u) | 0x64006400u;   // 1024 + 16 q(16+4i), ...
+    p3.u = (t & 0x00f000f0u) | 0x64006400u;
+    const half2v h0 = (p0.h + off_lo) * dd;   // (q - 8) exact, then one rounding
+    const half2v h1 = (p1.h + off_lo) * dd;
+    const half2v h2 = (p2.h * sixteenth + off_hi) * dd;
+    const half2v h3 = (p3.h * sixteenth + off_hi) * dd;
+    half8 o;
+    o[0] = h0[0]; o[1] = h0[1]; o[2] = h1[0]; o[3] = h1[1];
+    o[4] = h2[0]; o[5] = h2[1]; o[6] = h3[0]; o[7] = h3[1];
+    return o;
+}
+
+// Half a block (nibble dwords 2*half, 2*half+1 -> 16 values); e = the 18
+// block bytes as 5 dwords.
+__device__ __forceinline__ void decode_q4_half(const uint32_t (&e)[5], int half, bool live, half8 (&out)[2]) {
+    const half2v dd = q4_scale8(e[0], live);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const uint32_t lo = half ? e[2 + j] : e[j], hi = half ? e[3 + j] : e[1 + j];
-        const uint32_t n = kk::align_bytes(hi, lo, 2);   // nibble bytes 4i .. 4i+3, i = 2*half + j
-        const uint32_t t = n >> 8;
-        union { uint32_t u; half2v h; } p0, p1, p2, p3;
-        p0.u = (n & 0x000f000fu) | 0x64006400u;   // 1024 + q(4i),    1024 + q(4i+2)
-        p1.u = (t & 0x000f000fu) | 0x64006400u;   // 1024 + q(4i+1),  1024 + q(4i+3)
-        p2.u = (n & 0x00f000f0u) | 0x64006400u;   // 1024 + 16 q(16+4i), ...
-        p3.u = (t & 0x00f000f0u) | 0x64006400u;
-        const half2v h0 = (p0.h + off_lo) * dd;   // (q - 8) exact, then one rounding
-        const half2v h1 = (p1.h + off_lo) * dd;
-        const half2v h2 = (p2.h * sixteenth + off_hi) * dd;
-        const half2v h3 = (p3.h * sixteenth + off_hi) * dd;
-        half8 o;
-        o[0] = h0[0]; o[1] = h0[1]; o[2] = h1[0]; o[3] = h1[1];
-        o[4] = h2[0]; o[5] = h2[1]; o[6] = h3[0]; o[7] = h3[1];
-        out[j] = o;
+        out[j] = decode_q4_dword(kk::align_bytes(hi, lo, 2), dd);   // nibble bytes 4i .. 4i+3, i = 2*half + j
     }
+}
+
+// (a & mask) | bits in one VALU op (the compiler splits it in two when the
+// mask is a literal: gfx9 VOP3 takes none).
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(mask), "v"(bits));
+    return r;
+}
+
+// Nibble dword i of a block -> (q - 8) / 8 * d for block positions 8i .. 8i+7
+// in block order, d = the block's F16 scale bits. (q - 8) / 8 is exact:
+// p = 1024 + q gives p / 8 - 129, p = 1024 + 16 q gives p / 128 - 9; one
+// rounding in the product, |value| <= |d|.
+__device__ __forceinline__ half8 decode_q4_scaled(uint32_t n, uint32_t dbits) {
+    const uint32_t magic = 0x64006400u, mask_lo = 0x000f000fu, mask_hi = 0x00f000f0u;
+    const half2v lo_mul = {static_cast<_Float16>(0.125f), static_cast<_Float16>(0.125f)};
+    const half2v lo_add = {static_cast<_Float16>(-129.0f), static_cast<_Float16>(-129.0f)};
+    const half2v hi_mul = {static_cast<_Float16>(0.0078125f), static_cast<_Float16>(0.0078125f)};
+    const half2v hi_add = {static_cast<_Float16>(-9.0f), static_cast<_Float16>(-9.0f)};
+    union { uint16_t u; _Float16 h; } du;
+    du.u = static_cast<uint16_t>(dbits);
+    const half2v dd = {du.h, du.h};
+    const uint32_t t = n >> 8;
+    union { uint32_t u; half2v h; } p0, p1, p2, p3;
+    p0.u = and_or(n, mask_lo, magic);   // 1024 + q(4i),    1024 + q(4i+2)
+    p1.u = and_or(t, mask_lo, magic);   // 1024 + q(4i+1),  1024 + q(4i+3)
+    p2.u = and_or(n, mask_hi, magic);   // 1024 + 16 q(16+4i), ...
+    p3.u = and_or(t, mask_hi, magic);
+    const half2v h0 = (p0.h * lo_mul + lo_add) * dd;
+    const half2v h1 = (p1.h * lo_mul + lo_add) * dd;
+    const half2v h2 = (p2.h * hi_mul + hi_add) * dd;
+    const half2v h3 = (p3.h * hi_mul + hi_add) * dd;
+    half8 o;
+    o[0] = h0[0]; o[1] = h0[1]; o[2] = h1[0]; o[3] = h1[1];
+    o[4] = h2[0]; o[5] = h2[1]; o[6] = h3[0]; o[7] = h3[1];
+    return o;
 }
 
 // Workgroup tile 128 (M) x BN (N) x 128 (K) per step, 8 waves: two
@@ -398,6 +448,319 @@ __global__ __launch_bounds__(kGemmThreads) void mfma_gemm(const uint8_t *__restr
     }
 }
 
+// ---------------------------------------------------------------------------
+// q4_lds_gemm: Q4_0 weights, K % 128 == 0, 4-byte aligned weight pointers.
+//
+// Workgroup tile: BM activation rows x 4*WN weight rows; 8 waves. Wave w owns
+// weight rows WN*(w&3) .. +WN over all BM rows and takes K32 slices
+// 2*(w>>2), 2*(w>>2)+1 of every 128-K stage (two k-groups, whose sums meet in
+// LDS at the end in a fixed order).
+//
+// Per stage the 8 waves copy the activation tile (BM x 128 fp16) and the raw
+// Q4_0 bytes of the tile's weight rows (4 blocks = 72 B per row) from global
+// memory straight into LDS (global_load_lds: one contiguous 256 B or 1 KB LDS
+// range per wave instruction, no registers), two stages ahead into a ring of
+// three buffers. Each wave decodes its own columns' blocks from LDS into
+// v_mfma_f32_16x16x32_f16 B operands: a K32 slice is one Q4_0 block, and lane
+// l takes column l%16 and nibble dword l/16, whose 8 values are block
+// positions 8(l/16) .. +8 in the prepass's block order. No weight value is
+// decoded twice and no decoded weight passes through LDS.
+//
+// Activation row r of a stage is 16 chunks of 16 B; chunk c sits at position
+// c ^ (r & 15), so the 16 lanes reading one operand row group hit 16
+// distinct bank quads. MFMA layout (wave64): A[l%16][8(l/16) .. +8),
+// B[8(l/16) .. +8)[l%16], D[4(l/16) + r][l%16].
+//
+// Tiles are numbered weight-tile major and dealt to the 8 XCDs in contiguous
+// ranges: the M tiles of one weight tile share an XCD and its L2.
+constexpr int kQlK = 128;                   // K per stage
+constexpr int kQlBufs = 3;
+constexpr int kQlThreads = 512;
+constexpr int kQlRowStage = 72;             // raw bytes per weight row and stage
+
+template <int BM, int WN, bool PAIR>
+struct QlShape {
+    static constexpr int BN = 4 * WN;                                   // weight rows per tile
+    static constexpr int RG = BM / 16, CG = WN / 16;                    // MFMA tiles per wave
+    static constexpr int ABytes = BM * kQlK * 2;
+    // PAIR: gate rows, then up rows, each half a whole number of copies
+    static constexpr int HalfCopies = BN / 2 * (kQlRowStage / 4) / 64;
+    static_assert(!PAIR || HalfCopies * 64 == BN / 2 * (kQlRowStage / 4), "pair halves in whole copies");
+    static constexpr int BCopies = ((BN * kQlRowStage / 4 + 63) / 64 + 7) / 8 * 8;   // 256 B each
+    static constexpr int BBytes = BCopies * 256;                        // rows, then slack
+    static constexpr int StageBytes = ABytes + BBytes;
+    static constexpr int ACopiesPerWave = BM * 16 / 64 / 8;             // 1 KB each
+    static constexpr int BCopiesPerWave = BCopies / 8;
+    static constexpr int CopiesPerWave = ACopiesPerWave + BCopiesPerWave;
+    static constexpr int TileStride = BN + 4;                           // floats per LDS output row
+    static constexpr int XferBytes = BM * TileStride * 4;
+    static constexpr int RingBytes = kQlBufs * StageBytes > XferBytes ? kQlBufs * StageBytes : XferBytes;
+    static constexpr int LdsBytes = RingBytes + BM * 4;                 // + the tile's row scales
+    static_assert(CopiesPerWave <= 15, "vmcnt immediate");
+    static_assert(LdsBytes <= 160 * 1024, "LDS");
+};
+
+// One stage's copies (buffer_load ... lds) of a q4_lds_gemm workgroup's wave
+// `wid`: activation copies wid + 8t (1 KB each), weight copies wid + 8t
+// (256 B each; PAIR: below HalfCopies from the gate matrix, the next
+// HalfCopies from the up matrix). Offsets are per lane and fixed over
+// stages; the stage offset is the SGPR soffset. (A separate function, not a
+// lambda of the kernel: the host pass rejects a kernel-local lambda that
+// hands captured values to these builtins, and then drops the launch stub.)
+template <typename S, bool PAIR>
+__device__ __forceinline__ void ql_copy_stage(const uint32_t (&a_off)[S::ACopiesPerWave],
+                                              const uint32_t (&b_off)[S::BCopiesPerWave], _Float16 *a_tile,
+                                              int a_extent, uint8_t *b_tile, uint8_t *b_tile2, int b_extent, int wid,
+                                              int s, int buf_index) {
+    extern __shared__ __align__(16) uint8_t ql_lds[];
+    constexpr int kRsrcWord3 = 0x00020000;                      // gfx9 raw buffer
+    const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(a_tile, 0, a_extent, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(b_tile, 0, b_extent, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t b_rsrc2 = __builtin_amdgcn_make_buffer_rsrc(b_tile2, 0, b_extent, kRsrcWord3);
+    const int buf = buf_index * S::StageBytes;
+#pragma unroll
+    for (int t = 0; t < S::ACopiesPerWave; ++t)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (__attribute__((address_space(3))) uint8_t *)ql_lds + buf + (wid + 8 * t) * 1024,
+                                                 16, a_off[t], s * (kQlK * 2), 0, 0);
+#pragma unroll
+    for (int t = 0; t < S::BCopiesPerWave; ++t) {
+        const int i = wid + 8 * t;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(PAIR && i >= S::HalfCopies && i < 2 * S::HalfCopies ? b_rsrc2 : b_rsrc,
+                                                 (__attribute__((address_space(3))) uint8_t *)ql_lds + buf + S::ABytes + i * 256,
+                                                 4, b_off[t], s * kQlRowStage, 0, 0);
+    }
+}
+
+// PAIR: the stage's weight rows are the tile's BN/2 gate rows (matrix w), then
+// its BN/2 up rows (matrix w2); a wave's first CG/2 column tiles are gate and
+// its last CG/2 are up for the same output columns.
+template <int BM, int WN, bool PAIR>
+__global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restrict__ w, const uint8_t *__restrict__ w2,
+                                                         const _Float16 *__restrict__ x16,
+                                                         const float *__restrict__ row_inv, float *__restrict__ y,
+                                                         int m_rows, int n_rows, int k_pad, int stages,
+                                                         uint32_t row_bytes, int m_tiles, int tiles, int tiles_per_xcd) {
+    using S = QlShape<BM, WN, PAIR>;
+    static_assert(!PAIR || S::CG % 2 == 0, "pair tiles hold gate and up column tiles");
+    constexpr int kOut = PAIR ? S::BN / 2 : S::BN;             // output columns per tile
+    extern __shared__ __align__(16) uint8_t ql_lds[];
+
+    const int bid = blockIdx.x;
+    const int tile = (bid % kXcds) * tiles_per_xcd + bid / kXcds;
+    if (tile >= tiles) return;                                  // whole workgroup, before any barrier
+    const int nt = tile / m_tiles;
+    const int mt = tile - nt * m_tiles;
+    const int m0 = mt * BM, n0 = nt * kOut;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+    const int kh = wid >> 2, wn = wid & 3;
+    const int g = lane >> 4, c16 = lane & 15;
+    // The tile's row scales, loaded before the first copy and handed to the
+    // epilogue through LDS: no global load there (on gfx9 a wait for a load
+    // also waits for every store issued before it).
+    const float row_scale = threadIdx.x < BM ? row_inv[m0 + threadIdx.x] * 8.0f : 0.0f;
+    float *scale_lds = reinterpret_cast<float *>(ql_lds + S::RingBytes);
+
+    // Copies are raw buffer loads into LDS (buffer_load ... lds): the tile's
+    // base and extent in a buffer resource, the per-lane byte offset (fixed
+    // over stages) in a VGPR and the stage offset (256 B of activations, 72 B
+    // of weights per row) in an SGPR, so a copy costs no address arithmetic;
+    // reads past the resource's extent return 0.
+    // A copy i: rows 4i .. 4i+3 of the tile, lane -> row 4i + lane/16, LDS
+    // position lane%16, which holds chunk (lane%16) ^ (row & 15).
+    _Float16 *const a_tile = const_cast<_Float16 *>(x16 + static_cast<size_t>(m0) * k_pad);
+    const int a_extent = BM * k_pad * 2;
+    uint32_t a_off[S::ACopiesPerWave];
+#pragma unroll
+    for (int t = 0; t < S::ACopiesPerWave; ++t) {
+        const int r = 4 * (wid + 8 * t) + g;
+        a_off[t] = static_cast<uint32_t>(r * k_pad + 8 * (c16 ^ (r & 15))) * 2;
+    }
+    // B copy i: dwords 64i .. 64i+63 of the stage's [row][72 B] bytes (PAIR:
+    // copies below HalfCopies are gate rows, the next HalfCopies up rows);
+    // lanes past the last row copy a valid dword into the slack.
+    constexpr int kRows = PAIR ? S::BN / 2 : S::BN;             // weight rows per matrix and tile
+    const int b_extent = min(kRows, n_rows - n0) * static_cast<int>(row_bytes);
+    uint8_t *const b_tile = const_cast<uint8_t *>(w + static_cast<size_t>(n0) * row_bytes);
+    uint8_t *const b_tile2 = const_cast<uint8_t *>(w2 + static_cast<size_t>(n0) * row_bytes);
+    uint32_t b_off[S::BCopiesPerWave];
+#pragma unroll
+    for (int t = 0; t < S::BCopiesPerWave; ++t) {
+        const int i = wid + 8 * t;
+        const int d = (PAIR && i >= S::HalfCopies && i < 2 * S::HalfCopies ? i - S::HalfCopies : i) * 64 + lane;
+        const int row = min(d / (kQlRowStage / 4), kRows - 1);
+        const int dw = d - (d / (kQlRowStage / 4)) * (kQlRowStage / 4);
+        const int wrow = min(n0 + row, n_rows - 1) - n0;
+        b_off[t] = static_cast<uint32_t>(wrow) * row_bytes + 4 * dw;
+    }
+    auto copy_stage = [&](int s, int buf_index) {
+        ql_copy_stage<S, PAIR>(a_off, b_off, a_tile, a_extent, b_tile, b_tile2, b_extent, wid, s, buf_index);
+    };
+
+    float4v acc[S::RG][S::CG];
+#pragma unroll
+    for (int i = 0; i < S::RG; ++i)
+#pragma unroll
+        for (int j = 0; j < S::CG; ++j) acc[i][j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // One stage: this k-group's two K32 slices. Operand reads run one MFMA
+    // group ahead (the next two A row tiles, or the next slice's weight bytes
+    // and first A tiles, are read before the current group's MFMAs issue), so
+    // LDS latency hides behind MFMA work.
+    auto read_b = [&](const uint8_t *b_lds, int j, uint32_t (&nib)[S::CG], uint32_t (&sbits)[S::CG]) {
+#pragma unroll
+        for (int cg = 0; cg < S::CG; ++cg) {
+            const int brow = !PAIR ? wn * WN + cg * 16
+                                   : (cg < S::CG / 2 ? 0 : S::BN / 2) + wn * (WN / 2) + (cg % (S::CG / 2)) * 16;
+            const uint8_t *blk = b_lds + (brow + c16) * kQlRowStage + 18 * j;
+            sbits[cg] = *reinterpret_cast<const uint16_t *>(blk);
+            if ((j & 1) == 0) {   // even block: starts on a dword, nibble dword g at +2 + 4g
+                const uint32_t *p = reinterpret_cast<const uint32_t *>(blk + 4 * g);
+                nib[cg] = __builtin_amdgcn_alignbyte(p[1], p[0], 2);
+            } else {              // odd block: starts 2 B past a dword, nibble dword g on a dword
+                nib[cg] = *reinterpret_cast<const uint32_t *>(blk + 2 + 4 * g);
+            }
+        }
+    };
+    auto read_a = [&](const uint8_t *a_lds, int j, int rg) {
+        return *reinterpret_cast<const half8 *>(a_lds + (rg * 16 + c16) * 256 + ((4 * j + g) ^ c16) * 16);
+    };
+    auto compute = [&](const uint8_t *buf) {
+        const uint8_t *a_lds = buf;
+        const uint8_t *b_lds = buf + S::ABytes;
+        uint32_t nib[S::CG], sbits[S::CG];
+        read_b(b_lds, 2 * kh, nib, sbits);
+        half8 a0 = read_a(a_lds, 2 * kh, 0), a1 = read_a(a_lds, 2 * kh, 1);
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+            const int j = 2 * kh + jj;                          // the stage's block j (parity of jj)
+            half8 b[S::CG];
+#pragma unroll
+            for (int cg = 0; cg < S::CG; ++cg) b[cg] = decode_q4_scaled(nib[cg], sbits[cg]);
+#pragma unroll
+            for (int rg = 0; rg < S::RG; rg += 2) {
+                half8 n0 = a0, n1 = a1;
+                if (rg + 2 < S::RG) {
+                    n0 = read_a(a_lds, j, rg + 2);
+                    n1 = read_a(a_lds, j, rg + 3);
+                } else if (jj == 0) {
+                    read_b(b_lds, j + 1, nib, sbits);
+                    n0 = read_a(a_lds, j + 1, 0);
+                    n1 = read_a(a_lds, j + 1, 1);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int cg = 0; cg < S::CG; ++cg) {
+                    acc[rg][cg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b[cg], acc[rg][cg], 0, 0, 0);
+                    acc[rg + 1][cg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b[cg], acc[rg + 1][cg], 0, 0, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                a0 = n0;
+                a1 = n1;
+            }
+        }
+    };
+
+    // At the top of stage s only the copies of stage s+1 may still be in
+    // flight; the barrier makes every wave's copies of s visible and ends all
+    // reads of buffer (s+2) % 3 (stage s-1) before it is refilled.
+    copy_stage(0, 0);
+    if (stages > 1) copy_stage(1, 1);
+    int buf_index = 0;
+    for (int s = 0; s < stages; ++s) {
+        if (s + 1 < stages)
+            __builtin_amdgcn_s_waitcnt(0x0F70 | S::CopiesPerWave);
+        else
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");
+        if (s + 2 < stages) copy_stage(s + 2, buf_index == 0 ? 2 : buf_index - 1);
+        compute(ql_lds + buf_index * S::StageBytes);
+        buf_index = buf_index == kQlBufs - 1 ? 0 : buf_index + 1;
+    }
+
+    // Epilogue. k-group 1 writes its sums into a row-major LDS tile (row
+    // stride BN + 4 floats: the 4 rows of one write land 16 banks apart);
+    // k-group 0 adds its own (acc0 + acc1, a fixed order) and applies the row
+    // scales in place; then all waves store whole tile rows.
+    __syncthreads();                                            // ring idle
+    constexpr int kTs = S::TileStride;
+    float *tile_lds = reinterpret_cast<float *>(ql_lds);
+    if (threadIdx.x < BM) scale_lds[threadIdx.x] = row_scale;
+    if (kh == 1) {
+#pragma unroll
+        for (int rg = 0; rg < S::RG; ++rg)
+#pragma unroll
+            for (int cg = 0; cg < S::CG; ++cg)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    tile_lds[(rg * 16 + 4 * g + r) * kTs + wn * WN + cg * 16 + c16] = acc[rg][cg][r];
+    }
+    __syncthreads();
+    if constexpr (PAIR) {
+        // SiLU(gate) * up into acc's gate slots, then (after every read of the
+        // tile) into output columns 0 .. BN/2
+        constexpr int kHalf = S::CG / 2;
+        if (kh == 0) {
+#pragma unroll
+            for (int rg = 0; rg < S::RG; ++rg)
+#pragma unroll
+                for (int cg = 0; cg < kHalf; ++cg)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int row = rg * 16 + 4 * g + r;
+                        const float s = scale_lds[row];
+                        const float gs = (acc[rg][cg][r] + tile_lds[row * kTs + wn * WN + cg * 16 + c16]) * s;
+                        const float us = (acc[rg][cg + kHalf][r] + tile_lds[row * kTs + wn * WN + (cg + kHalf) * 16 + c16]) * s;
+                        acc[rg][cg][r] = kk::swiglu_value(gs, us);
+                    }
+        }
+        __syncthreads();
+        if (kh == 0) {
+#pragma unroll
+            for (int rg = 0; rg < S::RG; ++rg)
+#pragma unroll
+                for (int cg = 0; cg < kHalf; ++cg)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        tile_lds[(rg * 16 + 4 * g + r) * kTs + wn * (WN / 2) + cg * 16 + c16] = acc[rg][cg][r];
+        }
+    } else {
+        if (kh == 0) {
+#pragma unroll
+            for (int rg = 0; rg < S::RG; ++rg)
+#pragma unroll
+                for (int cg = 0; cg < S::CG; ++cg)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int row = rg * 16 + 4 * g + r;
+                        float *t = tile_lds + row * kTs + wn * WN + cg * 16 + c16;
+                        *t = (acc[rg][cg][r] + *t) * scale_lds[row];
+                    }
+        }
+    }
+    __syncthreads();
+    constexpr int kQuads = kOut / 4;
+    const bool vec = (n_rows & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+    for (int i = threadIdx.x; i < BM * kQuads; i += kQlThreads) {
+        const int row = i / kQuads, q = i - row * kQuads;
+        const int m = m0 + row, n = n0 + 4 * q;
+        if (m >= m_rows || n >= n_rows) continue;
+        const float4v v = *reinterpret_cast<const float4v *>(tile_lds + row * kTs + 4 * q);
+        float *dst = y + static_cast<size_t>(m) * n_rows + n;
+        if (vec && n + 3 < n_rows) {
+            *reinterpret_cast<float4v *>(dst) = v;
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                if (n + t < n_rows) dst[t] = v[t];
+        }
+    }
+}
+
 struct GemmPlan {
     int m_pad, k_pad, m_tiles, bn, n_tiles;
     size_t x16_bytes, row_inv_bytes;
@@ -443,6 +806,99 @@ hipError_t launch_gemm(const void *w, const void *w2, const _Float16 *x16, const
     return hipGetLastError();
 }
 
+constexpr int kMaxDevices = 64;
+
+int device_cus() {
+    static int cus[kMaxDevices] = {};
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) return 256;
+    if (cus[device] == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || v <= 0) v = 256;
+        cus[device] = v;
+    }
+    return cus[device];
+}
+
+struct QlTile {
+    int bm, wn;
+};
+
+// The candidate with the smallest estimated time: whole rounds of tiles over
+// the CUs x tile work, with penalties for the LDS activation reads per MFMA
+// (~1/WN) and the weight decode per MFMA (~1/BM). KUNLUN_GEMM_TILE=BMxWN
+// (e.g. 128x48) forces a candidate.
+QlTile pick_ql_tile(int batch, int n, bool pair) {
+    static const QlTile kAll[] = {{128, 64}, {128, 48}, {128, 32}, {64, 64}, {64, 32}};
+    auto allowed = [pair](const QlTile &t) { return !pair || t.wn % 32 == 0; };
+    const char *forced = std::getenv("KUNLUN_GEMM_TILE");
+    if (forced && *forced) {
+        int bm = 0, wn = 0;
+        if (std::sscanf(forced, "%dx%d", &bm, &wn) == 2)
+            for (const QlTile &t : kAll)
+                if (t.bm == bm && t.wn == wn && allowed(t)) return t;
+    }
+    const long cus = device_cus();
+    QlTile pick = {128, 64};
+    double best = 0.0;
+    for (const QlTile &t : kAll) {
+        if (!allowed(t)) continue;
+        const long out = pair ? 2 * t.wn : 4 * t.wn;
+        const long tiles = (static_cast<long>(batch) + t.bm - 1) / t.bm * ((n + out - 1) / out);
+        const long rounds = (tiles + cus - 1) / cus;
+        const double cost = static_cast<double>(rounds) * t.bm * 4 * t.wn * (1.0 + 16.0 / t.wn) * (1.0 + 32.0 / t.bm);
+        if (best == 0.0 || cost < best) {
+            best = cost;
+            pick = t;
+        }
+    }
+    return pick;
+}
+
+template <int BM, int WN, bool PAIR>
+hipError_t launch_ql_gemm(const void *w, const void *w2, const _Float16 *x16, const float *row_inv, float *y, int batch,
+                          int n, int k, int k_pad, hipStream_t stream) {
+    using S = QlShape<BM, WN, PAIR>;
+    static bool configured[kMaxDevices] = {};     // LDS above 64 KiB: opted into once per device
+    int device = 0;
+    hipError_t rc = hipGetDevice(&device);
+    if (rc != hipSuccess) return rc;
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    if (!configured[device]) {
+        rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&q4_lds_gemm<BM, WN, PAIR>),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, S::LdsBytes);
+        if (rc != hipSuccess) return rc;
+        configured[device] = true;
+    }
+    const int out = PAIR ? S::BN / 2 : S::BN;
+    const int m_tiles = (batch + BM - 1) / BM;
+    const int tiles = m_tiles * ((n + out - 1) / out);
+    const int tiles_per_xcd = (tiles + kXcds - 1) / kXcds;
+    const uint32_t row_bytes = static_cast<uint32_t>(k / 32 * 18);
+    hipLaunchKernelGGL((q4_lds_gemm<BM, WN, PAIR>), dim3(tiles_per_xcd * kXcds), dim3(kQlThreads), S::LdsBytes, stream,
+                       static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(w2), x16, row_inv, y, batch, n,
+                       k_pad, k / kQlK, row_bytes, m_tiles, tiles, tiles_per_xcd);
+    return hipGetLastError();
+}
+
+template <bool PAIR>
+hipError_t launch_ql(const void *w, const void *w2, const _Float16 *x16, const float *row_inv, float *y, int batch,
+                     int n, int k, int k_pad, hipStream_t stream) {
+    const QlTile t = pick_ql_tile(batch, n, PAIR);
+    if (t.bm == 128 && t.wn == 64) return launch_ql_gemm<128, 64, PAIR>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
+    if (t.bm == 128 && t.wn == 32) return launch_ql_gemm<128, 32, PAIR>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
+    if (t.bm == 64 && t.wn == 64) return launch_ql_gemm<64, 64, PAIR>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
+    if (t.bm == 64 && t.wn == 32) return launch_ql_gemm<64, 32, PAIR>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
+    if constexpr (!PAIR)
+        if (t.bm == 128 && t.wn == 48) return launch_ql_gemm<128, 48, false>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
+    return hipErrorInvalidValue;
+}
+
+// The LDS-copy Q4_0 GEMM takes K in whole 128-K stages and dword-aligned weights.
+bool ql_shape(int k, const void *w, const void *w2) {
+    return k % kQlK == 0 && (reinterpret_cast<uintptr_t>(w) & 3) == 0 && (reinterpret_cast<uintptr_t>(w2) & 3) == 0;
+}
+
 } // namespace
 
 extern "C" size_t kk_gemm_workspace_bytes(int k, int n, int batch) {
@@ -471,6 +927,7 @@ extern "C" int kk_gemm(int type, const void *w, const float *x, float *y, int k,
     if (rc != hipSuccess) return rc;
     const size_t w_bytes = type == 1 ? static_cast<size_t>(n) * k * 2 : static_cast<size_t>(n) * (k / 32) * 18;
     if (route) *route = type == 2 ? "q4_gemm_mfma" : "f16_gemm_mfma";
+    if (type == 2 && ql_shape(k, w, w)) return launch_ql<false>(w, w, x16, row_inv, y, batch, n, k, p.k_pad, stream);
     if (type == 2)
         return p.bn == 128 ? launch_gemm<false, 128>(w, w, x16, row_inv, y, batch, n, k, p, w_bytes, stream)
                            : launch_gemm<false, 64>(w, w, x16, row_inv, y, batch, n, k, p, w_bytes, stream);
@@ -502,6 +959,8 @@ extern "C" int kk_gemm_swiglu(int type, const void *w_gate, const void *w_up, co
     if (rc != hipSuccess) return rc;
     const size_t w_bytes = type == 1 ? static_cast<size_t>(n) * k * 2 : static_cast<size_t>(n) * (k / 32) * 18;
     if (route) *route = type == 2 ? "q4_gemm_swiglu_mfma" : "f16_gemm_swiglu_mfma";
+    if (type == 2 && ql_shape(k, w_gate, w_up))
+        return launch_ql<true>(w_gate, w_up, x16, row_inv, y, batch, n, k, p.k_pad, stream);
     if (type == 2) return launch_gemm<false, 128, true>(w_gate, w_up, x16, row_inv, y, batch, n, k, p, w_bytes, stream);
     return launch_gemm<true, 128, true>(w_gate, w_up, x16, row_inv, y, batch, n, k, p, w_bytes, stream);
 }

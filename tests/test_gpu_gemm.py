@@ -76,3 +76,53 @@ def test_gemm_matches_gemv_within_fp16(gpu, oracle, monkeypatch):
     _, ok, _ = check_gemm(y_gemm, gold, dec, x)
     assert ok
     assert np.max(np.abs(y_gemv - gold)) < np.max(np.abs(y_gemm - gold)) + 1e-6
+
+
+# Q4_0 with K % 128 == 0 and dword-aligned weights runs the LDS-copy kernel;
+# KUNLUN_GEMM_TILE forces each of its tile shapes (BM x WN, 4*WN weight rows).
+TILES = ["128x64", "128x48", "128x32", "64x64", "64x32"]
+TILE_SHAPES = [(384, 700, 200), (128, 64, 64), (256, 1000, 129)]   # partial M/N tiles; 1..3 K stages
+
+
+@pytest.mark.parametrize("tile", TILES)
+@pytest.mark.parametrize("k,n,batch", TILE_SHAPES)
+def test_gemm_tile_variants(gpu, oracle, monkeypatch, tile, k, n, batch):
+    monkeypatch.setenv("KUNLUN_GEMM_TILE", tile)
+    seed = k + n + batch
+    w = gaussian((n, k), 0.02, seed)
+    x = gaussian((batch, k), 1.0, seed + 1)
+    payload, dec = weight_payload(kl.WeightType.q4_0, w, oracle)
+    y, route, guard_ok = run_matmul(kl.WeightType.q4_0, payload, x, k, n, batch)
+    gold = oracle.gold(dec, x, threads=16)
+    finite, ok, rel = check_gemm(y, gold, dec, x)
+    print(f"  tile {tile} k={k} n={n} b={batch} rel={rel:.3g}", flush=True)
+    assert route == "q4_gemm_mfma"
+    assert guard_ok and finite and ok and rel <= 2e-3
+
+
+@pytest.mark.parametrize("w_offset", [2, 1])
+def test_gemm_misaligned_weights(gpu, oracle, w_offset):
+    # weights off a dword boundary take the register-staged kernel; same bound
+    k, n, batch = 512, 130, 96
+    w = gaussian((n, k), 0.02, 40 + w_offset)
+    x = gaussian((batch, k), 1.0, 41)
+    payload, dec = weight_payload(kl.WeightType.q4_0, w, oracle)
+    y, route, guard_ok = run_matmul(kl.WeightType.q4_0, payload, x, k, n, batch, w_offset=w_offset)
+    gold = oracle.gold(dec, x)
+    finite, ok, rel = check_gemm(y, gold, dec, x)
+    assert route == "q4_gemm_mfma"
+    assert guard_ok and finite and ok and rel <= 2e-3
+
+
+def test_gemm_tiles_agree_exactly(gpu, oracle, monkeypatch):
+    # every tile shape sums each output in the same order: identical bits
+    k, n, batch = 512, 384, 128
+    w = gaussian((n, k), 0.02, 50)
+    x = gaussian((batch, k), 1.0, 51)
+    payload, _ = weight_payload(kl.WeightType.q4_0, w, oracle)
+    outs = []
+    for tile in TILES:
+        monkeypatch.setenv("KUNLUN_GEMM_TILE", tile)
+        outs.append(run_matmul(kl.WeightType.q4_0, payload, x, k, n, batch)[0])
+    for y in outs[1:]:
+        assert np.array_equal(y.view(np.uint32), outs[0].view(np.uint32))

@@ -283,3 +283,20 @@ def test_matmul_swiglu_gemm_matches_two_matmuls(gpu, oracle):
     # the same fp16 products, so SiLU(g) * u agrees to F32 rounding
     expected = oracle.swiglu(g, u)
     assert np.allclose(fused, expected, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("tile", ["128x64", "128x32", "64x64", "64x32"])
+def test_matmul_swiglu_tile_variants(gpu, oracle, monkeypatch, tile):
+    # the pair tiles of the LDS-copy Q4_0 kernel: gate and up column tiles per wave
+    monkeypatch.setenv("KUNLUN_GEMM_TILE", tile)
+    k, n, batch = 384, 300, 130
+    wg = gaussian((n, k), 0.02, 61)
+    wu = gaussian((n, k), 0.02, 62)
+    x = gaussian((batch, k), 1.0, 63)
+    pg, dg = weight_payload(kl.WeightType.q4_0, wg, oracle)
+    pu, du = weight_payload(kl.WeightType.q4_0, wu, oracle)
+    y, route = run_pair(kl.WeightType.q4_0, pg, pu, x, k, n, batch)
+    finite, ok, worst = check_pair(y, x, dg, du, oracle, 2e-3)
+    print(f"  pair tile {tile} worst/bound={worst:.3g}", flush=True)
+    assert route == "q4_gemm_swiglu_mfma"
+    assert finite and ok
