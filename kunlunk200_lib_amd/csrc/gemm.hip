@@ -628,36 +628,59 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
     auto compute = [&](const uint8_t *buf) {
         const uint8_t *a_lds = buf;
         const uint8_t *b_lds = buf + S::ABytes;
+        const int j0 = 2 * kh, j1 = j0 + 1;                     // this k-group's blocks of the stage
         uint32_t nib[S::CG], sbits[S::CG];
-        read_b(b_lds, 2 * kh, nib, sbits);
-        half8 a0 = read_a(a_lds, 2 * kh, 0), a1 = read_a(a_lds, 2 * kh, 1);
+        half8 b0[S::CG], b1[S::CG];
+        read_b(b_lds, j0, nib, sbits);
+        half8 a0 = read_a(a_lds, j0, 0), a1 = read_a(a_lds, j0, 1);
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-            const int j = 2 * kh + jj;                          // the stage's block j (parity of jj)
-            half8 b[S::CG];
+        for (int cg = 0; cg < S::CG; ++cg) b0[cg] = decode_q4_scaled(nib[cg], sbits[cg]);
+        // Block j0: the first MFMA group also reads block j1's weight bytes,
+        // and each later group decodes some of them after issuing its MFMAs
+        // (the decode overlaps MFMA execution instead of stalling it).
 #pragma unroll
-            for (int cg = 0; cg < S::CG; ++cg) b[cg] = decode_q4_scaled(nib[cg], sbits[cg]);
-#pragma unroll
-            for (int rg = 0; rg < S::RG; rg += 2) {
-                half8 n0 = a0, n1 = a1;
-                if (rg + 2 < S::RG) {
-                    n0 = read_a(a_lds, j, rg + 2);
-                    n1 = read_a(a_lds, j, rg + 3);
-                } else if (jj == 0) {
-                    read_b(b_lds, j + 1, nib, sbits);
-                    n0 = read_a(a_lds, j + 1, 0);
-                    n1 = read_a(a_lds, j + 1, 1);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int cg = 0; cg < S::CG; ++cg) {
-                    acc[rg][cg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b[cg], acc[rg][cg], 0, 0, 0);
-                    acc[rg + 1][cg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b[cg], acc[rg + 1][cg], 0, 0, 0);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-                a0 = n0;
-                a1 = n1;
+        for (int rg = 0; rg < S::RG; rg += 2) {
+            const int grp = rg / 2;
+            half8 n0, n1;
+            if (rg + 2 < S::RG) {
+                n0 = read_a(a_lds, j0, rg + 2);
+                n1 = read_a(a_lds, j0, rg + 3);
+            } else {
+                n0 = read_a(a_lds, j1, 0);
+                n1 = read_a(a_lds, j1, 1);
             }
+            if (grp == 0) read_b(b_lds, j1, nib, sbits);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int cg = 0; cg < S::CG; ++cg) {
+                acc[rg][cg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b0[cg], acc[rg][cg], 0, 0, 0);
+                acc[rg + 1][cg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b0[cg], acc[rg + 1][cg], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int cg = 0; cg < S::CG; ++cg)
+                if (grp > 0 && (cg + 1 < S::RG / 2 ? cg + 1 : S::RG / 2 - 1) == grp)
+                    b1[cg] = decode_q4_scaled(nib[cg], sbits[cg]);
+            a0 = n0;
+            a1 = n1;
+        }
+        // Block j1.
+#pragma unroll
+        for (int rg = 0; rg < S::RG; rg += 2) {
+            half8 n0 = a0, n1 = a1;
+            if (rg + 2 < S::RG) {
+                n0 = read_a(a_lds, j1, rg + 2);
+                n1 = read_a(a_lds, j1, rg + 3);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int cg = 0; cg < S::CG; ++cg) {
+                acc[rg][cg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b1[cg], acc[rg][cg], 0, 0, 0);
+                acc[rg + 1][cg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b1[cg], acc[rg + 1][cg], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            a0 = n0;
+            a1 = n1;
         }
     };
 
