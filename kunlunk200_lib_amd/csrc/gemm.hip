@@ -449,18 +449,19 @@ __global__ __launch_bounds__(kGemmThreads) void mfma_gemm(const uint8_t *__restr
 }
 
 // ---------------------------------------------------------------------------
-// q4_lds_gemm: Q4_0 weights, K % 128 == 0, 4-byte aligned weight pointers.
+// q4_lds_gemm: Q4_0 weights, K % 256 == 0, 16-byte aligned weight pointers.
 //
 // Workgroup tile: BM activation rows x 4*WN weight rows; 8 waves. Wave w owns
 // weight rows WN*(w&3) .. +WN over all BM rows and takes K32 slices
 // 2*(w>>2), 2*(w>>2)+1 of every 128-K stage (two k-groups, whose sums meet in
 // LDS at the end in a fixed order).
 //
-// Per stage the 8 waves copy the activation tile (BM x 128 fp16) and the raw
-// Q4_0 bytes of the tile's weight rows (4 blocks = 72 B per row) from global
-// memory straight into LDS (global_load_lds: one contiguous 256 B or 1 KB LDS
-// range per wave instruction, no registers), two stages ahead into a ring of
-// three buffers. Each wave decodes its own columns' blocks from LDS into
+// The 8 waves copy the activation tile (BM x 128 fp16 per stage) and the raw
+// Q4_0 bytes of the tile's weight rows (8 blocks = 144 B = nine 16-byte
+// chunks per row and stage pair) from global memory straight into LDS
+// (buffer_load_dwordx4 ... lds: 1 KB of LDS per wave instruction, no
+// registers), two stages ahead: a ring of three activation stages and two
+// weight stage pairs. Each wave decodes its own columns' blocks from LDS into
 // v_mfma_f32_16x16x32_f16 B operands: a K32 slice is one Q4_0 block, and lane
 // l takes column l%16 and nibble dword l/16, whose 8 values are block
 // positions 8(l/16) .. +8 in the prepass's block order. No weight value is
@@ -473,61 +474,67 @@ __global__ __launch_bounds__(kGemmThreads) void mfma_gemm(const uint8_t *__restr
 //
 // Tiles are numbered weight-tile major and dealt to the 8 XCDs in contiguous
 // ranges: the M tiles of one weight tile share an XCD and its L2.
-constexpr int kQlK = 128;                   // K per stage
-constexpr int kQlBufs = 3;
+constexpr int kQlK = 128;                   // K per stage (4 Q4_0 blocks)
+constexpr int kQlABufs = 3;                 // activation stages in LDS
 constexpr int kQlThreads = 512;
-constexpr int kQlRowStage = 72;             // raw bytes per weight row and stage
+constexpr int kQlRowPair = 144;             // raw weight bytes per row and stage pair (8 blocks = 9 x 16 B)
 
 template <int BM, int WN, bool PAIR>
 struct QlShape {
     static constexpr int BN = 4 * WN;                                   // weight rows per tile
     static constexpr int RG = BM / 16, CG = WN / 16;                    // MFMA tiles per wave
-    static constexpr int ABytes = BM * kQlK * 2;
-    // PAIR: gate rows, then up rows, each half a whole number of copies
-    static constexpr int HalfCopies = BN / 2 * (kQlRowStage / 4) / 64;
-    static_assert(!PAIR || HalfCopies * 64 == BN / 2 * (kQlRowStage / 4), "pair halves in whole copies");
-    static constexpr int BCopies = ((BN * kQlRowStage / 4 + 63) / 64 + 7) / 8 * 8;   // 256 B each
-    static constexpr int BBytes = BCopies * 256;                        // rows, then slack
-    static constexpr int StageBytes = ABytes + BBytes;
-    static constexpr int ACopiesPerWave = BM * 16 / 64 / 8;             // 1 KB each
-    static constexpr int BCopiesPerWave = BCopies / 8;
-    static constexpr int CopiesPerWave = ACopiesPerWave + BCopiesPerWave;
+    static constexpr int ABytes = BM * kQlK * 2;                        // one stage of activations
+    static constexpr int BBytes = BN * kQlRowPair;                      // one stage pair of weights
+    static constexpr int ACopiesPerWave = BM * 16 / 64 / 8;             // 1 KB each, per stage
+    static constexpr int BCopies = BN * (kQlRowPair / 16) / 64;         // 1 KB each, per stage pair
+    static_assert(BCopies * 64 == BN * (kQlRowPair / 16), "whole weight copies");
+    static constexpr int HalfCopies = BCopies / 2;                      // PAIR: gate rows, then up rows
+    static_assert(!PAIR || HalfCopies * 64 == BN / 2 * (kQlRowPair / 16), "pair halves in whole copies");
+    static constexpr int BCopiesPerWave = (BCopies + 7) / 8;            // waves below BCopies % 8 (if
+    static constexpr int BCopiesRem = BCopies % 8;                      // not 0) issue one more
     static constexpr int TileStride = BN + 4;                           // floats per LDS output row
     static constexpr int XferBytes = BM * TileStride * 4;
-    static constexpr int RingBytes = kQlBufs * StageBytes > XferBytes ? kQlBufs * StageBytes : XferBytes;
+    static constexpr int CopyBytes = kQlABufs * ABytes + 2 * BBytes;
+    static constexpr int RingBytes = CopyBytes > XferBytes ? CopyBytes : XferBytes;
     static constexpr int LdsBytes = RingBytes + BM * 4;                 // + the tile's row scales
-    static_assert(CopiesPerWave <= 15, "vmcnt immediate");
+    static_assert(ACopiesPerWave + BCopiesPerWave <= 15, "vmcnt immediate");
     static_assert(LdsBytes <= 160 * 1024, "LDS");
 };
 
-// One stage's copies (buffer_load ... lds) of a q4_lds_gemm workgroup's wave
-// `wid`: activation copies wid + 8t (1 KB each), weight copies wid + 8t
-// (256 B each; PAIR: below HalfCopies from the gate matrix, the next
-// HalfCopies from the up matrix). Offsets are per lane and fixed over
-// stages; the stage offset is the SGPR soffset. (A separate function, not a
-// lambda of the kernel: the host pass rejects a kernel-local lambda that
-// hands captured values to these builtins, and then drops the launch stub.)
-template <typename S, bool PAIR>
-__device__ __forceinline__ void ql_copy_stage(const uint32_t (&a_off)[S::ACopiesPerWave],
-                                              const uint32_t (&b_off)[S::BCopiesPerWave], _Float16 *a_tile,
-                                              int a_extent, uint8_t *b_tile, uint8_t *b_tile2, int b_extent, int wid,
-                                              int s, int buf_index) {
+// Copies of a q4_lds_gemm workgroup's wave `wid` (buffer_load_dwordx4 ... lds,
+// 1 KB of LDS each): the activation copies wid + 8t of stage s into A buffer
+// s % 3, and the weight copies wid + 8t (below BCopies; PAIR: below
+// HalfCopies from the gate matrix, the rest from the up matrix) of stage pair
+// p into B buffer p % 2. Offsets are per lane and fixed over stages; the stage
+// offset is the SGPR soffset. (Separate functions, not lambdas of the kernel:
+// the host pass rejects a kernel-local lambda that hands captured values to
+// these builtins, and then drops the launch stub.)
+template <typename S>
+__device__ __forceinline__ void ql_copy_a(const uint32_t (&a_off)[S::ACopiesPerWave], _Float16 *a_tile, int a_extent,
+                                          int wid, int s) {
     extern __shared__ __align__(16) uint8_t ql_lds[];
-    constexpr int kRsrcWord3 = 0x00020000;                      // gfx9 raw buffer
-    const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(a_tile, 0, a_extent, kRsrcWord3);
-    const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(b_tile, 0, b_extent, kRsrcWord3);
-    const __amdgpu_buffer_rsrc_t b_rsrc2 = __builtin_amdgcn_make_buffer_rsrc(b_tile2, 0, b_extent, kRsrcWord3);
-    const int buf = buf_index * S::StageBytes;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(a_tile, 0, a_extent, 0x00020000);
+    const int buf = (s % kQlABufs) * S::ABytes;
 #pragma unroll
     for (int t = 0; t < S::ACopiesPerWave; ++t)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (__attribute__((address_space(3))) uint8_t *)ql_lds + buf + (wid + 8 * t) * 1024,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) uint8_t *)ql_lds + buf + (wid + 8 * t) * 1024,
                                                  16, a_off[t], s * (kQlK * 2), 0, 0);
+}
+
+template <typename S, bool PAIR>
+__device__ __forceinline__ void ql_copy_b(const uint32_t (&b_off)[S::BCopiesPerWave], uint8_t *b_tile,
+                                          uint8_t *b_tile2, int b_extent, int wid, int p) {
+    extern __shared__ __align__(16) uint8_t ql_lds[];
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(b_tile, 0, b_extent, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsrc2 = __builtin_amdgcn_make_buffer_rsrc(b_tile2, 0, b_extent, 0x00020000);
+    const int buf = kQlABufs * S::ABytes + (p & 1) * S::BBytes;
 #pragma unroll
     for (int t = 0; t < S::BCopiesPerWave; ++t) {
         const int i = wid + 8 * t;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(PAIR && i >= S::HalfCopies && i < 2 * S::HalfCopies ? b_rsrc2 : b_rsrc,
-                                                 (__attribute__((address_space(3))) uint8_t *)ql_lds + buf + S::ABytes + i * 256,
-                                                 4, b_off[t], s * kQlRowStage, 0, 0);
+        if (i < S::BCopies)                                     // wave-uniform
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(PAIR && i >= S::HalfCopies ? rsrc2 : rsrc,
+                                                     (__attribute__((address_space(3))) uint8_t *)ql_lds + buf + i * 1024,
+                                                     16, b_off[t], p * kQlRowPair, 0, 0);
     }
 }
 
@@ -563,9 +570,9 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
 
     // Copies are raw buffer loads into LDS (buffer_load ... lds): the tile's
     // base and extent in a buffer resource, the per-lane byte offset (fixed
-    // over stages) in a VGPR and the stage offset (256 B of activations, 72 B
-    // of weights per row) in an SGPR, so a copy costs no address arithmetic;
-    // reads past the resource's extent return 0.
+    // over stages) in a VGPR and the stage offset (256 B of activations per
+    // row and stage, 144 B of weights per row and stage pair) in an SGPR, so a
+    // copy costs no address arithmetic; reads past the extent return 0.
     // A copy i: rows 4i .. 4i+3 of the tile, lane -> row 4i + lane/16, LDS
     // position lane%16, which holds chunk (lane%16) ^ (row & 15).
     _Float16 *const a_tile = const_cast<_Float16 *>(x16 + static_cast<size_t>(m0) * k_pad);
@@ -576,9 +583,8 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
         const int r = 4 * (wid + 8 * t) + g;
         a_off[t] = static_cast<uint32_t>(r * k_pad + 8 * (c16 ^ (r & 15))) * 2;
     }
-    // B copy i: dwords 64i .. 64i+63 of the stage's [row][72 B] bytes (PAIR:
-    // copies below HalfCopies are gate rows, the next HalfCopies up rows);
-    // lanes past the last row copy a valid dword into the slack.
+    // B copy i: 16-byte chunks 64c .. 64c+63 (c = i, or i - HalfCopies for the
+    // up rows of PAIR) of the [row][144 B] stage-pair bytes, 9 chunks per row.
     constexpr int kRows = PAIR ? S::BN / 2 : S::BN;             // weight rows per matrix and tile
     const int b_extent = min(kRows, n_rows - n0) * static_cast<int>(row_bytes);
     uint8_t *const b_tile = const_cast<uint8_t *>(w + static_cast<size_t>(n0) * row_bytes);
@@ -587,15 +593,14 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
 #pragma unroll
     for (int t = 0; t < S::BCopiesPerWave; ++t) {
         const int i = wid + 8 * t;
-        const int d = (PAIR && i >= S::HalfCopies && i < 2 * S::HalfCopies ? i - S::HalfCopies : i) * 64 + lane;
-        const int row = min(d / (kQlRowStage / 4), kRows - 1);
-        const int dw = d - (d / (kQlRowStage / 4)) * (kQlRowStage / 4);
+        const int q = (PAIR && i >= S::HalfCopies ? i - S::HalfCopies : i) * 64 + lane;
+        const int row = min(q / (kQlRowPair / 16), kRows - 1);
+        const int chunk = q - (q / (kQlRowPair / 16)) * (kQlRowPair / 16);
         const int wrow = min(n0 + row, n_rows - 1) - n0;
-        b_off[t] = static_cast<uint32_t>(wrow) * row_bytes + 4 * dw;
+        b_off[t] = static_cast<uint32_t>(wrow) * row_bytes + 16 * chunk;
     }
-    auto copy_stage = [&](int s, int buf_index) {
-        ql_copy_stage<S, PAIR>(a_off, b_off, a_tile, a_extent, b_tile, b_tile2, b_extent, wid, s, buf_index);
-    };
+    // this wave's copies per stage (activations) and per stage pair (weights)
+    const int my_b_copies = S::BCopiesRem == 0 || wid < S::BCopiesRem ? S::BCopiesPerWave : S::BCopiesPerWave - 1;
 
     float4v acc[S::RG][S::CG];
 #pragma unroll
@@ -607,12 +612,14 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
     // group ahead (the next two A row tiles, or the next slice's weight bytes
     // and first A tiles, are read before the current group's MFMAs issue), so
     // LDS latency hides behind MFMA work.
+    // b_lds: this stage's 72 bytes of each weight row (row stride 144 B; the
+    // 16 rows of one read land in 16 distinct banks).
     auto read_b = [&](const uint8_t *b_lds, int j, uint32_t (&nib)[S::CG], uint32_t (&sbits)[S::CG]) {
 #pragma unroll
         for (int cg = 0; cg < S::CG; ++cg) {
             const int brow = !PAIR ? wn * WN + cg * 16
                                    : (cg < S::CG / 2 ? 0 : S::BN / 2) + wn * (WN / 2) + (cg % (S::CG / 2)) * 16;
-            const uint8_t *blk = b_lds + (brow + c16) * kQlRowStage + 18 * j;
+            const uint8_t *blk = b_lds + (brow + c16) * kQlRowPair + 18 * j;
             sbits[cg] = *reinterpret_cast<const uint16_t *>(blk);
             if ((j & 1) == 0) {   // even block: starts on a dword, nibble dword g at +2 + 4g
                 const uint32_t *p = reinterpret_cast<const uint32_t *>(blk + 4 * g);
@@ -625,9 +632,7 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
     auto read_a = [&](const uint8_t *a_lds, int j, int rg) {
         return *reinterpret_cast<const half8 *>(a_lds + (rg * 16 + c16) * 256 + ((4 * j + g) ^ c16) * 16);
     };
-    auto compute = [&](const uint8_t *buf) {
-        const uint8_t *a_lds = buf;
-        const uint8_t *b_lds = buf + S::ABytes;
+    auto compute = [&](const uint8_t *a_lds, const uint8_t *b_lds) {
         const int j0 = 2 * kh, j1 = j0 + 1;                     // this k-group's blocks of the stage
         uint32_t nib[S::CG], sbits[S::CG];
         half8 b0[S::CG], b1[S::CG];
@@ -684,25 +689,36 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
         }
     };
 
-    // At the top of stage s only the copies of stage s+1 may still be in
-    // flight; the barrier makes every wave's copies of s visible and ends all
-    // reads of buffer (s+2) % 3 (stage s-1) before it is refilled.
-    copy_stage(0, 0);
-    if (stages > 1) copy_stage(1, 1);
-    int buf_index = 0;
+    // Issue order: A(0), B(0), A(1); then at stage s (after its wait and the
+    // barrier) A(s+2) and, at even s, B(s/2 + 1). The memory counter is in
+    // order, so at the top of stage s: even s needs A(s) and B(s/2), which
+    // leaves A(s+1) in flight; odd s needs A(s), which leaves A(s+1) and
+    // B((s+1)/2) in flight. The barrier then makes every wave's copies
+    // visible and ends all reads of the buffers the next copies refill
+    // (stage s-1's activations, stage pair s/2 - 1's weights).
+    ql_copy_a<S>(a_off, a_tile, a_extent, wid, 0);
+    ql_copy_b<S, PAIR>(b_off, b_tile, b_tile2, b_extent, wid, 0);
+    if (stages > 1) ql_copy_a<S>(a_off, a_tile, a_extent, wid, 1);
     for (int s = 0; s < stages; ++s) {
-        if (s + 1 < stages)
-            __builtin_amdgcn_s_waitcnt(0x0F70 | S::CopiesPerWave);
-        else
+        if (s + 1 >= stages)
             __builtin_amdgcn_s_waitcnt(0x0F70);
+        else if ((s & 1) == 0)
+            __builtin_amdgcn_s_waitcnt(0x0F70 | S::ACopiesPerWave);
+        else if (my_b_copies == S::BCopiesPerWave)              // wave-uniform
+            __builtin_amdgcn_s_waitcnt(0x0F70 | (S::ACopiesPerWave + S::BCopiesPerWave));
+        else
+            __builtin_amdgcn_s_waitcnt(0x0F70 | (S::ACopiesPerWave + S::BCopiesPerWave - 1));
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("" ::: "memory");
-        if (s + 2 < stages) copy_stage(s + 2, buf_index == 0 ? 2 : buf_index - 1);
-        compute(ql_lds + buf_index * S::StageBytes);
-        buf_index = buf_index == kQlBufs - 1 ? 0 : buf_index + 1;
+        if (s + 2 < stages) {
+            ql_copy_a<S>(a_off, a_tile, a_extent, wid, s + 2);
+            if ((s & 1) == 0) ql_copy_b<S, PAIR>(b_off, b_tile, b_tile2, b_extent, wid, s / 2 + 1);
+        }
+        compute(ql_lds + (s % kQlABufs) * S::ABytes,
+                ql_lds + kQlABufs * S::ABytes + ((s >> 1) & 1) * S::BBytes + (s & 1) * (kQlRowPair / 2));
     }
 
     // Epilogue. k-group 1 writes its sums into a row-major LDS tile (row
@@ -775,7 +791,7 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
         const float4v v = *reinterpret_cast<const float4v *>(tile_lds + row * kTs + 4 * q);
         float *dst = y + static_cast<size_t>(m) * n_rows + n;
         if (vec && n + 3 < n_rows) {
-            *reinterpret_cast<float4v *>(dst) = v;
+            __builtin_nontemporal_store(v, reinterpret_cast<float4v *>(dst));   // streamed out, not kept in L2
         } else {
 #pragma unroll
             for (int t = 0; t < 4; ++t)
@@ -852,7 +868,7 @@ struct QlTile {
 // (~1/WN) and the weight decode per MFMA (~1/BM). KUNLUN_GEMM_TILE=BMxWN
 // (e.g. 128x48) forces a candidate.
 QlTile pick_ql_tile(int batch, int n, bool pair) {
-    static const QlTile kAll[] = {{128, 64}, {128, 48}, {128, 32}, {64, 64}, {64, 32}};
+    static const QlTile kAll[] = {{128, 48}, {128, 32}, {64, 64}, {64, 32}};
     auto allowed = [pair](const QlTile &t) { return !pair || t.wn % 32 == 0; };
     const char *forced = std::getenv("KUNLUN_GEMM_TILE");
     if (forced && *forced) {
@@ -862,7 +878,7 @@ QlTile pick_ql_tile(int batch, int n, bool pair) {
                 if (t.bm == bm && t.wn == wn && allowed(t)) return t;
     }
     const long cus = device_cus();
-    QlTile pick = {128, 64};
+    QlTile pick = {128, 32};
     double best = 0.0;
     for (const QlTile &t : kAll) {
         if (!allowed(t)) continue;
@@ -908,7 +924,6 @@ template <bool PAIR>
 hipError_t launch_ql(const void *w, const void *w2, const _Float16 *x16, const float *row_inv, float *y, int batch,
                      int n, int k, int k_pad, hipStream_t stream) {
     const QlTile t = pick_ql_tile(batch, n, PAIR);
-    if (t.bm == 128 && t.wn == 64) return launch_ql_gemm<128, 64, PAIR>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
     if (t.bm == 128 && t.wn == 32) return launch_ql_gemm<128, 32, PAIR>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
     if (t.bm == 64 && t.wn == 64) return launch_ql_gemm<64, 64, PAIR>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
     if (t.bm == 64 && t.wn == 32) return launch_ql_gemm<64, 32, PAIR>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
@@ -917,9 +932,11 @@ hipError_t launch_ql(const void *w, const void *w2, const _Float16 *x16, const f
     return hipErrorInvalidValue;
 }
 
-// The LDS-copy Q4_0 GEMM takes K in whole 128-K stages and dword-aligned weights.
+// The LDS-copy Q4_0 GEMM takes K in whole stage pairs (256) and 16-byte aligned
+// weights (rows of (K / 256) * 144 bytes, copied 16 bytes per lane).
 bool ql_shape(int k, const void *w, const void *w2) {
-    return k % kQlK == 0 && (reinterpret_cast<uintptr_t>(w) & 3) == 0 && (reinterpret_cast<uintptr_t>(w2) & 3) == 0;
+    return k % (2 * kQlK) == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(w2) & 15) == 0;
 }
 
 } // namespace

@@ -26,7 +26,7 @@ def check_gemm(y, gold, w_dec, x, tol=2e-3):
 
 
 SHAPES = [(4096, 4096, 512), (4096, 11008, 512), (256, 65, 64), (96, 17, 70), (512, 300, 130),
-          (16384, 64, 64), (1024, 129, 200)]
+          (16384, 64, 64), (1024, 129, 200), (384, 200, 96)]
 
 
 @pytest.mark.parametrize("type_", [kl.WeightType.q4_0, kl.WeightType.f16], ids=["q4_0", "f16"])
@@ -78,10 +78,11 @@ def test_gemm_matches_gemv_within_fp16(gpu, oracle, monkeypatch):
     assert np.max(np.abs(y_gemv - gold)) < np.max(np.abs(y_gemm - gold)) + 1e-6
 
 
-# Q4_0 with K % 128 == 0 and dword-aligned weights runs the LDS-copy kernel;
-# KUNLUN_GEMM_TILE forces each of its tile shapes (BM x WN, 4*WN weight rows).
-TILES = ["128x64", "128x48", "128x32", "64x64", "64x32"]
-TILE_SHAPES = [(384, 700, 200), (128, 64, 64), (256, 1000, 129)]   # partial M/N tiles; 1..3 K stages
+# Q4_0 with K % 256 == 0 and 16-byte aligned weights runs the LDS-copy kernel
+# (other shapes the register-staged one); KUNLUN_GEMM_TILE forces each of its
+# tile shapes (BM x WN, 4*WN weight rows).
+TILES = ["128x48", "128x32", "64x64", "64x32"]
+TILE_SHAPES = [(512, 700, 200), (256, 64, 64), (768, 1000, 129)]   # partial M/N tiles; 2..6 K stages
 
 
 @pytest.mark.parametrize("tile", TILES)
@@ -100,9 +101,9 @@ def test_gemm_tile_variants(gpu, oracle, monkeypatch, tile, k, n, batch):
     assert guard_ok and finite and ok and rel <= 2e-3
 
 
-@pytest.mark.parametrize("w_offset", [2, 1])
+@pytest.mark.parametrize("w_offset", [2, 1, 8])
 def test_gemm_misaligned_weights(gpu, oracle, w_offset):
-    # weights off a dword boundary take the register-staged kernel; same bound
+    # weights off a 16-byte boundary take the register-staged kernel; same bound
     k, n, batch = 512, 130, 96
     w = gaussian((n, k), 0.02, 40 + w_offset)
     x = gaussian((batch, k), 1.0, 41)

@@ -285,11 +285,11 @@ def test_matmul_swiglu_gemm_matches_two_matmuls(gpu, oracle):
     assert np.allclose(fused, expected, rtol=1e-5, atol=1e-6)
 
 
-@pytest.mark.parametrize("tile", ["128x64", "128x32", "64x64", "64x32"])
+@pytest.mark.parametrize("tile", ["128x32", "64x64", "64x32"])
 def test_matmul_swiglu_tile_variants(gpu, oracle, monkeypatch, tile):
     # the pair tiles of the LDS-copy Q4_0 kernel: gate and up column tiles per wave
     monkeypatch.setenv("KUNLUN_GEMM_TILE", tile)
-    k, n, batch = 384, 300, 130
+    k, n, batch = 512, 300, 130
     wg = gaussian((n, k), 0.02, 61)
     wu = gaussian((n, k), 0.02, 62)
     x = gaussian((batch, k), 1.0, 63)
