@@ -44,11 +44,13 @@ int gemm_min_batch() {
 }
 
 // Batch range of the single-pass Q4_0 MFMA GEMV (KUNLUN_Q4_MFMA_MIN/MAX, within
-// 1..16). Below 5 columns the batch-1 kernel's passes (two columns each) are faster.
-bool q4_mfma_batch(int batch) {
+// 1..16). Below the minimum the batch-1 kernel's passes (two columns each) are
+// faster: the streamed kernel (K % 256 == 0, 16-byte aligned weights) wins from
+// 3 columns, the register-staged one from 5.
+bool q4_mfma_batch(int batch, bool streamed) {
     const char * lo = std::getenv("KUNLUN_Q4_MFMA_MIN");
     const char * hi = std::getenv("KUNLUN_Q4_MFMA_MAX");
-    const int min_b = std::max(1, lo && *lo ? std::atoi(lo) : 5);
+    const int min_b = std::max(1, lo && *lo ? std::atoi(lo) : streamed ? 3 : 5);
     const int max_b = std::min(16, hi && *hi ? std::atoi(hi) : 16);
     return batch >= min_b && batch <= max_b;
 }
@@ -130,7 +132,8 @@ void matmul(Kernel & kernel, int id, void * y, const void * w, const void * x, i
                                                          static_cast<float *>(y), k, n, batch, ctx.stream),
                           "kk_dense_mfma_gemv");
         impl.route = type == WeightType::f16 ? "f16_mfma_gemv" : "f32_mfma_gemv";
-    } else if (type == WeightType::q4_0 && q4_mfma_batch(batch) && k % 64 == 0 && ((uintptr_t)w & 3) == 0) {
+    } else if (type == WeightType::q4_0 && q4_mfma_batch(batch, k % 256 == 0 && ((uintptr_t)w & 15) == 0) &&
+               k % 64 == 0 && ((uintptr_t)w & 3) == 0) {
         grow(id, ctx, impl.gemm_workspace, impl.gemm_workspace_size, kk_q4_mfma_gemv_workspace_bytes(k));
         detail::check_hip((hipError_t)kk_q4_mfma_gemv(w, static_cast<const float *>(x), static_cast<float *>(y), k, n,
                                                       batch, impl.gemm_workspace, ctx.cus, ctx.stream),

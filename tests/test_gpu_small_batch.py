@@ -7,8 +7,8 @@ f32-accumulate bound |err| <= 1e-4 * ||x_b|| * ||w_r||.
 import numpy as np
 import pytest
 
-# The MFMA GEMV takes batch 5..16 by default; tests reach batch 2..4 through
-# KUNLUN_Q4_MFMA_MIN (read per call).
+# The MFMA GEMV takes batch 3..16 (streamed kernel) or 5..16 by default; tests
+# reach the smaller batches through KUNLUN_Q4_MFMA_MIN (read per call).
 
 import kunlunk200_lib_amd as kl
 from gpu_util import check_f32_accumulate, run_matmul
@@ -51,6 +51,40 @@ def test_tails(gpu, oracle, k, n, batch):
     y, route, guard_ok, res = q4_case(oracle, k, n, batch, k + n + batch)
     assert route == "q4_mfma_gemv"
     assert guard_ok and res["finite"] and res["north_star"] and res["reference"]
+
+
+def test_weights_off_16_bytes(gpu, oracle):
+    # K % 256 == 0 streams through LDS when the weights are 16-byte aligned;
+    # 4-byte aligned weights take the chunked kernel: same bound either way
+    k, n, batch = 2048, 300, 7
+    w = gaussian((n, k), 0.02, 91)
+    x = gaussian((batch, k), 1.0, 92)
+    q4 = kl.quantize_q4_0(w)
+    dec = oracle.q4_decode(q4, k, n)
+    gold = oracle.gold(dec, x)
+    for w_offset in (0, 4):
+        y, route, guard_ok = run_matmul(kl.WeightType.q4_0, q4, x, k, n, batch, w_offset=w_offset)
+        res = check_f32_accumulate(y, gold, dec, x)
+        assert route == "q4_mfma_gemv"
+        assert guard_ok and res["finite"] and res["north_star"] and res["reference"]
+
+
+def test_default_batch_routing(gpu, oracle, monkeypatch):
+    # defaults: the streamed kernel (K % 256 == 0, 16-byte aligned weights)
+    # from batch 3, the register-staged one from batch 5, batch-1 passes below
+    monkeypatch.delenv("KUNLUN_Q4_MFMA_MIN")
+    cases = [(512, 3, 0, "q4_mfma_gemv"), (512, 2, 0, "q4_gemv_dot8"), (576, 3, 0, "q4_gemv_dot8"),
+             (576, 5, 0, "q4_mfma_gemv"), (512, 4, 4, "q4_gemv_dot8")]
+    for k, batch, w_offset, want in cases:
+        w = gaussian((70, k), 0.02, k + batch)
+        x = gaussian((batch, k), 1.0, k + batch + 1)
+        q4 = kl.quantize_q4_0(w)
+        dec = oracle.q4_decode(q4, k, 70)
+        y, route, guard_ok = run_matmul(kl.WeightType.q4_0, q4, x, k, 70, batch, w_offset=w_offset)
+        res = check_f32_accumulate(y, oracle.gold(dec, x), dec, x)
+        print(f"  k={k} b={batch} w_offset={w_offset} route={route}", flush=True)
+        assert route == want, (k, batch, w_offset, route)
+        assert guard_ok and res["finite"] and res["north_star"] and res["reference"]
 
 
 def test_extreme_rows(gpu, oracle):
