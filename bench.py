@@ -38,6 +38,7 @@ LAYER = [("qkv", 4096, 12288), ("gate", 4096, 11008), ("up", 4096, 11008), ("dow
 DOMINANT = ("gate", 4096, 11008)
 COPIES = 3
 ROTATE_BYTES = 640 * 1000 * 1000     # > 2x the 256 MB Infinity Cache
+SPREAD_LOOPS, SPREAD_LAUNCHES = 10, 30  # per-shape spread: loops of launches (median, min, max)
 
 
 def log(msg: str) -> None:
@@ -477,14 +478,25 @@ def main() -> int:
     step_bytes = sum(q4_bytes(k, n) for _, k, n in LAYER)
     value = step_bytes / (step_ms * 1e-3) / 1e9
 
+    # Spread: SPREAD_LOOPS more event-timed loops of SPREAD_LAUNCHES launches
+    # each (an event per launch would make the loop host-bound and time the
+    # submission instead); median, min and max of the loops' per-launch means.
+    def loop_means(fn) -> list:
+        return [timed(fn, SPREAD_LAUNCHES, 2) / SPREAD_LAUNCHES * 1e3 for _ in range(SPREAD_LOOPS)]
+
     per_shape = {}
     for name, k, n in LAYER:
         def one(i, name=name, k=k, n=n):
             kl.matmul(kernel, device, ys[name].data, weights(name, i), xs[name].data, k, n, 1, kl.WeightType.q4_0)
         ms = timed(one, args.kernel_reps, 5) / args.kernel_reps
         gbps = q4_bytes(k, n) / (ms * 1e-3) / 1e9
+        spread = loop_means(one)
         per_shape[f"{name}_k{k}_n{n}"] = {"us": round(ms * 1e3, 3), "gbps": round(gbps, 1),
-                                           "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "route": kernel.route}
+                                           "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "route": kernel.route,
+                                           "loop_mean_us": {"loops": SPREAD_LOOPS, "launches": SPREAD_LAUNCHES,
+                                                            "median": round(float(np.median(spread)), 3),
+                                                            "min": round(min(spread), 3),
+                                                            "max": round(max(spread), 3)}}
     dname, dk, dn = DOMINANT
     dom = per_shape[f"{dname}_k{dk}_n{dn}"]
     achieved = dom["gbps"]
