@@ -135,8 +135,9 @@ bool swiglu(Kernel &, int device, void * y, size_t y_bytes,
 // src/q4-pair.inc:9-80): Y[batch,n] = SiLU(X W_gate^T) * (X W_up^T), F32 Y.
 // w_gate and w_up are [n,k] weights of one type (f32, f16 or q4_0) and the
 // arguments follow matmul's rules. At batch >= 64 (Q4_0, F16) both products
-// run in one fp16-MFMA GEMM with the SiLU * up epilogue; smaller batches run
-// two GEMVs and the SwiGLU kernel. Submits; select + wait completes it.
+// run in one fp16-MFMA GEMM with the SiLU * up epilogue; Q4_0 at batch 1..2
+// runs both matrices in one GEMV pass with the same epilogue; other batches
+// run two GEMVs and the SwiGLU kernel. Submits; select + wait completes it.
 void matmul_swiglu(Kernel &, int device, void * y, const void * w_gate, const void * w_up, const void * x,
                    int k, int n, int batch, WeightType type);
 

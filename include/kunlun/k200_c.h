@@ -198,7 +198,8 @@ const char *kunlun_kernel_route(const kunlun_kernel *kernel);
 /* matmul_swiglu(): Y[batch,n] = SiLU(X W_gate^T) * (X W_up^T) for two [n,k]
  * weights of one type (KUNLUN_F32, KUNLUN_F16, KUNLUN_Q4_0), with matmul()'s
  * argument rules. The reference computes this with two matmul calls and
- * swiglu; here batch >= 64 fuses both products and the SwiGLU into one GEMM.
+ * swiglu; here batch >= 64 fuses both products and the SwiGLU into one GEMM,
+ * and Q4_0 at batch 1..2 into one GEMV pass.
  * Submits; kunlun_select(device) + kunlun_wait() completes it. */
 void kunlun_matmul_swiglu(kunlun_kernel *kernel, int device, void *y, const void *w_gate, const void *w_up,
                           const void *x, int k, int n, int batch, int type);

@@ -355,8 +355,12 @@ constexpr int kDot8MaxRowsPerWave = 64;
 // PASSES = activation staging passes: B * (K/32) * 4 <= PASSES * 64 * WAVES.
 // SLICES = ceil(K / 4096): 64-pair slices per row. Rows are split over the
 // grid's waves as base or base+1 contiguous rows (rem waves get one more).
-template <int B, int U, int WAVES, int SLICES, int DEPTH, int PASSES>
+// PAIR (U = 2): an item is output row r of both the gate matrix w and the up
+// matrix w2, and the row result is SiLU(gate) * up (the swiglu kernel's
+// element function), so the pair reads X once and needs no second pass.
+template <int B, int U, int WAVES, int SLICES, int DEPTH, int PASSES, bool PAIR = false>
 __global__ __launch_bounds__(64 * WAVES) void q4_gemv_dot8(const uint8_t *__restrict__ w,
+                                                          const uint8_t *__restrict__ w2,
                                                           const float *__restrict__ x,
                                                           float *__restrict__ y, int k, int n, int y_stride,
                                                           int rows_base, int rows_rem) {
@@ -377,7 +381,8 @@ __global__ __launch_bounds__(64 * WAVES) void q4_gemv_dot8(const uint8_t *__rest
     const int r_begin = wave * rows_base + min(wave, rows_rem);
     const int rows = rows_base + (wave < rows_rem ? 1 : 0);   // 0 <= rows <= kDot8MaxRowsPerWave
     const int r_end = r_begin + rows;
-    const int chunks = (rows + U - 1) / U;
+    static_assert(!PAIR || U == 2, "a pair item is one gate row and one up row");
+    const int chunks = PAIR ? rows : (rows + U - 1) / U;
     const int items = chunks * slices;
     float *my_results = results + wid * B * kDot8MaxRowsPerWave;
 
@@ -388,9 +393,10 @@ __global__ __launch_bounds__(64 * WAVES) void q4_gemv_dot8(const uint8_t *__rest
         const int p = min(lane + kWave * j, pairs - 1);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int r = max(0, min(min(r_begin + c * U + u, r_end - 1), n - 1));
+            const int r = max(0, min(min(r_begin + (PAIR ? c : c * U + u), r_end - 1), n - 1));
+            const uint8_t *base = PAIR && u == 1 ? w2 : w;
             const uint32_t *src = reinterpret_cast<const uint32_t *>(
-                w + static_cast<size_t>(r) * row_bytes + static_cast<size_t>(p) * 36);
+                base + static_cast<size_t>(r) * row_bytes + static_cast<size_t>(p) * 36);
             const kk::u32x4_a4 a = kk::load_u32x4(src);
             const kk::u32x4_a4 b = kk::load_u32x4(src + 4);
             buf[u][0] = a.x; buf[u][1] = a.y; buf[u][2] = a.z; buf[u][3] = a.w;
@@ -527,13 +533,22 @@ __global__ __launch_bounds__(64 * WAVES) void q4_gemv_dot8(const uint8_t *__rest
             }
         }
         if (j == slices - 1) {
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int rr = c * U + u;
+            if (PAIR) {
 #pragma unroll
                 for (int b = 0; b < B; ++b) {
-                    const float v = kk::wave_sum_uniform(acc[u][b]);
-                    if (lane == 0 && rr < rows) my_results[b * kDot8MaxRowsPerWave + rr] = v;
+                    const float gate = kk::wave_sum_uniform(acc[0][b]);
+                    const float up = kk::wave_sum_uniform(acc[PAIR ? 1 : 0][b]);
+                    if (lane == 0 && c < rows) my_results[b * kDot8MaxRowsPerWave + c] = kk::swiglu_value(gate, up);
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int rr = c * U + u;
+#pragma unroll
+                    for (int b = 0; b < B; ++b) {
+                        const float v = kk::wave_sum_uniform(acc[u][b]);
+                        if (lane == 0 && rr < rows) my_results[b * kDot8MaxRowsPerWave + rr] = v;
+                    }
                 }
             }
         }
@@ -767,10 +782,10 @@ hipError_t launch_q4_stream(const uint8_t *w, const float *x, float *y, int k, i
     return hipGetLastError();
 }
 
-template <int B, int SLICES, int DEPTH>
-hipError_t launch_q4_dot8_depth(const uint8_t *w, const float *x, float *y, int k, int n, int y_stride,
-                                hipStream_t stream, const DeviceInfo &info) {
-    constexpr int kWaves = 8, kU = 1;
+template <int B, int SLICES, int DEPTH, bool PAIR = false>
+hipError_t launch_q4_dot8_depth(const uint8_t *w, const uint8_t *w2, const float *x, float *y, int k, int n,
+                                int y_stride, hipStream_t stream, const DeviceInfo &info) {
+    constexpr int kWaves = 8, kU = PAIR ? 2 : 1;
     constexpr int kPasses = B * SLICES;   // B * K/8 staging groups <= B * SLICES * 512
     const size_t lds = static_cast<size_t>(B) * (k / 32) * 100 + static_cast<size_t>(kWaves) * B * kDot8MaxRowsPerWave * 4;
     const int per_cu = env_int("KUNLUN_GEMV_WAVES_PER_CU", 8);
@@ -779,40 +794,43 @@ hipError_t launch_q4_dot8_depth(const uint8_t *w, const float *x, float *y, int 
     const int groups = static_cast<int>(std::max<long long>(1, (want + kWaves - 1) / kWaves));
     const int waves = groups * kWaves;
     const int rows_base = n / waves, rows_rem = n % waves;
-    auto kernel = &q4_gemv_dot8<B, kU, kWaves, SLICES, DEPTH, kPasses>;
+    auto kernel = &q4_gemv_dot8<B, kU, kWaves, SLICES, DEPTH, kPasses, PAIR>;
     static bool attribute_set = false;    // per instantiation
     if (!attribute_set) {
         (void)hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                                   64 * 1024);
         attribute_set = true;
     }
-    hipLaunchKernelGGL(kernel, dim3(groups), dim3(64 * kWaves), lds, stream, w, x, y, k, n, y_stride, rows_base,
+    hipLaunchKernelGGL(kernel, dim3(groups), dim3(64 * kWaves), lds, stream, w, w2, x, y, k, n, y_stride, rows_base,
                        rows_rem);
     return hipGetLastError();
 }
 
-template <int B, int SLICES>
-hipError_t launch_q4_dot8_slices(const uint8_t *w, const float *x, float *y, int k, int n, int y_stride,
-                                 hipStream_t stream, const DeviceInfo &info) {
-    switch (env_int("KUNLUN_Q4_DEPTH", 3)) {
-    case 2: return launch_q4_dot8_depth<B, SLICES, 2>(w, x, y, k, n, y_stride, stream, info);
-    case 4: return launch_q4_dot8_depth<B, SLICES, 4>(w, x, y, k, n, y_stride, stream, info);
-    default: return launch_q4_dot8_depth<B, SLICES, 3>(w, x, y, k, n, y_stride, stream, info);
+template <int B, int SLICES, bool PAIR>
+hipError_t launch_q4_dot8_slices(const uint8_t *w, const uint8_t *w2, const float *x, float *y, int k, int n,
+                                 int y_stride, hipStream_t stream, const DeviceInfo &info) {
+    // items in flight per wave: 3 single rows at batch 1; 2 when an item is
+    // twice the work (two batch columns, or a gate/up row pair)
+    switch (env_int("KUNLUN_Q4_DEPTH", B == 2 || PAIR ? 2 : 3)) {
+    case 2: return launch_q4_dot8_depth<B, SLICES, 2, PAIR>(w, w2, x, y, k, n, y_stride, stream, info);
+    case 4: return launch_q4_dot8_depth<B, SLICES, 4, PAIR>(w, w2, x, y, k, n, y_stride, stream, info);
+    default: return launch_q4_dot8_depth<B, SLICES, 3, PAIR>(w, w2, x, y, k, n, y_stride, stream, info);
     }
 }
 
-// Q4_0 batch chunk of B (1 or 2) columns; B * K <= 16384.
-template <int B>
-hipError_t launch_q4_dot8(const uint8_t *w, const float *x, float *y, int k, int n, int y_stride,
+// Q4_0 batch chunk of B (1 or 2) columns; B * K <= 16384. PAIR: w is the gate
+// matrix, w2 the up matrix, y = SiLU(X w^T) * (X w2^T).
+template <int B, bool PAIR = false>
+hipError_t launch_q4_dot8(const uint8_t *w, const uint8_t *w2, const float *x, float *y, int k, int n, int y_stride,
                           hipStream_t stream, const DeviceInfo &info) {
     const int slices = (k + 4095) / 4096;
     if (B == 2 || slices <= 1) {
-        if (slices <= 1) return launch_q4_dot8_slices<B, 1>(w, x, y, k, n, y_stride, stream, info);
-        return launch_q4_dot8_slices<B, 2>(w, x, y, k, n, y_stride, stream, info);
+        if (slices <= 1) return launch_q4_dot8_slices<B, 1, PAIR>(w, w2, x, y, k, n, y_stride, stream, info);
+        return launch_q4_dot8_slices<B, 2, PAIR>(w, w2, x, y, k, n, y_stride, stream, info);
     }
-    if (slices == 2) return launch_q4_dot8_slices<1, 2>(w, x, y, k, n, y_stride, stream, info);
-    if (slices == 3) return launch_q4_dot8_slices<1, 3>(w, x, y, k, n, y_stride, stream, info);
-    return launch_q4_dot8_slices<1, 4>(w, x, y, k, n, y_stride, stream, info);
+    if (slices == 2) return launch_q4_dot8_slices<1, 2, PAIR>(w, w2, x, y, k, n, y_stride, stream, info);
+    if (slices == 3) return launch_q4_dot8_slices<1, 3, PAIR>(w, w2, x, y, k, n, y_stride, stream, info);
+    return launch_q4_dot8_slices<1, 4, PAIR>(w, w2, x, y, k, n, y_stride, stream, info);
 }
 
 template <int B, bool F16>
@@ -869,8 +887,8 @@ extern "C" int kk_dense_matmul(int type, const void *w, const float *x, float *y
             const int bc = std::min(pair_batch, batch - b0);
             const float *xc = x + static_cast<size_t>(b0) * k;
             float *yc = y + static_cast<size_t>(b0) * n;
-            const hipError_t rc = bc == 1 ? launch_q4_dot8<1>(wb, xc, yc, k, n, n, stream, info)
-                                          : launch_q4_dot8<2>(wb, xc, yc, k, n, n, stream, info);
+            const hipError_t rc = bc == 1 ? launch_q4_dot8<1>(wb, wb, xc, yc, k, n, n, stream, info)
+                                          : launch_q4_dot8<2>(wb, wb, xc, yc, k, n, n, stream, info);
             if (rc != hipSuccess) return rc;
         }
         return hipSuccess;
@@ -927,6 +945,32 @@ extern "C" int kk_dense_matmul(int type, const void *w, const float *x, float *y
             default: rc = launch_dense<4, false>(wb, xc, yc, k, n, n, stream, info); break;
             }
         }
+        if (rc != hipSuccess) return rc;
+    }
+    return hipSuccess;
+}
+
+extern "C" int kk_q4_gemv_pair_swiglu_supported(const void *w_gate, const void *w_up, const float *x, int k, int n,
+                                                int batch) {
+    return w_gate && w_up && x && k > 0 && n > 0 && (k % 64) == 0 && k <= 16384 && batch >= 1 && batch <= 2 &&
+           (reinterpret_cast<uintptr_t>(w_gate) & 3) == 0 && (reinterpret_cast<uintptr_t>(w_up) & 3) == 0 &&
+           (reinterpret_cast<uintptr_t>(x) & 15) == 0 && env_int("KUNLUN_GEMV_GENERAL", 0) == 0 &&
+           env_int("KUNLUN_Q4_KERNEL", 0) == 0;
+}
+
+extern "C" int kk_q4_gemv_pair_swiglu(const void *w_gate, const void *w_up, const float *x, float *y, int k, int n,
+                                     int batch, hipStream_t stream) {
+    if (!y || !kk_q4_gemv_pair_swiglu_supported(w_gate, w_up, x, k, n, batch)) return hipErrorInvalidValue;
+    const DeviceInfo info = device_info();
+    const uint8_t *wg = static_cast<const uint8_t *>(w_gate);
+    const uint8_t *wu = static_cast<const uint8_t *>(w_up);
+    const int pair_batch = k <= 8192 ? 2 : 1;   // staged digits: B * K <= 16384
+    for (int b0 = 0; b0 < batch; b0 += pair_batch) {
+        const int bc = std::min(pair_batch, batch - b0);
+        const float *xc = x + static_cast<size_t>(b0) * k;
+        float *yc = y + static_cast<size_t>(b0) * n;
+        const hipError_t rc = bc == 1 ? launch_q4_dot8<1, true>(wg, wu, xc, yc, k, n, n, stream, info)
+                                      : launch_q4_dot8<2, true>(wg, wu, xc, yc, k, n, n, stream, info);
         if (rc != hipSuccess) return rc;
     }
     return hipSuccess;

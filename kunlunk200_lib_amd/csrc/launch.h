@@ -27,6 +27,15 @@ int kk_gemm(int type, const void *w, const float *x, float *y, int k, int n, int
 int kk_gemm_swiglu(int type, const void *w_gate, const void *w_up, const float *x, float *y, int k, int n,
                    int batch, void *workspace, hipStream_t stream, const char **route);
 
+// Y[batch,n] = SiLU(X W_gate^T) * (X W_up^T) for Q4_0 weights at batch 1..2
+// in one pass (the q4_gemv_dot8 GEMV with both matrices per wave and the
+// swiglu element function as its epilogue). _supported tells whether these
+// arguments qualify: K % 64 == 0, K <= 16384, 4-byte aligned weights,
+// 16-byte aligned X, and the default GEMV kernel selection.
+int kk_q4_gemv_pair_swiglu_supported(const void *w_gate, const void *w_up, const float *x, int k, int n, int batch);
+int kk_q4_gemv_pair_swiglu(const void *w_gate, const void *w_up, const float *x, float *y, int k, int n, int batch,
+                           hipStream_t stream);
+
 // y = SiLU(gate) * up over `rows` rows of `width` contiguous values of
 // `bytes` (4: F32, 2: F16) each; strides in bytes. F32 intermediates.
 int kk_swiglu(void *y, const void *gate, const void *up, int width, int rows, int gate_stride, int up_stride,

@@ -169,6 +169,13 @@ void matmul_swiglu(Kernel & kernel, int id, void * y, const void * w_gate, const
                                                      static_cast<float *>(y), k, n, batch, impl.gemm_workspace,
                                                      ctx.stream, &impl.route),
                           "kk_gemm_swiglu");
+    } else if (type == WeightType::q4_0 &&
+               kk_q4_gemv_pair_swiglu_supported(w_gate, w_up, static_cast<const float *>(x), k, n, batch)) {
+        // decode: both matrices in one GEMV pass, SwiGLU in its epilogue
+        detail::check_hip((hipError_t)kk_q4_gemv_pair_swiglu(w_gate, w_up, static_cast<const float *>(x),
+                                                             static_cast<float *>(y), k, n, batch, ctx.stream),
+                          "kk_q4_gemv_pair_swiglu");
+        impl.route = "q4_gemv_fused_pair_swiglu";
     } else {
         // gate and up rows side by side in the workspace: [batch][2n] F32
         const size_t half = (size_t)batch * n * 4;

@@ -285,6 +285,73 @@ def test_matmul_swiglu_gemm_matches_two_matmuls(gpu, oracle):
     assert np.allclose(fused, expected, rtol=1e-5, atol=1e-6)
 
 
+def device_swiglu(g, u):
+    # the library's swiglu on device copies of g and u ([rows][width] F32)
+    rows, width = g.shape
+    bufs = [kl.Buffer(0, g.nbytes), kl.Buffer(0, u.nbytes), kl.Buffer(0, g.nbytes)]
+    try:
+        bufs[0].upload(np.ascontiguousarray(g, np.float32))
+        bufs[1].upload(np.ascontiguousarray(u, np.float32))
+        layout = kl.SwiGLULayout(width, rows, 4 * width, 4 * width, 4 * width, kl.InputType.f32)
+        kernel = kl.Kernel()
+        with kl.runtime_mutex():
+            assert kl.swiglu(kernel, 0, bufs[2].data, g.nbytes, bufs[0].data, g.nbytes, bufs[1].data, u.nbytes, layout)
+        return bufs[2].download(g.size, np.float32).reshape(rows, width)
+    finally:
+        for b in bufs:
+            b.close()
+
+
+# (k, n, batch, non-finite activation): K <= 4096 (one slice), K > 8192 with
+# batch 2 (two one-column passes), N tails, one infinite activation
+DECODE_PAIR_CASES = [(4096, 11008, 1, False), (4096, 300, 2, False), (12352, 70, 1, False), (12352, 70, 2, False),
+                     (256, 65, 1, False), (64, 1, 2, False), (1024, 129, 1, True)]
+
+
+@pytest.mark.parametrize("k,n,batch,inf", DECODE_PAIR_CASES)
+def test_matmul_swiglu_decode_pair_fused(gpu, oracle, k, n, batch, inf):
+    # batch 1..2 Q4_0: gate and up rows in one GEMV pass with SwiGLU as the
+    # epilogue. The gate and up sums are the standalone GEMV's own, so the
+    # result equals two matmul calls plus swiglu on the device bit for bit.
+    seed = 5 * k + n + batch
+    wg = gaussian((n, k), 0.02, seed)
+    wu = gaussian((n, k), 0.02, seed + 1)
+    x = gaussian((batch, k), 1.0, seed + 2)
+    if inf:
+        x[0, 5] = np.inf
+    pg, dg = weight_payload(kl.WeightType.q4_0, wg, oracle)
+    pu, du = weight_payload(kl.WeightType.q4_0, wu, oracle)
+    fused, route = run_pair(kl.WeightType.q4_0, pg, pu, x, k, n, batch)
+    assert route == "q4_gemv_fused_pair_swiglu"
+    from gpu_util import run_matmul
+    g, r1, _ = run_matmul(kl.WeightType.q4_0, pg, x, k, n, batch)
+    u, r2, _ = run_matmul(kl.WeightType.q4_0, pu, x, k, n, batch)
+    assert r1 == r2 == "q4_gemv_dot8"
+    expected = device_swiglu(g, u)
+    print(f"  decode pair k={k} n={n} b={batch} inf={inf}", flush=True)
+    assert np.array_equal(fused.view(np.uint32), expected.view(np.uint32))
+    if inf:
+        assert np.all(np.isnan(fused[0])) and (batch == 1 or np.all(np.isfinite(fused[1:])))
+    else:
+        finite, ok, worst = check_pair(fused, x, dg, du, oracle, 1e-4)
+        assert finite and ok, worst
+
+
+def test_matmul_swiglu_decode_pair_unfused_fallbacks(gpu, oracle):
+    # batch 1 fuses; batch 3 takes two single-pass GEMVs plus swiglu
+    k, n = 512, 96
+    wg = gaussian((n, k), 0.02, 71)
+    wu = gaussian((n, k), 0.02, 72)
+    pg, dg = weight_payload(kl.WeightType.q4_0, wg, oracle)
+    pu, du = weight_payload(kl.WeightType.q4_0, wu, oracle)
+    for batch in (1, 3):
+        x = gaussian((batch, k), 1.0, 73 + batch)
+        y, route = run_pair(kl.WeightType.q4_0, pg, pu, x, k, n, batch)
+        finite, ok, worst = check_pair(y, x, dg, du, oracle, 1e-4)
+        assert route == ("q4_gemv_fused_pair_swiglu" if batch == 1 else "q4_gemv_pair_swiglu")
+        assert finite and ok, worst
+
+
 @pytest.mark.parametrize("tile", ["128x32", "64x64", "64x32"])
 def test_matmul_swiglu_tile_variants(gpu, oracle, monkeypatch, tile):
     # the pair tiles of the LDS-copy Q4_0 kernel: gate and up column tiles per wave
