@@ -314,31 +314,40 @@ __global__ __launch_bounds__(kThreads) void q4_mfma_gemv(const uint8_t *__restri
 }
 
 // ---------------------------------------------------------------------------
-// q4_lds_gemv: the same products, streamed (K % 256 == 0, 16-byte aligned
-// weights). A workgroup owns 64 weight rows (four 16-row MFMA tiles); its 8
-// waves are 2 k-groups x 4 tiles: wave w computes tile w & 3 over blocks
-// 4 (w >> 2) .. +3 of every 8-block stage, and the k-groups' sums meet in LDS
-// at the end in a fixed order. Per stage the waves copy the stage's A
-// fragments (8 blocks x (hi, lo) = 16 KiB, from L2) and the 64 rows' raw
-// bytes (144 B = nine 16-byte chunks per row, from HBM; consecutive lanes
-// take consecutive chunks, so one copy touches about 7 rows) straight into
-// LDS (buffer_load_dwordx4 ... lds; per-lane offsets fixed over stages, the
-// stage offset in the SGPR soffset), five stages ahead into a ring of six.
-// Weight rows sit 144 bytes apart in LDS, so a tile's 16 rows read 16
-// distinct banks; A fragments are lane-contiguous.
+// q4_lds_gemv<SB>: the same products, streamed (K % (32 SB) == 0, 16-byte
+// aligned weights). A workgroup owns 64 weight rows (four 16-row MFMA tiles);
+// its 8 waves are 2 k-groups x 4 tiles: wave w computes tile w & 3 over
+// blocks SB/2 (w >> 2) .. +SB/2-1 of every SB-block stage, and the k-groups'
+// sums meet in LDS at the end in a fixed order. Per stage the waves copy the
+// stage's A fragments (SB blocks x (hi, lo) = 2 SB KiB, from L2) and the 64
+// rows' raw bytes (18 SB B per row as 16-byte chunks, from HBM; consecutive
+// lanes take consecutive chunks, so one copy touches a few rows) straight
+// into LDS (buffer_load_dwordx4 ... lds; per-lane offsets fixed over stages,
+// the stage offset in the SGPR soffset), into a ring of Slots stages, all but
+// one ahead. One barrier per stage: SB = 16 halves the barriers of SB = 8 for
+// the same LDS (3 x 50 KiB against 6 x 25 KiB). Weight rows sit 18 SB bytes
+// apart in LDS, so a tile's 16 rows read 16 distinct banks; A fragments are
+// lane-contiguous.
 constexpr int kLgThreads = 512;
 constexpr int kLgRows = 64;                                  // weight rows per workgroup
-constexpr int kLgStageBlocks = 8;                            // 256 K per stage
-constexpr int kLgRowStage = kLgStageBlocks * 18;             // 144 B of a row per stage
-constexpr int kLgStages = 6;                                 // ring of six stages
-constexpr int kLgAStageBytes = kLgStageBlocks * kFragBlockBytes;      // 16 KiB
-constexpr int kLgBStageBytes = kLgRows * kLgRowStage;                 // 9 KiB
-constexpr int kLgStageBytes = kLgAStageBytes + kLgBStageBytes;
-constexpr int kLgACopies = kLgAStageBytes / 1024;            // 16: two per wave
-constexpr int kLgBCopies = kLgBStageBytes / 1024;            // 9: wave 0 issues two
-constexpr int kLgLdsBytes = kLgStages * kLgStageBytes;       // 150 KiB
-static_assert(kLgBCopies * 1024 == kLgBStageBytes && kLgACopies % 8 == 0, "whole copies");
-static_assert(kLgLdsBytes <= 160 * 1024, "LDS");
+
+template <int SB>
+struct LgShape {
+    static_assert(SB == 8 || SB == 16, "stage of 8 or 16 blocks");
+    static constexpr int RowStage = SB * 18;                           // bytes of a row per stage
+    static constexpr int Slots = SB == 8 ? 6 : 3;                      // ring stages
+    static constexpr int AStageBytes = SB * kFragBlockBytes;           // 16 / 32 KiB
+    static constexpr int BStageBytes = kLgRows * RowStage;             // 9 / 18 KiB
+    static constexpr int StageBytes = AStageBytes + BStageBytes;
+    static constexpr int ACopies = AStageBytes / 1024, BCopies = BStageBytes / 1024;
+    static constexpr int ACopiesPerWave = ACopies / 8;                 // 2 / 4
+    static constexpr int BCopiesPerWave = (BCopies + 7) / 8;           // 2 / 3 (waves below
+    static constexpr int BCopiesRem = BCopies % 8;                     // BCopies % 8 issue them all)
+    static constexpr int WaveBlocks = SB / 2;                          // blocks per wave and stage
+    static constexpr int LdsBytes = Slots * StageBytes;                // 150 KiB
+    static_assert(BCopies * 1024 == BStageBytes && ACopies % 8 == 0 && BCopiesRem != 0, "whole copies");
+    static_assert(LdsBytes <= 160 * 1024, "LDS");
+};
 
 // s_waitcnt vmcnt(n), any n <= 63 (gfx9 keeps vmcnt[5:4] in bits 15:14)
 template <int N>
@@ -346,19 +355,14 @@ __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N <= 63, "vmcnt");
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
-// vmcnt(per_stage * stages_after) for stages_after = 0 .. 4 and 3 or 4
-// copies per stage (wave-uniform)
-__device__ __forceinline__ void wait_lg_copies(int per_stage, int stages_after) {
-    if (per_stage == 3) {
-        switch (stages_after) {
-        case 0: wait_vmcnt<0>(); break;  case 1: wait_vmcnt<3>(); break; case 2: wait_vmcnt<6>(); break;
-        case 3: wait_vmcnt<9>(); break;  default: wait_vmcnt<12>(); break;
-        }
-    } else {
-        switch (stages_after) {
-        case 0: wait_vmcnt<0>(); break;  case 1: wait_vmcnt<4>(); break; case 2: wait_vmcnt<8>(); break;
-        case 3: wait_vmcnt<12>(); break; default: wait_vmcnt<16>(); break;
-        }
+__device__ __forceinline__ void wait_vmcnt_dyn(int n) {     // n wave-uniform, 0 .. 16
+    switch (n) {
+    case 0: wait_vmcnt<0>(); break;   case 1: wait_vmcnt<1>(); break;   case 2: wait_vmcnt<2>(); break;
+    case 3: wait_vmcnt<3>(); break;   case 4: wait_vmcnt<4>(); break;   case 5: wait_vmcnt<5>(); break;
+    case 6: wait_vmcnt<6>(); break;   case 7: wait_vmcnt<7>(); break;   case 8: wait_vmcnt<8>(); break;
+    case 9: wait_vmcnt<9>(); break;   case 10: wait_vmcnt<10>(); break; case 11: wait_vmcnt<11>(); break;
+    case 12: wait_vmcnt<12>(); break; case 13: wait_vmcnt<13>(); break; case 14: wait_vmcnt<14>(); break;
+    case 15: wait_vmcnt<15>(); break; default: wait_vmcnt<16>(); break;
     }
 }
 
@@ -369,34 +373,39 @@ __device__ __forceinline__ uint32_t lg_and_or(uint32_t a, uint32_t mask, uint32_
     return r;
 }
 
-// One stage's copies of wave `wid`: A copies wid and wid + 8, weight copies
-// wid (and 8 for wave 0). (A separate function: the host pass rejects a
+// One stage's copies of wave `wid`: A copies wid + 8t, weight copies wid + 8t
+// (those below BCopies). (A separate function: the host pass rejects a
 // kernel-local lambda that hands captured values to these builtins, and then
 // drops the launch stub.)
+template <int SB>
 __device__ __forceinline__ void lg_copy_stage(const uint8_t *frag, int frag_bytes, uint8_t *w_tile, int w_extent,
-                                              uint32_t b_off0, uint32_t b_off1, int wid, int lane, int s) {
+                                              const uint32_t (&b_off)[LgShape<SB>::BCopiesPerWave], int wid,
+                                              int lane, int s) {
+    using L = LgShape<SB>;
     extern __shared__ __align__(16) uint8_t lg_lds[];
     const __amdgpu_buffer_rsrc_t a_rsrc =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(frag), 0, frag_bytes, 0x00020000);
     const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(w_tile, 0, w_extent, 0x00020000);
     __attribute__((address_space(3))) uint8_t *buf =
-        (__attribute__((address_space(3))) uint8_t *)lg_lds + (s % kLgStages) * kLgStageBytes;
+        (__attribute__((address_space(3))) uint8_t *)lg_lds + (s % L::Slots) * L::StageBytes;
 #pragma unroll
-    for (int t = 0; t < kLgACopies / 8; ++t)
+    for (int t = 0; t < L::ACopiesPerWave; ++t)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, buf + (wid + 8 * t) * 1024, 16,
-                                                 (wid + 8 * t) * 1024 + lane * 16, s * kLgAStageBytes, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, buf + kLgAStageBytes + wid * 1024, 16, b_off0,
-                                             s * kLgRowStage, 0, 0);
-    if (wid == 0)                                               // wave-uniform
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, buf + kLgAStageBytes + 8 * 1024, 16, b_off1,
-                                                 s * kLgRowStage, 0, 0);
+                                                 (wid + 8 * t) * 1024 + lane * 16, s * L::AStageBytes, 0, 0);
+#pragma unroll
+    for (int t = 0; t < L::BCopiesPerWave; ++t)
+        if (wid + 8 * t < L::BCopies)                           // wave-uniform
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, buf + L::AStageBytes + (wid + 8 * t) * 1024, 16,
+                                                     b_off[t], s * L::RowStage, 0, 0);
 }
 
+template <int SB>
 __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restrict__ w,
                                                          const _Float16 *__restrict__ frag,
                                                          const float *__restrict__ row_inv, float *__restrict__ y,
                                                          int n, int batch, int stages, uint32_t row_bytes,
                                                          int tiles, int tiles_per_xcd) {
+    using L = LgShape<SB>;
     extern __shared__ __align__(16) uint8_t lg_lds[];
     const int bid = blockIdx.x;
     const int tile = (bid % 8) * tiles_per_xcd + bid / 8;       // contiguous row ranges per XCD
@@ -407,19 +416,21 @@ __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restr
     const int g = lane >> 4, c16 = lane & 15;
     const int n0 = tile * kLgRows;
 
-    // weight copy i: 16-byte chunks 64i .. 64i+63 of the stage's [row][144 B]
-    // bytes (9 per row); rows past n repeat row n - 1 and are never stored
+    // weight copy i: 16-byte chunks 64i .. 64i+63 of the stage's [row][RowStage]
+    // bytes; rows past n repeat row n - 1 and are never stored
+    constexpr int kChunks = L::RowStage / 16;                   // per row: 9 / 18
     const int w_extent = min(kLgRows, n - n0) * static_cast<int>(row_bytes);
     uint8_t *const w_tile = const_cast<uint8_t *>(w + static_cast<size_t>(n0) * row_bytes);
-    auto b_off = [&](int i) {
-        const int q = i * 64 + lane;
-        const int row = q / 9, chunk = q - (q / 9) * 9;
-        return static_cast<uint32_t>(min(n0 + row, n - 1) - n0) * row_bytes + 16 * chunk;
-    };
-    const uint32_t b_off0 = b_off(wid), b_off1 = b_off(8);
-    const int frag_bytes = stages * kLgAStageBytes;
+    uint32_t b_off[L::BCopiesPerWave];
+#pragma unroll
+    for (int t = 0; t < L::BCopiesPerWave; ++t) {
+        const int q = min(wid + 8 * t, L::BCopies - 1) * 64 + lane;
+        const int row = q / kChunks, chunk = q - (q / kChunks) * kChunks;
+        b_off[t] = static_cast<uint32_t>(min(n0 + row, n - 1) - n0) * row_bytes + 16 * chunk;
+    }
+    const int frag_bytes = stages * L::AStageBytes;
     const uint8_t *fbytes = reinterpret_cast<const uint8_t *>(frag);
-    const int my_copies = kLgACopies / 8 + (wid == 0 ? 2 : 1);   // per stage: 4 or 3
+    const int my_copies = L::ACopiesPerWave + (wid < L::BCopiesRem ? L::BCopiesPerWave : L::BCopiesPerWave - 1);
 
     float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
     uint32_t mask_lo = 0x000f000fu, mask_hi = 0x00f000f0u, magic = 0x64006400u;
@@ -428,37 +439,38 @@ __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restr
     const half2v off72 = {static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
     const half2v sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
 
-    // Stage t's copies are issued at stage t - 5 (the prologue issues 0..4),
-    // after that stage's barrier, into buffer t % 6 (stage t - 6's, which
-    // every wave finished before the barrier). At the top of stage s this
-    // wave's copies of stages s+1 .. min(s+4, stages-1) may still be in flight.
-    const int ahead0 = min(kLgStages - 1, stages);
-    for (int s = 0; s < ahead0; ++s) lg_copy_stage(fbytes, frag_bytes, w_tile, w_extent, b_off0, b_off1, wid, lane, s);
+    // Stage t's copies are issued at stage t - (Slots - 1) (the prologue
+    // issues the first Slots - 1), after that stage's barrier, into buffer
+    // t % Slots (stage t - Slots's, which every wave finished before the
+    // barrier). At the top of stage s this wave's copies of stages
+    // s+1 .. min(s+Slots-2, stages-1) may still be in flight.
+    const int ahead0 = min(L::Slots - 1, stages);
+    for (int s = 0; s < ahead0; ++s) lg_copy_stage<SB>(fbytes, frag_bytes, w_tile, w_extent, b_off, wid, lane, s);
     for (int s = 0; s < stages; ++s) {
-        wait_lg_copies(my_copies, min(kLgStages - 2, stages - 1 - s));
+        wait_vmcnt_dyn(my_copies * min(L::Slots - 2, stages - 1 - s));
         lds_barrier();
-        if (s + kLgStages - 1 < stages)
-            lg_copy_stage(fbytes, frag_bytes, w_tile, w_extent, b_off0, b_off1, wid, lane, s + kLgStages - 1);
-        const uint8_t *abuf = lg_lds + (s % kLgStages) * kLgStageBytes;
-        const uint8_t *brow = abuf + kLgAStageBytes + (wt * 16 + c16) * kLgRowStage;
-        uint32_t qs[4], d16[4];
-        half8 ahi[4], alo[4];
+        if (s + L::Slots - 1 < stages)
+            lg_copy_stage<SB>(fbytes, frag_bytes, w_tile, w_extent, b_off, wid, lane, s + L::Slots - 1);
+        const uint8_t *abuf = lg_lds + (s % L::Slots) * L::StageBytes;
+        const uint8_t *brow = abuf + L::AStageBytes + (wt * 16 + c16) * L::RowStage;
+        uint32_t qs[L::WaveBlocks], d16[L::WaveBlocks];
+        half8 ahi[L::WaveBlocks], alo[L::WaveBlocks];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int j = 4 * kh + i;                               // block of the stage (parity of i)
+        for (int i = 0; i < L::WaveBlocks; ++i) {
+            const int j = L::WaveBlocks * kh + i;               // block of the stage (parity of i)
             d16[i] = *reinterpret_cast<const uint16_t *>(brow + 18 * j);
-            if ((i & 1) == 0) {                                     // even block: nibble dword g at +2 + 4g
+            if ((i & 1) == 0) {                                 // even block: nibble dword g at +2 + 4g
                 const uint32_t *p = reinterpret_cast<const uint32_t *>(brow + 18 * j + 4 * g);
                 qs[i] = __builtin_amdgcn_alignbyte(p[1], p[0], 2);
-            } else {                                                // odd block: on a dword
+            } else {                                            // odd block: on a dword
                 qs[i] = *reinterpret_cast<const uint32_t *>(brow + 18 * j + 2 + 4 * g);
             }
             ahi[i] = *reinterpret_cast<const half8 *>(abuf + j * kFragBlockBytes + lane * 16);
             alo[i] = *reinterpret_cast<const half8 *>(abuf + j * kFragBlockBytes + kWave * 16 + lane * 16);
         }
-        float4v t[4];
+        float4v t[L::WaveBlocks];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < L::WaveBlocks; ++i) {
             // exact fp16 q - 8 of positions (4g, 4g+2, 4g+1, 4g+3, 16+4g, ...):
             // 1024 + q less 1032, and (1024 + 16 q) / 16 less 72
             union { uint32_t u; half2v h; } p0, p1, p2, p3;
@@ -477,7 +489,7 @@ __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restr
             t[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[i], bf, t[i], 0, 0, 0);
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < L::WaveBlocks; ++i) {
             const float d = kk::half_bits_to_float(d16[i]);
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[r] = fmaf(d, t[i][r], acc[r]);
@@ -501,6 +513,29 @@ __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restr
             if (m < batch) y[static_cast<size_t>(m) * n + rr] = acc[r] * row_inv[m];
         }
     }
+}
+
+// Launch q4_lds_gemv<SB> (dynamic LDS above 64 KiB opted into once per
+// device; callers hold the runtime lock).
+template <int SB>
+hipError_t launch_lds_gemv(const uint8_t *w, const _Float16 *frag, const float *row_inv, float *y, int k, int n,
+                           int batch, int device, hipStream_t stream) {
+    using L = LgShape<SB>;
+    constexpr int kMaxDevices = 64;
+    static bool configured[kMaxDevices] = {};
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    if (!configured[device]) {
+        const hipError_t rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&q4_lds_gemv<SB>),
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize, L::LdsBytes);
+        if (rc != hipSuccess) return rc;
+        configured[device] = true;
+    }
+    const int tiles = (n + kLgRows - 1) / kLgRows;
+    const int tiles_per_xcd = (tiles + 7) / 8;
+    hipLaunchKernelGGL(q4_lds_gemv<SB>, dim3(tiles_per_xcd * 8), dim3(kLgThreads), L::LdsBytes, stream, w, frag,
+                       row_inv, y, n, batch, k / (SB * 32), static_cast<uint32_t>(k / 32 * 18), tiles,
+                       tiles_per_xcd);
+    return hipGetLastError();
 }
 
 } // namespace
@@ -536,20 +571,10 @@ extern "C" int kk_q4_mfma_gemv(const void *w, const float *x, float *y, int k, i
         if (rc != hipSuccess) return rc;
         configured[device] = true;
     }
-    if (k % (kLgStageBlocks * 32) == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0) {
-        static bool lg_configured[kMaxDevices] = {};
-        if (!lg_configured[device]) {
-            rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&q4_lds_gemv),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, kLgLdsBytes);
-            if (rc != hipSuccess) return rc;
-            lg_configured[device] = true;
-        }
-        const int tiles = (n + kLgRows - 1) / kLgRows;
-        const int tiles_per_xcd = (tiles + 7) / 8;
-        hipLaunchKernelGGL(q4_lds_gemv, dim3(tiles_per_xcd * 8), dim3(kLgThreads), kLgLdsBytes, stream,
-                           static_cast<const uint8_t *>(w), frag, row_inv, y, n, batch, k / (kLgStageBlocks * 32),
-                           static_cast<uint32_t>(k / 32 * 18), tiles, tiles_per_xcd);
-        return hipGetLastError();
+    if ((reinterpret_cast<uintptr_t>(w) & 15) == 0) {
+        const uint8_t *wb = static_cast<const uint8_t *>(w);
+        if (k % 512 == 0) return launch_lds_gemv<16>(wb, frag, row_inv, y, k, n, batch, device, stream);
+        if (k % 256 == 0) return launch_lds_gemv<8>(wb, frag, row_inv, y, k, n, batch, device, stream);
     }
     const int tiles = (n + kTileRows - 1) / kTileRows;
     const int groups = std::max(1, std::min((tiles + kWaves - 1) / kWaves, cus));

@@ -45,6 +45,8 @@ def test_config2_shapes(gpu, oracle, batch):
     assert guard_ok and res["finite"] and res["north_star"] and res["reference"]
 
 
+# streamed kernel with 16-block stages: K % 512 == 0 (1024, 2048, 4096, 16384);
+# 8-block stages: K % 256 == 0 only (11008); register-staged: the rest
 @pytest.mark.parametrize("k,n,batch", [(64, 1, 2), (64, 17, 16), (4160, 33, 3), (11008, 4096, 4), (16384, 70, 16),
                                        (1024, 16, 5), (2048, 1000, 9), (4096, 4096, 15)])
 def test_tails(gpu, oracle, k, n, batch):
