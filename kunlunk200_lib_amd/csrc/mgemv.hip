@@ -66,6 +66,10 @@ static_assert(kStageStride % 16 == 0 && kChunkRowBytes % 16 == 0, "16-byte copie
 // between the max reduction and the stores (one pass over X). Row scale
 // s_m = 2^(14 - e), 2^(e-1) <= max|x_m| < 2^e (non-finite or zero rows keep
 // s = 1); frag holds blocks_pad blocks (zero beyond k and for rows >= batch).
+// PACKED (batch <= 8, 8 workgroups): one fragment per block, A row m holding
+// the hi part of batch row m and A row m + 8 its lo part, so one MFMA per
+// block computes both and the two halves of D are added at the end.
+template <bool PACKED>
 __global__ __launch_bounds__(kPrepassThreads) void x_to_frag(const float *__restrict__ x, int batch, int k,
                                                              int blocks_pad, _Float16 *__restrict__ frag,
                                                              float *__restrict__ row_inv) {
@@ -118,8 +122,13 @@ __global__ __launch_bounds__(kPrepassThreads) void x_to_frag(const float *__rest
             lo[t] = static_cast<_Float16>(a - static_cast<float>(h));
         }
         const int lane = g * kBatchRows + m;
-        *reinterpret_cast<half8 *>(frag + (static_cast<size_t>(j * 2 + 0) * kWave + lane) * 8) = hi;
-        *reinterpret_cast<half8 *>(frag + (static_cast<size_t>(j * 2 + 1) * kWave + lane) * 8) = lo;
+        if constexpr (PACKED) {
+            *reinterpret_cast<half8 *>(frag + (static_cast<size_t>(j) * kWave + lane) * 8) = hi;
+            *reinterpret_cast<half8 *>(frag + (static_cast<size_t>(j) * kWave + lane + 8) * 8) = lo;
+        } else {
+            *reinterpret_cast<half8 *>(frag + (static_cast<size_t>(j * 2 + 0) * kWave + lane) * 8) = hi;
+            *reinterpret_cast<half8 *>(frag + (static_cast<size_t>(j * 2 + 1) * kWave + lane) * 8) = lo;
+        }
     }
 }
 
@@ -331,20 +340,21 @@ __global__ __launch_bounds__(kThreads) void q4_mfma_gemv(const uint8_t *__restri
 constexpr int kLgThreads = 512;
 constexpr int kLgRows = 64;                                  // weight rows per workgroup
 
-template <int SB>
+template <int SB, bool PACKED>
 struct LgShape {
     static_assert(SB == 8 || SB == 16, "stage of 8 or 16 blocks");
     static constexpr int RowStage = SB * 18;                           // bytes of a row per stage
-    static constexpr int Slots = SB == 8 ? 6 : 3;                      // ring stages
-    static constexpr int AStageBytes = SB * kFragBlockBytes;           // 16 / 32 KiB
+    static constexpr int Slots = SB == 8 ? 6 : PACKED ? 4 : 3;         // ring stages
+    static constexpr int ABlockBytes = PACKED ? kFragBlockBytes / 2 : kFragBlockBytes;
+    static constexpr int AStageBytes = SB * ABlockBytes;               // 8 / 16 / 32 KiB
     static constexpr int BStageBytes = kLgRows * RowStage;             // 9 / 18 KiB
     static constexpr int StageBytes = AStageBytes + BStageBytes;
     static constexpr int ACopies = AStageBytes / 1024, BCopies = BStageBytes / 1024;
-    static constexpr int ACopiesPerWave = ACopies / 8;                 // 2 / 4
+    static constexpr int ACopiesPerWave = ACopies / 8;                 // 1 / 2 / 4
     static constexpr int BCopiesPerWave = (BCopies + 7) / 8;           // 2 / 3 (waves below
     static constexpr int BCopiesRem = BCopies % 8;                     // BCopies % 8 issue them all)
     static constexpr int WaveBlocks = SB / 2;                          // blocks per wave and stage
-    static constexpr int LdsBytes = Slots * StageBytes;                // 150 KiB
+    static constexpr int LdsBytes = Slots * StageBytes;                // 102 .. 150 KiB
     static_assert(BCopies * 1024 == BStageBytes && ACopies % 8 == 0 && BCopiesRem != 0, "whole copies");
     static_assert(LdsBytes <= 160 * 1024, "LDS");
 };
@@ -377,11 +387,11 @@ __device__ __forceinline__ uint32_t lg_and_or(uint32_t a, uint32_t mask, uint32_
 // (those below BCopies). (A separate function: the host pass rejects a
 // kernel-local lambda that hands captured values to these builtins, and then
 // drops the launch stub.)
-template <int SB>
+template <int SB, bool PACKED>
 __device__ __forceinline__ void lg_copy_stage(const uint8_t *frag, int frag_bytes, uint8_t *w_tile, int w_extent,
-                                              const uint32_t (&b_off)[LgShape<SB>::BCopiesPerWave], int wid,
+                                              const uint32_t (&b_off)[LgShape<SB, PACKED>::BCopiesPerWave], int wid,
                                               int lane, int s) {
-    using L = LgShape<SB>;
+    using L = LgShape<SB, PACKED>;
     extern __shared__ __align__(16) uint8_t lg_lds[];
     const __amdgpu_buffer_rsrc_t a_rsrc =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(frag), 0, frag_bytes, 0x00020000);
@@ -399,13 +409,13 @@ __device__ __forceinline__ void lg_copy_stage(const uint8_t *frag, int frag_byte
                                                      b_off[t], s * L::RowStage, 0, 0);
 }
 
-template <int SB>
+template <int SB, bool PACKED>
 __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restrict__ w,
                                                          const _Float16 *__restrict__ frag,
                                                          const float *__restrict__ row_inv, float *__restrict__ y,
                                                          int n, int batch, int stages, uint32_t row_bytes,
                                                          int tiles, int tiles_per_xcd) {
-    using L = LgShape<SB>;
+    using L = LgShape<SB, PACKED>;
     extern __shared__ __align__(16) uint8_t lg_lds[];
     const int bid = blockIdx.x;
     const int tile = (bid % 8) * tiles_per_xcd + bid / 8;       // contiguous row ranges per XCD
@@ -445,12 +455,13 @@ __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restr
     // barrier). At the top of stage s this wave's copies of stages
     // s+1 .. min(s+Slots-2, stages-1) may still be in flight.
     const int ahead0 = min(L::Slots - 1, stages);
-    for (int s = 0; s < ahead0; ++s) lg_copy_stage<SB>(fbytes, frag_bytes, w_tile, w_extent, b_off, wid, lane, s);
+    for (int s = 0; s < ahead0; ++s)
+        lg_copy_stage<SB, PACKED>(fbytes, frag_bytes, w_tile, w_extent, b_off, wid, lane, s);
     for (int s = 0; s < stages; ++s) {
         wait_vmcnt_dyn(my_copies * min(L::Slots - 2, stages - 1 - s));
         lds_barrier();
         if (s + L::Slots - 1 < stages)
-            lg_copy_stage<SB>(fbytes, frag_bytes, w_tile, w_extent, b_off, wid, lane, s + L::Slots - 1);
+            lg_copy_stage<SB, PACKED>(fbytes, frag_bytes, w_tile, w_extent, b_off, wid, lane, s + L::Slots - 1);
         const uint8_t *abuf = lg_lds + (s % L::Slots) * L::StageBytes;
         const uint8_t *brow = abuf + L::AStageBytes + (wt * 16 + c16) * L::RowStage;
         uint32_t qs[L::WaveBlocks], d16[L::WaveBlocks];
@@ -465,8 +476,8 @@ __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restr
             } else {                                            // odd block: on a dword
                 qs[i] = *reinterpret_cast<const uint32_t *>(brow + 18 * j + 2 + 4 * g);
             }
-            ahi[i] = *reinterpret_cast<const half8 *>(abuf + j * kFragBlockBytes + lane * 16);
-            alo[i] = *reinterpret_cast<const half8 *>(abuf + j * kFragBlockBytes + kWave * 16 + lane * 16);
+            ahi[i] = *reinterpret_cast<const half8 *>(abuf + j * L::ABlockBytes + lane * 16);
+            if (!PACKED) alo[i] = *reinterpret_cast<const half8 *>(abuf + j * L::ABlockBytes + kWave * 16 + lane * 16);
         }
         float4v t[L::WaveBlocks];
 #pragma unroll
@@ -486,7 +497,7 @@ __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restr
             bf[4] = e2[0]; bf[5] = e2[1]; bf[6] = e3[0]; bf[7] = e3[1];
             t[i] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
             t[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[i], bf, t[i], 0, 0, 0);
-            t[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[i], bf, t[i], 0, 0, 0);
+            if (!PACKED) t[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[i], bf, t[i], 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < L::WaveBlocks; ++i) {
@@ -504,6 +515,12 @@ __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restr
     __syncthreads();
     if (kh == 1) return;
     acc += xfer[wt * kWave + lane];
+    if constexpr (PACKED) {
+        // D rows 8..15 (lanes 32..63) are the lo parts of batch rows 0..7
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] += __shfl_down(acc[r], 32);
+        if (g >= 2) return;
+    }
     // D reg r of lane (c16, g): batch row 4g + r, weight row n0 + 16 wt + c16
     const int rr = n0 + wt * 16 + c16;
     if (rr < n) {
@@ -517,22 +534,22 @@ __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restr
 
 // Launch q4_lds_gemv<SB> (dynamic LDS above 64 KiB opted into once per
 // device; callers hold the runtime lock).
-template <int SB>
+template <int SB, bool PACKED>
 hipError_t launch_lds_gemv(const uint8_t *w, const _Float16 *frag, const float *row_inv, float *y, int k, int n,
                            int batch, int device, hipStream_t stream) {
-    using L = LgShape<SB>;
+    using L = LgShape<SB, PACKED>;
     constexpr int kMaxDevices = 64;
     static bool configured[kMaxDevices] = {};
     if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
     if (!configured[device]) {
-        const hipError_t rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&q4_lds_gemv<SB>),
+        const hipError_t rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&q4_lds_gemv<SB, PACKED>),
                                                   hipFuncAttributeMaxDynamicSharedMemorySize, L::LdsBytes);
         if (rc != hipSuccess) return rc;
         configured[device] = true;
     }
     const int tiles = (n + kLgRows - 1) / kLgRows;
     const int tiles_per_xcd = (tiles + 7) / 8;
-    hipLaunchKernelGGL(q4_lds_gemv<SB>, dim3(tiles_per_xcd * 8), dim3(kLgThreads), L::LdsBytes, stream, w, frag,
+    hipLaunchKernelGGL((q4_lds_gemv<SB, PACKED>), dim3(tiles_per_xcd * 8), dim3(kLgThreads), L::LdsBytes, stream, w, frag,
                        row_inv, y, n, batch, k / (SB * 32), static_cast<uint32_t>(k / 32 * 18), tiles,
                        tiles_per_xcd);
     return hipGetLastError();
@@ -554,8 +571,16 @@ extern "C" int kk_q4_mfma_gemv(const void *w, const float *x, float *y, int k, i
     _Float16 *frag = static_cast<_Float16 *>(workspace);
     float *row_inv = reinterpret_cast<float *>(static_cast<char *>(workspace) +
                                                static_cast<size_t>(blocks_pad) * kFragBlockBytes);
-    hipLaunchKernelGGL(x_to_frag, dim3(kBatchRows), dim3(kPrepassThreads), 0, stream, x, batch, k, blocks_pad, frag,
-                       row_inv);
+    // streamed kernels: K % 256 == 0 and 16-byte aligned weights; batch <= 8
+    // packs hi and lo into one fragment (one MFMA per block)
+    const bool streamed = k % 256 == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0;
+    const bool packed = streamed && batch <= kBatchRows / 2;
+    if (packed)
+        hipLaunchKernelGGL(x_to_frag<true>, dim3(kBatchRows / 2), dim3(kPrepassThreads), 0, stream, x, batch, k,
+                           blocks_pad, frag, row_inv);
+    else
+        hipLaunchKernelGGL(x_to_frag<false>, dim3(kBatchRows), dim3(kPrepassThreads), 0, stream, x, batch, k,
+                           blocks_pad, frag, row_inv);
     hipError_t rc = hipGetLastError();
     if (rc != hipSuccess) return rc;
     // dynamic LDS above 64 KiB is opted into once per device (callers hold the runtime lock)
@@ -571,10 +596,13 @@ extern "C" int kk_q4_mfma_gemv(const void *w, const float *x, float *y, int k, i
         if (rc != hipSuccess) return rc;
         configured[device] = true;
     }
-    if ((reinterpret_cast<uintptr_t>(w) & 15) == 0) {
+    if (streamed) {
         const uint8_t *wb = static_cast<const uint8_t *>(w);
-        if (k % 512 == 0) return launch_lds_gemv<16>(wb, frag, row_inv, y, k, n, batch, device, stream);
-        if (k % 256 == 0) return launch_lds_gemv<8>(wb, frag, row_inv, y, k, n, batch, device, stream);
+        if (k % 512 == 0)
+            return packed ? launch_lds_gemv<16, true>(wb, frag, row_inv, y, k, n, batch, device, stream)
+                          : launch_lds_gemv<16, false>(wb, frag, row_inv, y, k, n, batch, device, stream);
+        return packed ? launch_lds_gemv<8, true>(wb, frag, row_inv, y, k, n, batch, device, stream)
+                      : launch_lds_gemv<8, false>(wb, frag, row_inv, y, k, n, batch, device, stream);
     }
     const int tiles = (n + kTileRows - 1) / kTileRows;
     const int groups = std::max(1, std::min((tiles + kWaves - 1) / kWaves, cus));
