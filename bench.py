@@ -307,6 +307,60 @@ def small_batch_leg(kernel, events, stream, device: int, reps: int) -> dict:
     return out
 
 
+I8_CASES = ((1024, 512, 4), (4096, 4096, 1), (4096, 4096, 32), (4096, 4096, 512))
+INT8_PEAK_TOPS = 5000.0
+
+
+def i8_leg(kernel, events, stream, device: int, reps: int) -> dict:
+    """rowwise_i8 weights (upload_i8_rows packing) at K1024 x N512
+    batch 4 and K4096 x N4096 batch 1, 32, 512, over rotating copies of the packed
+    weights. A call includes the on-GPU two-pass activation quantization. GB/s =
+    (nk + 4n + 4bk + 4bn) / time; TOPS = 2bkn / time (int8 MFMA)."""
+    out = {}
+    rng = np.random.Generator(np.random.PCG64(31))
+    for k, n, batch in I8_CASES:
+        w = rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)
+        size = kl.packed_i8_size(k, n)
+        first = kl.Buffer(device, size)
+        kl.upload_i8_rows(device, first.data, k, n, 0, n, w)
+        bufs = [first]
+        for _ in range(max(2, -(-ROTATE_BYTES // size)) - 1):
+            b = kl.Buffer(device, size)
+            with kl.runtime_mutex():
+                kl.select(device)
+                kl.check(kl.copy(b.data, first.data, size, kl.CopyKind.device_to_device))
+                kl.check(kl.wait())
+            bufs.append(b)
+        xb = kl.Buffer(device, 4 * batch * k)
+        xb.upload(rng.standard_normal((batch, k), dtype=np.float32))
+        yb = kl.Buffer(device, 4 * batch * n)
+
+        def call(i):
+            b = bufs[i % len(bufs)]
+            kl.matmul(kernel, device, yb.data, b.data, xb.data, k, n, batch, kl.WeightType.rowwise_i8,
+                      kl.packed_i8_scales(b.data, k, n), kl.packed_i8_maxima(b.data, k, n))
+        with kl.runtime_mutex():
+            for i in range(5):
+                call(i)
+            kl.select(device)
+            kl.check(kl.wait())
+            start, stop = events.create(), events.create()
+            events.record(start, stream)
+            for i in range(reps):
+                call(i)
+            events.record(stop, stream)
+            ms = events.elapsed_ms(start, stop) / reps
+            kl.check(kl.wait())
+        nbytes = n * k + 4 * n + 4 * batch * k + 4 * batch * n
+        tops = 2.0 * batch * k * n / (ms * 1e-3) / 1e12
+        out[f"i8_k{k}_n{n}_b{batch}"] = {"us": round(ms * 1e3, 3), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                         "tops": round(tops, 2), "int8_frac": round(tops / INT8_PEAK_TOPS, 4),
+                                         "route": kernel.route}
+        for b in bufs + [xb, yb]:
+            b.close()
+    return out
+
+
 NATIVE_SHAPES = ((4096, 4096), (4096, 11008), (11008, 4096))   # reference docs/native-q4.md:62-71
 NATIVE_REFERENCE_MS = {(4096, 4096): 0.338455, (4096, 11008): 0.712449, (11008, 4096): 0.843438}
 
@@ -418,7 +472,8 @@ def main() -> int:
     ap.add_argument("--small-reps", type=int, default=100, help="timed calls per small-batch config (0: skip)")
     ap.add_argument("--native-reps", type=int, default=100, help="timed native_q4_matmul calls per shape (0: skip)")
     ap.add_argument("--common-reps", type=int, default=50, help="timed common_q4_matmul calls per shape (0: skip)")
-    ap.add_argument("--only", choices=[name for name, _, _ in LAYER] + ["gemm", "copy", "small", "native", "common"],
+    ap.add_argument("--i8-reps", type=int, default=50, help="timed rowwise_i8 matmul calls per case (0: skip)")
+    ap.add_argument("--only", choices=[name for name, _, _ in LAYER] + ["gemm", "copy", "small", "native", "common", "i8"],
                     help="profiling aid: time only this GEMV's launch loop, the GEMM leg, or (copy) a "
                          f"{COPY_BYTES >> 20} MiB device-to-device copy that calibrates the traffic counters")
     args = ap.parse_args()
@@ -439,6 +494,9 @@ def main() -> int:
     if args.only == "small":
         print(json.dumps({"small_batch": small_batch_leg(kernel, events, stream, device, args.small_reps)}),
               flush=True)
+        return 0
+    if args.only == "i8":
+        print(json.dumps({"rowwise_i8": i8_leg(kernel, events, stream, device, args.i8_reps)}), flush=True)
         return 0
     if args.only == "common":
         print(json.dumps({"common_q4": common_leg(events, stream, device, args.common_reps)}), flush=True)
@@ -549,6 +607,7 @@ def main() -> int:
     small = small_batch_leg(kernel, events, stream, device, args.small_reps) if args.small_reps > 0 else None
     native = native_leg(events, stream, device, args.native_reps) if args.native_reps > 0 else None
     common = common_leg(events, stream, device, args.common_reps) if args.common_reps > 0 else None
+    i8 = i8_leg(kernel, events, stream, device, args.i8_reps) if args.i8_reps > 0 else None
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     result = {
         "metric": METRIC,
@@ -591,6 +650,7 @@ def main() -> int:
         "small_batch": small,
         "native_q4": native,
         "common_q4": common,
+        "rowwise_i8": i8,
     }
     print(json.dumps(result), flush=True)
     for bufs in copies.values():

@@ -318,6 +318,93 @@ __global__ __launch_bounds__(256) void i8_mfma_matmul(const int8_t *__restrict__
     }
 }
 
+// Batch 1..64 (2*batch <= 16 MT code rows: MT MFMA row tiles): one
+// workgroup per 16 weight rows, its 8 waves splitting K into contiguous ranges
+// of 64-value steps; a chunk of steps is loaded before its MFMAs (16 B per
+// lane and operand row tile per step: row l % 16 at k0 + 16 (l / 16)). The
+// waves' int32 sums meet in LDS (exact in any order), then the combine.
+constexpr int kGemvWaves = 8;
+template <int MT>
+__global__ __launch_bounds__(kGemvWaves * kWave) void i8_gemv_ksplit(const int8_t *__restrict__ codes,
+                                                                    const int8_t *__restrict__ w,
+                                                                    const float *__restrict__ scales,
+                                                                    const float *__restrict__ maxima,
+                                                                    const float *__restrict__ final_max,
+                                                                    float *__restrict__ y, int k, int n, int batch) {
+    constexpr int kChunk = MT <= 1 ? 8 : MT <= 2 ? 6 : MT <= 4 ? 4 : 2;   // steps loaded before their MFMAs
+    __shared__ int32x4 part[kGemvWaves - 1][MT][kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = threadIdx.x >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int n0 = blockIdx.x * 16;
+    const int rows = 2 * batch;
+    const int steps = (k + 63) / 64;
+    const int per = (steps + kGemvWaves - 1) / kGemvWaves;
+    const int s0 = wid * per, s1 = min(steps, s0 + per);
+    const int8_t *arow[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) arow[i] = codes + static_cast<size_t>(16 * i + c < rows ? 16 * i + c : 0) * k;
+    const int8_t *brow = w + static_cast<size_t>(min(n0 + c, n - 1)) * k;
+
+    int32x4 acc[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) acc[i] = int32x4{0, 0, 0, 0};
+    for (int sc = s0; sc < s1; sc += kChunk) {
+        int32x4 af[kChunk][MT], bf[kChunk];
+#pragma unroll
+        for (int t = 0; t < kChunk; ++t) {
+            const int kk0 = (sc + t) * 64 + 16 * g;
+            const bool ok = sc + t < s1 && kk0 < k;             // K % 32 == 0: a 16-byte chunk is all in or out
+            if (ok) {
+                const kk::u32x4_a4 b = kk::load_u32x4(reinterpret_cast<const uint32_t *>(brow + kk0));
+                bf[t] = int32x4{static_cast<int>(b.x), static_cast<int>(b.y), static_cast<int>(b.z), static_cast<int>(b.w)};
+            } else {
+                bf[t] = int32x4{0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int i = 0; i < MT; ++i) {
+                if (ok && 16 * i + c < rows) {
+                    const kk::u32x4_a4 a = kk::load_u32x4(reinterpret_cast<const uint32_t *>(arow[i] + kk0));
+                    af[t][i] = int32x4{static_cast<int>(a.x), static_cast<int>(a.y), static_cast<int>(a.z), static_cast<int>(a.w)};
+                } else {
+                    af[t][i] = int32x4{0, 0, 0, 0};
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < kChunk; ++t)
+#pragma unroll
+            for (int i = 0; i < MT; ++i) acc[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[t][i], bf[t], acc[i], 0, 0, 0);
+    }
+    if (wid > 0) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i) part[wid - 1][i][lane] = acc[i];
+    }
+    __syncthreads();
+    if (wid > 0) return;
+#pragma unroll
+    for (int v = 0; v < kGemvWaves - 1; ++v)
+#pragma unroll
+        for (int i = 0; i < MT; ++i) acc[i] += part[v][i][lane];
+
+    // D rows 4g + j of row tile i, weight row n0 + c: (q0, q1) of batch rows
+    // 8i + 2g and 8i + 2g + 1
+    const int r = n0 + c;
+    if (r >= n) return;
+    const float scale0 = final_max[0] / 127.0f;
+    const float scale1 = final_max[1] / 127.0f;
+    const float wmax = maxima[0] / 127.0f;
+    const float rs = scales[r];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int b = 8 * i + 2 * g + h;
+            if (b < batch)
+                y[static_cast<size_t>(b) * n + r] = combine(acc[i][2 * h], acc[i][2 * h + 1], wmax, scale0, scale1, rs);
+        }
+}
+
 int env_int(const char *name, int fallback) {
     const char *value = std::getenv(name);
     return value && *value ? std::atoi(value) : fallback;
@@ -365,9 +452,22 @@ extern "C" int kk_i8_matmul(const void *workspace, const int8_t *w, const float 
     if (!workspace || !w || !scales || !maxima || !y || k <= 0 || (k & 31) || n <= 0 || batch <= 0)
         return hipErrorInvalidValue;
     const Workspace ws = layout(const_cast<void *>(workspace), k, batch);
-    if (batch <= 8) {
-        if (route) *route = "i8_mfma_gemv";
-        return launch_i8<1, 2>(ws.codes, w, scales, maxima, ws.final_max, y, k, n, batch, stream);
+    if (batch <= 64) {
+        if (route) *route = batch <= 8 ? "i8_mfma_gemv" : "i8_mfma_gemm";
+        const dim3 grid((n + 15) / 16), block(kGemvWaves * kWave);
+        if (batch <= 8)
+            hipLaunchKernelGGL(i8_gemv_ksplit<1>, grid, block, 0, stream, ws.codes, w, scales, maxima, ws.final_max, y,
+                               k, n, batch);
+        else if (batch <= 16)
+            hipLaunchKernelGGL(i8_gemv_ksplit<2>, grid, block, 0, stream, ws.codes, w, scales, maxima, ws.final_max, y,
+                               k, n, batch);
+        else if (batch <= 32)
+            hipLaunchKernelGGL(i8_gemv_ksplit<4>, grid, block, 0, stream, ws.codes, w, scales, maxima, ws.final_max, y,
+                               k, n, batch);
+        else
+            hipLaunchKernelGGL(i8_gemv_ksplit<8>, grid, block, 0, stream, ws.codes, w, scales, maxima, ws.final_max, y,
+                               k, n, batch);
+        return hipGetLastError();
     }
     if (route) *route = "i8_mfma_gemm";
     return launch_i8<4, 4>(ws.codes, w, scales, maxima, ws.final_max, y, k, n, batch, stream);
