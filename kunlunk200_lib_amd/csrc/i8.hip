@@ -85,9 +85,28 @@ __device__ __forceinline__ int quant_residual(float residual, float max1) {
     return kk::round_clamp(residual * inv, 127);
 }
 
-__device__ __forceinline__ size_t code_index(size_t flat, int k, int component) {
-    const size_t b = flat / static_cast<size_t>(k), j = flat - b * static_cast<size_t>(k);
+// Values are handled in groups of 4 (flat index 4 q): K % 32 == 0, so a group
+// never crosses a row and its 4 codes go out as one 32-bit store at row
+// 2b + component.
+__device__ __forceinline__ size_t group_code_offset(size_t flat4, int k, int component) {
+    const size_t b = flat4 / static_cast<size_t>(k), j = flat4 - b * static_cast<size_t>(k);
     return (2 * b + component) * static_cast<size_t>(k) + j;
+}
+__device__ __forceinline__ uint32_t pack_codes(int a, int b, int c, int d) {
+    return (static_cast<uint32_t>(a) & 0xffu) | ((static_cast<uint32_t>(b) & 0xffu) << 8) |
+           ((static_cast<uint32_t>(c) & 0xffu) << 16) | (static_cast<uint32_t>(d) << 24);
+}
+// four activations from a 4-byte aligned address (X needs only float alignment)
+typedef float f32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+__device__ __forceinline__ float4 load_x4(const float *x, size_t q) {
+    const f32x4_a4 v = *reinterpret_cast<const f32x4_a4 *>(x + 4 * q);
+    return float4{v.x, v.y, v.z, v.w};
+}
+__device__ __forceinline__ bool finite4(const float4 &v) {
+    return isfinite(v.x) && isfinite(v.y) && isfinite(v.z) && isfinite(v.w);
+}
+__device__ __forceinline__ float absmax4(const float4 &v) {
+    return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
 }
 
 // Pass 1: per-workgroup max|x| and non-finite detection.
@@ -96,11 +115,12 @@ __global__ __launch_bounds__(kQuantThreads) void i8_pass_max(const float *__rest
     __shared__ float scratch[kQuantThreads / kWave];
     float m = 0.0f;
     bool bad = false;
-    for (size_t i = static_cast<size_t>(blockIdx.x) * kQuantThreads + threadIdx.x; i < count;
-         i += static_cast<size_t>(gridDim.x) * kQuantThreads) {
-        const float v = x[i];
-        bad |= !isfinite(v);
-        m = fmaxf(m, fabsf(v));
+    const size_t groups4 = count / 4;
+    for (size_t q = static_cast<size_t>(blockIdx.x) * kQuantThreads + threadIdx.x; q < groups4;
+         q += static_cast<size_t>(gridDim.x) * kQuantThreads) {
+        const float4 v = load_x4(x, q);
+        bad |= !finite4(v);
+        m = fmaxf(m, absmax4(v));
     }
     if (bad) flag_nonfinite(status);
     m = block_max<kQuantThreads>(m, scratch);
@@ -118,12 +138,15 @@ __global__ __launch_bounds__(kQuantThreads) void i8_pass_primary(const float *__
     float max0 = block_max<kQuantThreads>(m, scratch);
     if (max0 == 0.0f) max0 = 1.0f;
     float m1 = 0.0f;
-    for (size_t i = static_cast<size_t>(blockIdx.x) * kQuantThreads + threadIdx.x; i < count;
-         i += static_cast<size_t>(gridDim.x) * kQuantThreads) {
-        const float v = x[i];
-        const int q0 = quant_primary(v, max0);
-        codes[code_index(i, k, 0)] = static_cast<int8_t>(q0);
-        m1 = fmaxf(m1, fabsf(residual_of(v, q0, max0)));
+    const size_t groups4 = count / 4;
+    for (size_t q = static_cast<size_t>(blockIdx.x) * kQuantThreads + threadIdx.x; q < groups4;
+         q += static_cast<size_t>(gridDim.x) * kQuantThreads) {
+        const float4 v = load_x4(x, q);
+        const int a = quant_primary(v.x, max0), b = quant_primary(v.y, max0);
+        const int c = quant_primary(v.z, max0), d = quant_primary(v.w, max0);
+        *reinterpret_cast<uint32_t *>(codes + group_code_offset(4 * q, k, 0)) = pack_codes(a, b, c, d);
+        m1 = fmaxf(m1, fmaxf(fmaxf(fabsf(residual_of(v.x, a, max0)), fabsf(residual_of(v.y, b, max0))),
+                             fmaxf(fabsf(residual_of(v.z, c, max0)), fabsf(residual_of(v.w, d, max0)))));
     }
     m1 = block_max<kQuantThreads>(m1, scratch);
     if (threadIdx.x == 0) partial1[blockIdx.x] = m1;
@@ -145,11 +168,12 @@ __global__ __launch_bounds__(kQuantThreads) void i8_pass_residual(const float *_
     float max1 = block_max<kQuantThreads>(m1, scratch);
     if (max0 == 0.0f) max0 = 1.0f;
     if (max1 == 0.0f) max1 = 1.0f;
-    for (size_t i = static_cast<size_t>(blockIdx.x) * kQuantThreads + threadIdx.x; i < count;
-         i += static_cast<size_t>(gridDim.x) * kQuantThreads) {
-        const float v = x[i];
-        const int q0 = quant_primary(v, max0);
-        codes[code_index(i, k, 1)] = static_cast<int8_t>(quant_residual(residual_of(v, q0, max0), max1));
+    const size_t groups4 = count / 4;
+    for (size_t q = static_cast<size_t>(blockIdx.x) * kQuantThreads + threadIdx.x; q < groups4;
+         q += static_cast<size_t>(gridDim.x) * kQuantThreads) {
+        const float4 v = load_x4(x, q);
+        auto q1 = [&](float value) { return quant_residual(residual_of(value, quant_primary(value, max0), max0), max1); };
+        *reinterpret_cast<uint32_t *>(codes + group_code_offset(4 * q, k, 1)) = pack_codes(q1(v.x), q1(v.y), q1(v.z), q1(v.w));
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         final_max[0] = max0;
@@ -157,34 +181,47 @@ __global__ __launch_bounds__(kQuantThreads) void i8_pass_residual(const float *_
     }
 }
 
-// All three passes in one workgroup, for small X.
+// All three passes in one workgroup, for small X (count <= 4 * kFusedThreads *
+// kFusedGroups): each thread loads its groups once and keeps them in registers.
+constexpr int kFusedGroups = 16;
 __global__ __launch_bounds__(kFusedThreads) void i8_quantize_fused(const float *__restrict__ x, size_t count, int k,
                                                                   int8_t *__restrict__ codes,
                                                                   float *__restrict__ final_max, int *status) {
     __shared__ float scratch[kFusedThreads / kWave];
+    const int groups4 = static_cast<int>(count / 4);
+    float4 v[kFusedGroups];
     float m = 0.0f;
     bool bad = false;
-    for (size_t i = threadIdx.x; i < count; i += kFusedThreads) {
-        const float v = x[i];
-        bad |= !isfinite(v);
-        m = fmaxf(m, fabsf(v));
+#pragma unroll
+    for (int t = 0; t < kFusedGroups; ++t) {
+        const int q = static_cast<int>(threadIdx.x) + kFusedThreads * t;
+        v[t] = q < groups4 ? load_x4(x, q) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        bad |= !finite4(v[t]);
+        m = fmaxf(m, absmax4(v[t]));
     }
     if (bad) flag_nonfinite(status);
     float max0 = block_max<kFusedThreads>(m, scratch);
     if (max0 == 0.0f) max0 = 1.0f;
     float m1 = 0.0f;
-    for (size_t i = threadIdx.x; i < count; i += kFusedThreads) {
-        const float v = x[i];
-        const int q0 = quant_primary(v, max0);
-        codes[code_index(i, k, 0)] = static_cast<int8_t>(q0);
-        m1 = fmaxf(m1, fabsf(residual_of(v, q0, max0)));
+#pragma unroll
+    for (int t = 0; t < kFusedGroups; ++t) {
+        const int q = static_cast<int>(threadIdx.x) + kFusedThreads * t;
+        if (q >= groups4) break;
+        const int a = quant_primary(v[t].x, max0), b = quant_primary(v[t].y, max0);
+        const int c = quant_primary(v[t].z, max0), d = quant_primary(v[t].w, max0);
+        *reinterpret_cast<uint32_t *>(codes + group_code_offset(4 * static_cast<size_t>(q), k, 0)) = pack_codes(a, b, c, d);
+        m1 = fmaxf(m1, fmaxf(fmaxf(fabsf(residual_of(v[t].x, a, max0)), fabsf(residual_of(v[t].y, b, max0))),
+                             fmaxf(fabsf(residual_of(v[t].z, c, max0)), fabsf(residual_of(v[t].w, d, max0)))));
     }
     float max1 = block_max<kFusedThreads>(m1, scratch);
     if (max1 == 0.0f) max1 = 1.0f;
-    for (size_t i = threadIdx.x; i < count; i += kFusedThreads) {
-        const float v = x[i];
-        const int q0 = quant_primary(v, max0);
-        codes[code_index(i, k, 1)] = static_cast<int8_t>(quant_residual(residual_of(v, q0, max0), max1));
+#pragma unroll
+    for (int t = 0; t < kFusedGroups; ++t) {
+        const int q = static_cast<int>(threadIdx.x) + kFusedThreads * t;
+        if (q >= groups4) break;
+        auto q1 = [&](float value) { return quant_residual(residual_of(value, quant_primary(value, max0), max0), max1); };
+        *reinterpret_cast<uint32_t *>(codes + group_code_offset(4 * static_cast<size_t>(q), k, 1)) =
+            pack_codes(q1(v[t].x), q1(v[t].y), q1(v[t].z), q1(v[t].w));
     }
     if (threadIdx.x == 0) {
         final_max[0] = max0;
@@ -432,7 +469,8 @@ extern "C" int kk_i8_quantize(const float *x, int k, int batch, void *workspace,
     if (!x || !workspace || !status || k <= 0 || batch <= 0) return hipErrorInvalidValue;
     const Workspace ws = layout(workspace, k, batch);
     const size_t count = static_cast<size_t>(k) * batch;
-    const size_t fused_limit = static_cast<size_t>(env_int("KUNLUN_I8_FUSED_QUANT_LIMIT", 65536));
+    const size_t fused_limit = std::min<size_t>(static_cast<size_t>(env_int("KUNLUN_I8_FUSED_QUANT_LIMIT", 65536)),
+                                                4 * kFusedThreads * kFusedGroups);
     if (count <= fused_limit) {
         hipLaunchKernelGGL(i8_quantize_fused, dim3(1), dim3(kFusedThreads), 0, stream, x, count, k, ws.codes,
                            ws.final_max, status);

@@ -195,6 +195,17 @@ def test_rowwise_i8_bit_exact(gpu, oracle, k, n, batch):
     assert np.all(np.abs(y - gold) <= i8_error_bound(w, x))
 
 
+@pytest.mark.parametrize("k,n,batch", [(1024, 96, 3), (2048, 64, 40), (4096, 32, 20)])
+def test_rowwise_i8_activation_4_byte_aligned(gpu, oracle, k, n, batch):
+    # X only float-aligned: the quantizer's 16-byte loads run at 4-byte alignment
+    # (single-workgroup quantizer up to 65536 values, three passes above)
+    w = gaussian((n, k), 0.02, k + n)
+    x = gaussian((batch, k), 1.0, k + n + 1)
+    y, route, guard_ok = run_matmul(kl.WeightType.rowwise_i8, None, x, k, n, batch, w_f32=w, x_offset=4)
+    assert guard_ok
+    assert np.array_equal(y.view(np.uint32), oracle.rowwise_i8_matmul(w, x).view(np.uint32))
+
+
 def i8_error_bound(w, x):
     amax_w = np.abs(w).max(axis=1).astype(np.float64)[None, :]
     x64 = x.astype(np.float64)
