@@ -442,6 +442,148 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void i8_gemv_ksplit(const int8_
         }
 }
 
+// Batch > 64, K % 128 == 0: LDS-staged int8 GEMM. Workgroup tile: 128 code
+// rows (64 batch rows) x 128 weight rows; 8 waves = 2 k-groups x (2 x 2)
+// wave tiles of 64 x 64. A stage is 128 K: k-group h takes the stage's 64-K
+// step h. Both operands arrive by buffer_load_dwordx4 ... lds (1 KB of LDS per
+// wave instruction, no registers), three stages ahead into a ring of four.
+// LDS rows are 128 B (8 chunks of 16 B); chunk ch of row r sits at position
+// ch ^ ((r >> 1) & 7), so the 16 rows of an MFMA operand (row pairs share a
+// 256-byte bank period) read 16 distinct bank groups.
+constexpr int kIgRows = 128;                  // code rows and weight rows per tile
+constexpr int kIgK = 128;                     // K per stage
+constexpr int kIgSlots = 4;
+constexpr int kIgOpBytes = kIgRows * kIgK;    // 16 KiB per operand and stage
+constexpr int kIgStageBytes = 2 * kIgOpBytes;
+constexpr int kIgLdsBytes = kIgSlots * kIgStageBytes;   // 128 KiB
+constexpr int kIgCopiesPerWave = 4;           // 2 A + 2 B copies of 1 KiB per stage
+static_assert(kIgLdsBytes >= 4 * 64 * 64 * 4 && kIgLdsBytes <= 160 * 1024, "ring also holds the k-group sums");
+
+__device__ __forceinline__ void ig_wait(int stages_after) {   // vmcnt(4 * stages_after), 0..2
+    if (stages_after <= 0) __builtin_amdgcn_s_waitcnt(0x0F70);
+    else if (stages_after == 1) __builtin_amdgcn_s_waitcnt(0x0F70 | kIgCopiesPerWave);
+    else __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * kIgCopiesPerWave));
+}
+
+// Stage s's copies of wave `wid`: A copies wid, wid + 8 and B copies wid,
+// wid + 8 (copy i: rows 8i .. 8i+7 of the tile, lane -> row 8i + l/8,
+// position l % 8). (A separate function: the host pass rejects a kernel-local
+// lambda that hands captured values to these builtins.)
+__device__ __forceinline__ void ig_copy_stage(const int8_t *a_tile, int a_extent, const int8_t *b_tile, int b_extent,
+                                              const uint32_t (&a_off)[2], const uint32_t (&b_off)[2], int wid,
+                                              int s) {
+    extern __shared__ __align__(16) uint8_t ig_lds[];
+    const __amdgpu_buffer_rsrc_t a_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(a_tile), 0, a_extent, 0x00020000);
+    const __amdgpu_buffer_rsrc_t b_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(b_tile), 0, b_extent, 0x00020000);
+    __attribute__((address_space(3))) uint8_t *buf =
+        (__attribute__((address_space(3))) uint8_t *)ig_lds + (s % kIgSlots) * kIgStageBytes;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, buf + (wid + 8 * t) * 1024, 16, a_off[t], s * kIgK, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, buf + kIgOpBytes + (wid + 8 * t) * 1024, 16, b_off[t],
+                                                 s * kIgK, 0, 0);
+    }
+}
+
+__global__ __launch_bounds__(512) void i8_lds_gemm(const int8_t *__restrict__ codes, const int8_t *__restrict__ w,
+                                                   const float *__restrict__ scales, const float *__restrict__ maxima,
+                                                   const float *__restrict__ final_max, float *__restrict__ y,
+                                                   int k, int n, int batch, int m_tiles, int tiles, int tiles_per_xcd) {
+    extern __shared__ __align__(16) uint8_t ig_lds[];
+    const int bid = blockIdx.x;
+    const int tile = (bid % 8) * tiles_per_xcd + bid / 8;       // weight-tile major, contiguous per XCD
+    if (tile >= tiles) return;                                  // whole workgroup, before any barrier
+    const int nt = tile / m_tiles, mt = tile - nt * m_tiles;
+    const int rows = 2 * batch;
+    const int m0 = mt * kIgRows, n0 = nt * kIgRows;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+    const int kg = wid >> 2, wm = (wid >> 1) & 1, wn = wid & 1;
+    const int g = lane >> 4, c = lane & 15;
+
+    // copy offsets: lane l of copy i -> tile row 8i + l/8 (clamped to the last
+    // real row), chunk (l % 8) ^ ((row >> 1) & 7) of the stage's 128 bytes
+    const int a_rows = min(kIgRows, rows - m0), b_rows = min(kIgRows, n - n0);
+    const int8_t *a_tile = codes + static_cast<size_t>(m0) * k;
+    const int8_t *b_tile = w + static_cast<size_t>(n0) * k;
+    uint32_t a_off[2], b_off[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int row = 8 * (wid + 8 * t) + (lane >> 3);
+        const int chunk = (lane & 7) ^ ((row >> 1) & 7);
+        a_off[t] = static_cast<uint32_t>(min(row, a_rows - 1)) * k + 16 * chunk;
+        b_off[t] = static_cast<uint32_t>(min(row, b_rows - 1)) * k + 16 * chunk;
+    }
+    const int a_extent = a_rows * k, b_extent = b_rows * k;
+    const int stages = k / kIgK;
+
+    int32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = int32x4{0, 0, 0, 0};
+
+    const int ahead0 = min(kIgSlots - 1, stages);
+    for (int s = 0; s < ahead0; ++s) ig_copy_stage(a_tile, a_extent, b_tile, b_extent, a_off, b_off, wid, s);
+    for (int s = 0; s < stages; ++s) {
+        ig_wait(min(kIgSlots - 2, stages - 1 - s));
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");
+        if (s + kIgSlots - 1 < stages)
+            ig_copy_stage(a_tile, a_extent, b_tile, b_extent, a_off, b_off, wid, s + kIgSlots - 1);
+        const uint8_t *abuf = ig_lds + (s % kIgSlots) * kIgStageBytes;
+        const uint8_t *bbuf = abuf + kIgOpBytes;
+        // k-group kg: step kg of the stage, chunks 4 kg + g of each row
+        int32x4 af[4], bf[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ra = wm * 64 + i * 16 + c, rb = wn * 64 + i * 16 + c;
+            af[i] = *reinterpret_cast<const int32x4 *>(abuf + ra * kIgK + (((4 * kg + g) ^ ((ra >> 1) & 7)) * 16));
+            bf[i] = *reinterpret_cast<const int32x4 *>(bbuf + rb * kIgK + (((4 * kg + g) ^ ((rb >> 1) & 7)) * 16));
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+
+    // k-group 1 hands its sums to k-group 0 (exact int32 adds), which combines
+    __syncthreads();                                            // every copy landed (last wait: all), ring idle
+    int32x4 *xfer = reinterpret_cast<int32x4 *>(ig_lds) + (wid & 3) * 16 * kWave;
+    if (kg == 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xfer[(i * 4 + j) * kWave + lane] = acc[i][j];
+    }
+    __syncthreads();
+    if (kg == 1) return;
+    const float scale0 = final_max[0] / 127.0f;
+    const float scale1 = final_max[1] / 127.0f;
+    const float wmax = maxima[0] / 127.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = n0 + wn * 64 + j * 16 + c;
+        if (r >= n) continue;
+        const float rs = scales[r];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int32x4 d = acc[i][j] + xfer[(i * 4 + j) * kWave + lane];
+            // D rows 4g .. 4g+3 of row tile i: (q0, q1) of two batch rows
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int b = (m0 + wm * 64 + i * 16 + 4 * g) / 2 + h;
+                if (b < batch) y[static_cast<size_t>(b) * n + r] = combine(d[2 * h], d[2 * h + 1], wmax, scale0, scale1, rs);
+            }
+        }
+    }
+}
+
 int env_int(const char *name, int fallback) {
     const char *value = std::getenv(name);
     return value && *value ? std::atoi(value) : fallback;
@@ -508,5 +650,26 @@ extern "C" int kk_i8_matmul(const void *workspace, const int8_t *w, const float 
         return hipGetLastError();
     }
     if (route) *route = "i8_mfma_gemm";
+    if (k % kIgK == 0 && static_cast<long long>(2 * batch) * k <= 0x7fffffffLL &&
+        static_cast<long long>(n) * k <= 0x7fffffffLL) {
+        constexpr int kMaxDevices = 64;
+        static bool configured[kMaxDevices] = {};
+        int device = 0;
+        hipError_t rc = hipGetDevice(&device);
+        if (rc != hipSuccess) return rc;
+        if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+        if (!configured[device]) {
+            rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&i8_lds_gemm),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, kIgLdsBytes);
+            if (rc != hipSuccess) return rc;
+            configured[device] = true;
+        }
+        const int m_tiles = (2 * batch + kIgRows - 1) / kIgRows;
+        const int tiles = m_tiles * ((n + kIgRows - 1) / kIgRows);
+        const int tiles_per_xcd = (tiles + 7) / 8;
+        hipLaunchKernelGGL(i8_lds_gemm, dim3(tiles_per_xcd * 8), dim3(512), kIgLdsBytes, stream, ws.codes, w, scales,
+                           maxima, ws.final_max, y, k, n, batch, m_tiles, tiles, tiles_per_xcd);
+        return hipGetLastError();
+    }
     return launch_i8<4, 4>(ws.codes, w, scales, maxima, ws.final_max, y, k, n, batch, stream);
 }

@@ -173,9 +173,12 @@ def test_statistics_count_submissions(gpu, oracle):
 # --- rowwise_i8 --------------------------------------------------------------
 
 # batch <= 64: K-split kernel with 1, 2, 4 or 8 row tiles of 16 code rows
-# (batch 1-8, 9-16, 17-32, 33-64); above: the tiled GEMM
+# (batch 1-8, 9-16, 17-32, 33-64); above: the LDS-staged GEMM when K % 128 == 0
+# (partial M and N tiles: 100, 130, 97 batch rows, N 300, 130), else the
+# register-tiled one (96, 70)
 I8_SHAPES = [(64, 3, 1), (1024, 512, 4), (4096, 4096, 1), (96, 17, 9), (4096, 1024, 32),
-             (16384, 64, 2), (2048, 300, 8), (1024, 256, 100), (2048, 96, 17), (256, 70, 40), (512, 200, 64)]
+             (16384, 64, 2), (2048, 300, 8), (1024, 256, 100), (2048, 96, 17), (256, 70, 40), (512, 200, 64),
+             (512, 300, 130), (2048, 130, 97), (96, 40, 70)]
 
 
 @pytest.mark.parametrize("k,n,batch", I8_SHAPES)
