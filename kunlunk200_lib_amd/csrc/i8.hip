@@ -442,6 +442,127 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void i8_gemv_ksplit(const int8_
         }
 }
 
+// Batch 1..8 with batch * K <= 16384: the quantization and the product in one
+// launch. Every workgroup quantizes X itself (the single-workgroup pass's
+// arithmetic, X in registers) into an LDS code table, rows padded by 16 bytes
+// so the 16 MFMA rows read distinct banks, then runs the K-split product of
+// i8_gemv_ksplit<1> with A read from LDS.
+constexpr int kFusedGemvCount = 16384;
+constexpr int kFusedGemvGroups = kFusedGemvCount / 4 / (kGemvWaves * kWave);   // 8 float4 per thread
+__global__ __launch_bounds__(kGemvWaves * kWave) void i8_gemv_fused(const float *__restrict__ x,
+                                                                   const int8_t *__restrict__ w,
+                                                                   const float *__restrict__ scales,
+                                                                   const float *__restrict__ maxima,
+                                                                   float *__restrict__ y, int k, int n, int batch,
+                                                                   int *status) {
+    constexpr int kThreadsF = kGemvWaves * kWave;
+    __shared__ float scratch[kGemvWaves];
+    __shared__ __align__(16) int8_t table[2 * kFusedGemvCount + 16 * 16];   // [2 batch][k + 16]
+    __shared__ int32x4 part[kGemvWaves - 1][kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = threadIdx.x >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int rows = 2 * batch;
+    const int stride = k + 16;
+    const int groups4 = batch * k / 4;
+    const int n0 = blockIdx.x * 16;
+    const int steps = (k + 63) / 64;
+    const int per = (steps + kGemvWaves - 1) / kGemvWaves;
+    const int s0 = wid * per, s1 = min(steps, s0 + per);
+    const int8_t *brow = w + static_cast<size_t>(min(n0 + c, n - 1)) * k;
+    constexpr int kChunk = 8;
+    auto load_b = [&](int sc, int32x4 (&bf)[kChunk]) {
+#pragma unroll
+        for (int t = 0; t < kChunk; ++t) {
+            const int kk0 = (sc + t) * 64 + 16 * g;
+            if (sc + t < s1 && kk0 < k) {
+                const kk::u32x4_a4 b = kk::load_u32x4(reinterpret_cast<const uint32_t *>(brow + kk0));
+                bf[t] = int32x4{static_cast<int>(b.x), static_cast<int>(b.y), static_cast<int>(b.z), static_cast<int>(b.w)};
+            } else {
+                bf[t] = int32x4{0, 0, 0, 0};
+            }
+        }
+    };
+
+    // 1. two-pass quantization (reference src/k200.cpp:212-225); the X loads
+    // go first, then the wave's first weight chunk, which stays in flight
+    // while X is quantized (the memory counter is in order)
+    float4 v[kFusedGemvGroups];
+#pragma unroll
+    for (int t = 0; t < kFusedGemvGroups; ++t) {
+        const int q = static_cast<int>(threadIdx.x) + kThreadsF * t;
+        v[t] = q < groups4 ? load_x4(x, q) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    int32x4 bf[kChunk];
+    load_b(s0, bf);
+    __builtin_amdgcn_sched_barrier(0);
+    float m = 0.0f;
+    bool bad = false;
+#pragma unroll
+    for (int t = 0; t < kFusedGemvGroups; ++t) {
+        bad |= !finite4(v[t]);
+        m = fmaxf(m, absmax4(v[t]));
+    }
+    if (bad) flag_nonfinite(status);
+    float max0 = block_max<kThreadsF>(m, scratch);
+    if (max0 == 0.0f) max0 = 1.0f;
+    float m1 = 0.0f;
+#pragma unroll
+    for (int t = 0; t < kFusedGemvGroups; ++t) {
+        const int q = static_cast<int>(threadIdx.x) + kThreadsF * t;
+        if (q >= groups4) break;
+        const int a = quant_primary(v[t].x, max0), b = quant_primary(v[t].y, max0);
+        const int cc = quant_primary(v[t].z, max0), d = quant_primary(v[t].w, max0);
+        const int row = 4 * q / k, j = 4 * q - row * k;
+        *reinterpret_cast<uint32_t *>(table + (2 * row) * stride + j) = pack_codes(a, b, cc, d);
+        m1 = fmaxf(m1, fmaxf(fmaxf(fabsf(residual_of(v[t].x, a, max0)), fabsf(residual_of(v[t].y, b, max0))),
+                             fmaxf(fabsf(residual_of(v[t].z, cc, max0)), fabsf(residual_of(v[t].w, d, max0)))));
+    }
+    float max1 = block_max<kThreadsF>(m1, scratch);
+    if (max1 == 0.0f) max1 = 1.0f;
+#pragma unroll
+    for (int t = 0; t < kFusedGemvGroups; ++t) {
+        const int q = static_cast<int>(threadIdx.x) + kThreadsF * t;
+        if (q >= groups4) break;
+        auto q1 = [&](float value) { return quant_residual(residual_of(value, quant_primary(value, max0), max0), max1); };
+        const int row = 4 * q / k, j = 4 * q - row * k;
+        *reinterpret_cast<uint32_t *>(table + (2 * row + 1) * stride + j) =
+            pack_codes(q1(v[t].x), q1(v[t].y), q1(v[t].z), q1(v[t].w));
+    }
+    __syncthreads();
+
+    // 2. K-split int8 MFMA product (A from the table)
+    const int8_t *arow = table + (c < rows ? c : 0) * stride;
+    int32x4 acc = {0, 0, 0, 0};
+    for (int sc = s0; sc < s1; sc += kChunk) {
+        if (sc != s0) load_b(sc, bf);
+#pragma unroll
+        for (int t = 0; t < kChunk; ++t) {
+            const int kk0 = (sc + t) * 64 + 16 * g;
+            const int32x4 af = sc + t < s1 && kk0 < k && c < rows ? *reinterpret_cast<const int32x4 *>(arow + kk0)
+                                                                  : int32x4{0, 0, 0, 0};
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[t], acc, 0, 0, 0);
+        }
+    }
+    if (wid > 0) part[wid - 1][lane] = acc;
+    __syncthreads();
+    if (wid > 0) return;
+#pragma unroll
+    for (int vv = 0; vv < kGemvWaves - 1; ++vv) acc += part[vv][lane];
+    const int r = n0 + c;
+    if (r >= n) return;
+    const float scale0 = max0 / 127.0f;
+    const float scale1 = max1 / 127.0f;
+    const float wmax = maxima[0] / 127.0f;
+    const float rs = scales[r];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int b = 2 * g + h;
+        if (b < batch) y[static_cast<size_t>(b) * n + r] = combine(acc[2 * h], acc[2 * h + 1], wmax, scale0, scale1, rs);
+    }
+}
+
 // Batch > 64, K % 128 == 0: LDS-staged int8 GEMM. Workgroup tile: 128 code
 // rows (64 batch rows) x 128 weight rows; 8 waves = 2 k-groups x (2 x 2)
 // wave tiles of 64 x 64. A stage is 128 K: k-group h takes the stage's 64-K
@@ -672,4 +793,17 @@ extern "C" int kk_i8_matmul(const void *workspace, const int8_t *w, const float 
         return hipGetLastError();
     }
     return launch_i8<4, 4>(ws.codes, w, scales, maxima, ws.final_max, y, k, n, batch, stream);
+}
+
+extern "C" int kk_i8_gemv_fused_supported(int k, int batch) {
+    return k > 0 && (k % 32) == 0 && batch >= 1 && batch <= 8 && static_cast<long long>(batch) * k <= kFusedGemvCount;
+}
+
+extern "C" int kk_i8_gemv_fused(const float *x, const int8_t *w, const float *scales, const float *maxima, float *y,
+                                int k, int n, int batch, int *status, hipStream_t stream) {
+    if (!x || !w || !scales || !maxima || !y || !status || n <= 0 || !kk_i8_gemv_fused_supported(k, batch))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(i8_gemv_fused, dim3((n + 15) / 16), dim3(kGemvWaves * kWave), 0, stream, x, w, scales, maxima,
+                       y, k, n, batch, status);
+    return hipGetLastError();
 }

@@ -88,6 +88,13 @@ int kk_common_gemv(const void *w0, float *y0, const void *w1, float *y1, const v
 int kk_common_gemm(const void *w, const void *tiled, const void *row_scales, float *y, int rows, int defined_rows,
                    int kp, int n, int np, hipStream_t stream);
 
+// rowwise_i8 at batch 1..8 with batch * K <= 16384, quantization and product
+// in one launch (no workspace); the non-finite activation flag goes to
+// `status` as kk_i8_quantize's does.
+int kk_i8_gemv_fused_supported(int k, int batch);
+int kk_i8_gemv_fused(const float *x, const int8_t *w, const float *scales, const float *maxima, float *y, int k, int n,
+                     int batch, int *status, hipStream_t stream);
+
 // Bytes of device workspace kk_i8_quantize needs for `count` activations.
 size_t kk_i8_workspace_bytes(int k, int batch);
 // Two-pass per-tensor INT8 quantization of X[batch,k] into `workspace`
