@@ -240,16 +240,18 @@ def test_rowwise_i8_large_activation_path(gpu, oracle):
     assert np.array_equal(y.view(np.uint32), expect.view(np.uint32))
 
 
-def test_rowwise_i8_nonfinite_activation_aborts_at_wait(gpu):
+@pytest.mark.parametrize("k,batch", [(64, 1), (4096, 20)])
+def test_rowwise_i8_nonfinite_activation_aborts_at_wait(gpu, k, batch):
     # reference src/k200.cpp:213 aborts on a non-finite activation; here the
-    # device flags it and wait() aborts with the same diagnostic.
+    # device flags it and wait() aborts with the same diagnostic (batch 1: the
+    # fused GEMV's quantizer; 4096 x 20: the three-pass quantizer).
     code = (
         "import numpy as np, sys\n"
         f"sys.path.insert(0, {os.path.join(ROOT, 'tests')!r})\n"
         "import kunlunk200_lib_amd as kl\n"
         "from gpu_util import run_matmul\n"
-        "w = np.ones((8, 64), np.float32); x = np.ones((1, 64), np.float32); x[0, 3] = np.inf\n"
-        "run_matmul(kl.WeightType.rowwise_i8, None, x, 64, 8, 1, w_f32=w)\n"
+        f"w = np.ones((8, {k}), np.float32); x = np.ones(({batch}, {k}), np.float32); x[{batch} - 1, 3] = np.inf\n"
+        f"run_matmul(kl.WeightType.rowwise_i8, None, x, {k}, 8, {batch}, w_f32=w)\n"
         "print('NOT REJECTED')\n"
     )
     env = dict(os.environ, PYTHONPATH=ROOT)
