@@ -45,36 +45,41 @@ constexpr int kXcds = 8;                       // MI355X: workgroups go round-ro
 size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 
 // ---------------------------------------------------------------------------
-// Prepass: one workgroup per padded row.
-template <bool PERMUTE>
+// Prepass: one workgroup per padded row; PER groups of 8 values per thread
+// (PER * 8 * kPrepassThreads >= k_pad). Every load is issued before the
+// first wait: the row and group indices are clamped into X and the slots
+// past the row (or of a padding row) are zeroed afterwards.
+template <bool PERMUTE, int PER>
 __global__ __launch_bounds__(kPrepassThreads) void x_to_f16(const float *__restrict__ x, int m_rows, int k,
                                                            int k_pad, _Float16 *__restrict__ x16,
                                                            float *__restrict__ row_inv) {
     __shared__ float scratch[kPrepassThreads / kWave];
     const int row = blockIdx.x;
     const int groups = k >> 3;                       // 8 values per group
-    constexpr int kMaxGroupsPerThread = 16384 / 8 / kPrepassThreads;
-    float v[kMaxGroupsPerThread][8];
+    float v[PER][8];
     float m = 0.0f;
     const bool real = row < m_rows;
+    const float *src_row = x + static_cast<size_t>(min(row, m_rows - 1)) * k;
 #pragma unroll
-    for (int g = 0; g < kMaxGroupsPerThread; ++g) {
-        const int grp = g * kPrepassThreads + threadIdx.x;
-        if (real && grp < groups) {
-            const int blk = grp >> 2, i = grp & 3;
-            const float *src = x + static_cast<size_t>(row) * k + blk * 32;
-            if (PERMUTE) {   // positions 8i..8i+7 <- values 4i, 4i+2, 4i+1, 4i+3, 16+4i, ...
-                const float4 lo = *reinterpret_cast<const float4 *>(src + 4 * i);
-                const float4 hi = *reinterpret_cast<const float4 *>(src + 16 + 4 * i);
-                v[g][0] = lo.x; v[g][1] = lo.z; v[g][2] = lo.y; v[g][3] = lo.w;
-                v[g][4] = hi.x; v[g][5] = hi.z; v[g][6] = hi.y; v[g][7] = hi.w;
-            } else {
-                const float4 a = *reinterpret_cast<const float4 *>(src + 8 * i);
-                const float4 b = *reinterpret_cast<const float4 *>(src + 8 * i + 4);
-                v[g][0] = a.x; v[g][1] = a.y; v[g][2] = a.z; v[g][3] = a.w;
-                v[g][4] = b.x; v[g][5] = b.y; v[g][6] = b.z; v[g][7] = b.w;
-            }
+    for (int g = 0; g < PER; ++g) {
+        const int grp = min(g * kPrepassThreads + static_cast<int>(threadIdx.x), groups - 1);
+        const int blk = grp >> 2, i = grp & 3;
+        const float *src = src_row + blk * 32;
+        if (PERMUTE) {   // positions 8i..8i+7 <- values 4i, 4i+2, 4i+1, 4i+3, 16+4i, ...
+            const float4 lo = *reinterpret_cast<const float4 *>(src + 4 * i);
+            const float4 hi = *reinterpret_cast<const float4 *>(src + 16 + 4 * i);
+            v[g][0] = lo.x; v[g][1] = lo.z; v[g][2] = lo.y; v[g][3] = lo.w;
+            v[g][4] = hi.x; v[g][5] = hi.z; v[g][6] = hi.y; v[g][7] = hi.w;
         } else {
+            const float4 a = *reinterpret_cast<const float4 *>(src + 8 * i);
+            const float4 b = *reinterpret_cast<const float4 *>(src + 8 * i + 4);
+            v[g][0] = a.x; v[g][1] = a.y; v[g][2] = a.z; v[g][3] = a.w;
+            v[g][4] = b.x; v[g][5] = b.y; v[g][6] = b.z; v[g][7] = b.w;
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < PER; ++g) {
+        if (!real || g * kPrepassThreads + static_cast<int>(threadIdx.x) >= groups) {
 #pragma unroll
             for (int t = 0; t < 8; ++t) v[g][t] = 0.0f;
         }
@@ -94,7 +99,7 @@ __global__ __launch_bounds__(kPrepassThreads) void x_to_f16(const float *__restr
     if (threadIdx.x == 0) row_inv[row] = ldexpf(1.0f, e - 14);
     _Float16 *dst = x16 + static_cast<size_t>(row) * k_pad;
 #pragma unroll
-    for (int g = 0; g < kMaxGroupsPerThread; ++g) {
+    for (int g = 0; g < PER; ++g) {
         const int grp = g * kPrepassThreads + threadIdx.x;
         if (grp < (k_pad >> 3)) {
             half8 h;
@@ -103,6 +108,28 @@ __global__ __launch_bounds__(kPrepassThreads) void x_to_f16(const float *__restr
             *reinterpret_cast<half8 *>(dst + grp * 8) = h;
         }
     }
+}
+
+// x_to_f16 with the fewest groups per thread that cover k_pad (k_pad <= 16384
+// + alignment: at most 8 x 8 x 256 = 16384 values, checked by the callers'
+// k <= 16384 and kKAlign | 16384).
+void launch_x_to_f16(bool permute, const float *x, int batch, int k, int m_pad, int k_pad, _Float16 *x16,
+                     float *row_inv, hipStream_t stream) {
+    const int per_needed = (k_pad / 8 + kPrepassThreads - 1) / kPrepassThreads;
+    const dim3 grid(m_pad), block(kPrepassThreads);
+#define KK_X16(P, PER) hipLaunchKernelGGL((x_to_f16<P, PER>), grid, block, 0, stream, x, batch, k, k_pad, x16, row_inv)
+    if (permute) {
+        if (per_needed <= 1) KK_X16(true, 1);
+        else if (per_needed <= 2) KK_X16(true, 2);
+        else if (per_needed <= 4) KK_X16(true, 4);
+        else KK_X16(true, 8);
+    } else {
+        if (per_needed <= 1) KK_X16(false, 1);
+        else if (per_needed <= 2) KK_X16(false, 2);
+        else if (per_needed <= 4) KK_X16(false, 4);
+        else KK_X16(false, 8);
+    }
+#undef KK_X16
 }
 
 // ---------------------------------------------------------------------------
@@ -203,6 +230,7 @@ constexpr int kLdsA = kBM * kLdsStride;
 #endif
 constexpr int kStages = KUNLUN_GEMM_STAGES;    // register sets in flight (even)
 constexpr int kKAlign = kStages * kBK;         // k_pad granularity: whole main-loop iterations
+static_assert(16384 % kKAlign == 0, "k <= 16384 keeps k_pad <= 16384, within x_to_f16<., 8>");
 static_assert(kStages % 2 == 0, "LDS buffer parity follows the register set index");
 
 template <int BN>
@@ -957,12 +985,7 @@ extern "C" int kk_gemm(int type, const void *w, const float *x, float *y, int k,
     char *ws = static_cast<char *>(workspace);
     _Float16 *x16 = reinterpret_cast<_Float16 *>(ws);
     float *row_inv = reinterpret_cast<float *>(ws + p.x16_bytes);
-    if (type == 2)
-        hipLaunchKernelGGL(x_to_f16<true>, dim3(p.m_pad), dim3(kPrepassThreads), 0, stream, x, batch, k, p.k_pad, x16,
-                           row_inv);
-    else
-        hipLaunchKernelGGL(x_to_f16<false>, dim3(p.m_pad), dim3(kPrepassThreads), 0, stream, x, batch, k, p.k_pad, x16,
-                           row_inv);
+    launch_x_to_f16(type == 2, x, batch, k, p.m_pad, p.k_pad, x16, row_inv, stream);
     hipError_t rc = hipGetLastError();
     if (rc != hipSuccess) return rc;
     const size_t w_bytes = type == 1 ? static_cast<size_t>(n) * k * 2 : static_cast<size_t>(n) * (k / 32) * 18;
@@ -989,12 +1012,7 @@ extern "C" int kk_gemm_swiglu(int type, const void *w_gate, const void *w_up, co
     char *ws = static_cast<char *>(workspace);
     _Float16 *x16 = reinterpret_cast<_Float16 *>(ws);
     float *row_inv = reinterpret_cast<float *>(ws + p.x16_bytes);
-    if (type == 2)
-        hipLaunchKernelGGL(x_to_f16<true>, dim3(p.m_pad), dim3(kPrepassThreads), 0, stream, x, batch, k, p.k_pad, x16,
-                           row_inv);
-    else
-        hipLaunchKernelGGL(x_to_f16<false>, dim3(p.m_pad), dim3(kPrepassThreads), 0, stream, x, batch, k, p.k_pad, x16,
-                           row_inv);
+    launch_x_to_f16(type == 2, x, batch, k, p.m_pad, p.k_pad, x16, row_inv, stream);
     hipError_t rc = hipGetLastError();
     if (rc != hipSuccess) return rc;
     const size_t w_bytes = type == 1 ? static_cast<size_t>(n) * k * 2 : static_cast<size_t>(n) * (k / 32) * 18;
