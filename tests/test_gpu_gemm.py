@@ -25,8 +25,10 @@ def check_gemm(y, gold, w_dec, x, tol=2e-3):
     return bool(np.all(np.isfinite(y))), bool(np.all(err <= bound + 1e-30)), float(rel)
 
 
+# K up to 1024, 4096, 6144 and 16384: the activation prepass's 1, 2, 4 and 8
+# groups of 8 values per thread
 SHAPES = [(4096, 4096, 512), (4096, 11008, 512), (256, 65, 64), (96, 17, 70), (512, 300, 130),
-          (16384, 64, 64), (1024, 129, 200), (384, 200, 96)]
+          (16384, 64, 64), (1024, 129, 200), (384, 200, 96), (6144, 80, 66)]
 
 
 @pytest.mark.parametrize("type_", [kl.WeightType.q4_0, kl.WeightType.f16], ids=["q4_0", "f16"])
