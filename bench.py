@@ -10,7 +10,9 @@ rotate so the 256 MB Infinity Cache cannot hold the weights.
 
 value = algorithmic bytes of a step / step time, bytes per GEMV =
 n*(k/32)*18 + 4*b*k + 4*b*n. Timing uses HIP events recorded on the library's
-own stream around K steps (after W warm-up steps). roofline: the dominant
+own stream around K steps (after 200 ms of untimed steps and W warm-up
+steps). copy_ceiling: the runtime's device-to-device copy moving the gate and
+LM-head GEMVs' bytes, a ceiling reference at their size. roofline: the dominant
 kernel, the K4096xN11008 GEMV, timed alone the same way. cpu_baseline: the
 reference's CPU oracle (bench/native-q4-reference.h, FP64, 6 OpenMP threads)
 on the K4096xN11008 GEMV, repeated for about --cpu-seconds.
