@@ -193,7 +193,7 @@ size_t kunlun_matmul_count(int device);
  * time work with HIP events record them on this stream. */
 void *kunlun_stream(int device);
 /* Name of the kernel route the last matmul on `kernel` took (for tests and
- * profiling, e.g. "q4_gemv_pair"); NULL before the first call. */
+ * profiling, e.g. "q4_gemv_dot8"); NULL before the first call. */
 const char *kunlun_kernel_route(const kunlun_kernel *kernel);
 /* matmul_swiglu(): Y[batch,n] = SiLU(X W_gate^T) * (X W_up^T) for two [n,k]
  * weights of one type (KUNLUN_F32, KUNLUN_F16, KUNLUN_Q4_0), with matmul()'s
@@ -203,6 +203,17 @@ const char *kunlun_kernel_route(const kunlun_kernel *kernel);
  * Submits; kunlun_select(device) + kunlun_wait() completes it. */
 void kunlun_matmul_swiglu(kunlun_kernel *kernel, int device, void *y, const void *w_gate, const void *w_up,
                           const void *x, int k, int n, int batch, int type);
+/* Route and tile knobs of matmul. Each knob is named by its environment
+ * variable (KUNLUN_GEMM_MIN_BATCH, KUNLUN_Q4_MFMA_MIN, KUNLUN_Q4_MFMA_MAX,
+ * KUNLUN_DENSE_MFMA_MIN, KUNLUN_DENSE_MFMA_MAX, KUNLUN_GEMM_TILE (BMxWN),
+ * KUNLUN_GEMM_BN, KUNLUN_GEMV_GENERAL, KUNLUN_I8_FUSED_QUANT_LIMIT), which
+ * the library reads once, at the first matmul. kunlun_set_tuning sets a knob
+ * from text in the variable's syntax; a NULL value restores the value read
+ * from the environment. Returns 0, or -1 for an unknown name or a malformed
+ * value. kunlun_get_tuning returns the current value (-1: unset, the
+ * built-in choice) or -2 for an unknown name. */
+int kunlun_set_tuning(const char *name, const char *value);
+int kunlun_get_tuning(const char *name);
 
 #ifdef __cplusplus
 }

@@ -62,6 +62,8 @@ C_FUNCTIONS = [
     ("kunlun_matmul_count", _c_size, [_c_int]),
     ("kunlun_stream", _c_void_p, [_c_int]),
     ("kunlun_kernel_route", ctypes.c_char_p, [_c_void_p]),
+    ("kunlun_set_tuning", _c_int, [ctypes.c_char_p, ctypes.c_char_p]),
+    ("kunlun_get_tuning", _c_int, [ctypes.c_char_p]),
     ("kunlun_elementwise", None, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
                                   _c_int, ctypes.c_float]),
     ("kunlun_swiglu_reason", ctypes.c_char_p, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
@@ -628,6 +630,39 @@ def version() -> str:
 
 def matmul_count(device: int) -> int:
     return load().kunlun_matmul_count(int(device))
+
+
+def set_tuning(name: str, value) -> None:
+    """Sets a route/tile knob (named by its environment variable) from text in the
+    variable's syntax; None restores the value the library read from the environment."""
+    raw = None if value is None else str(value).encode()
+    if load().kunlun_set_tuning(name.encode(), raw) != 0:
+        raise ValueError(f"set_tuning: unknown knob or malformed value: {name}={value!r}")
+
+
+def get_tuning(name: str) -> int:
+    """Current value of a knob (-1: unset, the built-in choice)."""
+    v = load().kunlun_get_tuning(name.encode())
+    if v == -2:
+        raise ValueError(f"get_tuning: unknown knob {name}")
+    return v
+
+
+class tuning:
+    """Context manager: knobs set for the duration of a block, then restored."""
+
+    def __init__(self, **knobs):
+        self.knobs = knobs
+
+    def __enter__(self):
+        for name, value in self.knobs.items():
+            set_tuning(name, value)
+        return self
+
+    def __exit__(self, *exc):
+        for name in self.knobs:
+            set_tuning(name, None)
+        return False
 
 
 def stream(device: int) -> int:

@@ -86,17 +86,23 @@ __device__ __forceinline__ u32x4_a4 load_u32x4(const uint32_t *p) {
 }
 
 // Eight activations as signed fixed point X_t = rint(v[t] * to_fixed) (round
-// to nearest even via the 1.5 * 2^23 magic constant, one FMA; |X_t| <= 2^22
-// when every |v[t]| < 2^e and to_fixed = 2^(22-e)), written as six balanced
-// base-16 digits in [-8, 7]: Z = (X + 0x888888) ^ 0x888888 holds them as 4-bit
-// two's-complement nibbles (as_uint(fma) - 0x4b400000 + 0x888888 ==
-// as_uint(fma) + 0xb5488888). Digit dword l holds digit l of X_t in nibble t,
-// so for signed nibbles w_t: sum_t w_t X_t = sum_l 16^l sdot8(w, dig[l]).
-__device__ __forceinline__ void fixed_point_digits(const float (&v)[8], float to_fixed, uint32_t (&dig)[6]) {
+// to nearest even via the 1.5 * 2^23 magic constant, one FMA), written as
+// DIGITS balanced base-16 digits in [-8, 7]. With FRAC = 4 * DIGITS - 2,
+// to_fixed = 2^(FRAC-e) and every |v[t]| < 2^e, |X_t| <= 2^FRAC, and
+// Z = (X + 0x88..8) ^ 0x88..8 (DIGITS eights) holds the digits directly as
+// 4-bit two's-complement nibbles; the nibbles above DIGITS are zero
+// (as_uint(fma) - 0x4b400000 + 0x88..8 in one add). Digit dword l holds digit
+// l of X_t in nibble t, so for signed nibbles w_t:
+//   sum_t w_t X_t = sum_l 16^l sdot8(w, dig[l]).
+template <int DIGITS = 6>
+__device__ __forceinline__ void fixed_point_digits(const float (&v)[8], float to_fixed, uint32_t (&dig)[DIGITS]) {
+    static_assert(DIGITS == 5 || DIGITS == 6, "5 or 6 digits (19- or 23-bit fixed point)");
+    constexpr uint32_t kEights = DIGITS == 6 ? 0x888888u : 0x88888u;
+    constexpr uint32_t kAdd = kEights - 0x4b400000u;   // mod 2^32
     uint32_t z[8];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) z[t] = (__float_as_uint(fmaf(v[t], to_fixed, 12582912.0f)) + 0xb5488888u) ^ 0x888888u;
-    // 8 x 6 nibble transpose. E[s] byte c = (z[2s].n(2c), z[2s+1].n(2c)),
+    for (int t = 0; t < 8; ++t) z[t] = (__float_as_uint(fmaf(v[t], to_fixed, 12582912.0f)) + kAdd) ^ kEights;
+    // 8 x DIGITS nibble transpose. E[s] byte c = (z[2s].n(2c), z[2s+1].n(2c)),
     // O[s] byte c = (.. n(2c+1) ..); v_perm_b32(hi, lo, sel): selector byte
     // 0-3 picks a lo byte, 4-7 a hi byte, 0x0c gives 0.
     uint32_t ev[4], od[4];
@@ -114,7 +120,8 @@ __device__ __forceinline__ void fixed_point_digits(const float (&v)[8], float to
     const uint32_t o23 = __builtin_amdgcn_perm(od[3], od[2], 0x05010400u);
     dig[1] = __builtin_amdgcn_perm(o23, o01, 0x05040100u);
     dig[3] = __builtin_amdgcn_perm(o23, o01, 0x07060302u);
-    dig[5] = __builtin_amdgcn_perm(od[1], od[0], 0x0c0c0602u) | __builtin_amdgcn_perm(od[3], od[2], 0x06020c0cu);
+    if constexpr (DIGITS == 6)
+        dig[DIGITS - 1] = __builtin_amdgcn_perm(od[1], od[0], 0x0c0c0602u) | __builtin_amdgcn_perm(od[3], od[2], 0x06020c0cu);
 }
 
 // SiLU(g) * u in F32 with the reference's non-finite rules (reference

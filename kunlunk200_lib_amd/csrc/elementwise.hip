@@ -12,8 +12,9 @@ namespace {
 
 constexpr int kThreads = 256;
 
-// op: 0 add, 1 multiply, 2 silu, 4 scale (element e of b is b[e % b_count])
-__global__ __launch_bounds__(kThreads) void elementwise_flat(float *__restrict__ y, const float *a,
+// op: 0 add, 1 multiply, 2 silu, 4 scale (element e of b is b[e % b_count]).
+// y may alias a or b: element e is read before it is written, by the same lane.
+__global__ __launch_bounds__(kThreads) void elementwise_flat(float *y, const float *a,
                                                             const float *b, int count, int b_count, int op,
                                                             float parameter) {
     const int step = gridDim.x * kThreads;

@@ -18,6 +18,7 @@
 // product (the fp16-MFMA tolerance of the path is 2e-3 relative).
 #include "device_common.h"
 #include "launch.h"
+#include "tuning.h"
 
 #include <algorithm>
 #include <cstdio>
@@ -834,14 +835,13 @@ struct GemmPlan {
 };
 
 // Tile N: 128 (fewer LDS reads per MFMA) when that still gives every CU a
-// tile, else 64. KUNLUN_GEMM_BN=64|128 overrides.
+// tile, else 64. The kGemmBn knob (KUNLUN_GEMM_BN=64|128) overrides.
 GemmPlan plan(int k, int n, int batch) {
     GemmPlan p;
     p.m_pad = static_cast<int>(round_up(static_cast<size_t>(batch), kBM));
     p.k_pad = static_cast<int>(round_up(static_cast<size_t>(k), kKAlign));
     p.m_tiles = p.m_pad / kBM;
-    const char *forced = std::getenv("KUNLUN_GEMM_BN");
-    const int want = forced && *forced ? std::atoi(forced) : 0;
+    const int want = kk::tuning(kk::kGemmBn);
     p.bn = want == 64 || want == 128 ? want : (p.m_tiles * ((n + 127) / 128) >= 256 ? 128 : 64);
     p.n_tiles = (n + p.bn - 1) / p.bn;
     p.x16_bytes = round_up(static_cast<size_t>(p.m_pad) * p.k_pad * 2, 256);
@@ -893,18 +893,15 @@ struct QlTile {
 
 // The candidate with the smallest estimated time: whole rounds of tiles over
 // the CUs x tile work, with penalties for the LDS activation reads per MFMA
-// (~1/WN) and the weight decode per MFMA (~1/BM). KUNLUN_GEMM_TILE=BMxWN
-// (e.g. 128x48) forces a candidate.
+// (~1/WN) and the weight decode per MFMA (~1/BM). The kGemmTile knob
+// (KUNLUN_GEMM_TILE=BMxWN, e.g. 128x48) forces a candidate.
 QlTile pick_ql_tile(int batch, int n, bool pair) {
     static const QlTile kAll[] = {{128, 48}, {128, 32}, {64, 64}, {64, 32}};
     auto allowed = [pair](const QlTile &t) { return !pair || t.wn % 32 == 0; };
-    const char *forced = std::getenv("KUNLUN_GEMM_TILE");
-    if (forced && *forced) {
-        int bm = 0, wn = 0;
-        if (std::sscanf(forced, "%dx%d", &bm, &wn) == 2)
-            for (const QlTile &t : kAll)
-                if (t.bm == bm && t.wn == wn && allowed(t)) return t;
-    }
+    const int forced = kk::tuning(kk::kGemmTile);
+    if (forced > 0)
+        for (const QlTile &t : kAll)
+            if (t.bm * 1000 + t.wn == forced && allowed(t)) return t;
     const long cus = device_cus();
     QlTile pick = {128, 32};
     double best = 0.0;

@@ -8,16 +8,15 @@
 // are decoded exactly (the decoded value (q-8)*d is exact in F32).
 //
 // Kernels:
-//   q4_gemv_pair  Q4_0, K % 64 == 0, 4-byte aligned rows. A lane owns a pair
-//                 of adjacent blocks (36 bytes = 9 dwords, 64 weights) of each
-//                 row, loaded with dword-aligned 16+16+4 byte loads; the
-//                 first block's nibbles are re-aligned with v_alignbyte.
+//   q4_gemv_dot8  Q4_0, K % 64 == 0, 4-byte aligned rows: exact integer block
+//                 sums of nibbles and fixed-point activation digits (v_dot8).
 //   dense_gemv    F32 / F16, 16-byte aligned rows. A lane owns 16-byte chunks
 //                 spaced 1 KiB apart so every load instruction is coalesced.
 //   gemv_general  any format, alignment and K % 32: byte loads, one wave per
 //                 row. Correct for every input the API accepts; slow.
 #include "device_common.h"
 #include "launch.h"
+#include "tuning.h"
 
 #include <algorithm>
 #include <cstdlib>
@@ -30,327 +29,42 @@ constexpr int kThreads = 256;          // 4 waves per workgroup
 constexpr int kWavesPerGroup = kThreads / kWave;
 
 // ---------------------------------------------------------------------------
-// Q4_0, pair-of-blocks lanes.
-//
-// LDS holds X for the batch chunk as float4 in [b][h][q][p] order, where
-// block = 2p + h and q is the float4 slot (0..7) inside the 32-value block,
-// so lanes (consecutive p) read consecutive float4: conflict-free. It also
-// holds xsum[b][h][p], the sum of the block's 32 activations, used to apply
-// the -8 nibble offset once per block: sum((q-8) x) = sum(q x) - 8 sum(x).
-template <int B, int U>
-__global__ __launch_bounds__(kThreads) void q4_gemv_pair(const uint8_t *__restrict__ w,
-                                                        const float *__restrict__ x,
-                                                        float *__restrict__ y, int k, int n,
-                                                        int y_stride) {
-    extern __shared__ float4 lds[];
-    const int blocks = k >> 5;
-    const int pairs = blocks >> 1;
-    const size_t row_bytes = static_cast<size_t>(blocks) * 18;
-    float4 *xl = lds;
-    float *xs = reinterpret_cast<float *>(lds + static_cast<size_t>(B) * 8 * blocks);
-
-    for (int idx = threadIdx.x; idx < B * blocks; idx += kThreads) {
-        const int b = idx / blocks, blk = idx - b * blocks;
-        const int p = blk >> 1, h = blk & 1;
-        const float4 *src = reinterpret_cast<const float4 *>(x + static_cast<size_t>(b) * k + blk * 32);
-        float s = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const float4 v = src[q];
-            xl[((b * 2 + h) * 8 + q) * pairs + p] = v;
-            s += (v.x + v.y) + (v.z + v.w);
-        }
-        xs[(b * 2 + h) * pairs + p] = s;
-    }
-    __syncthreads();
-
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = blockIdx.x * kWavesPerGroup + (threadIdx.x >> 6);
-    const int waves = gridDim.x * kWavesPerGroup;
-    const int rowblocks = (n + U - 1) / U;
-
-    for (int rb = wave; rb < rowblocks; rb += waves) {
-        const int r0 = rb * U;
-        float acc[U][B];
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int b = 0; b < B; ++b) acc[u][b] = 0.0f;
-
-        for (int p = lane; p < pairs; p += kWave) {
-            uint32_t wd[U][9];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int r = min(r0 + u, n - 1);
-                const uint32_t *src = reinterpret_cast<const uint32_t *>(
-                    w + static_cast<size_t>(r) * row_bytes + static_cast<size_t>(p) * 36);
-                const kk::u32x4_a4 a = kk::load_u32x4(src);
-                const kk::u32x4_a4 c = kk::load_u32x4(src + 4);
-                wd[u][0] = a.x; wd[u][1] = a.y; wd[u][2] = a.z; wd[u][3] = a.w;
-                wd[u][4] = c.x; wd[u][5] = c.y; wd[u][6] = c.z; wd[u][7] = c.w;
-                wd[u][8] = src[8];
-            }
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                float xv[B][32];
-                float xsum[B];
-#pragma unroll
-                for (int b = 0; b < B; ++b) {
-#pragma unroll
-                    for (int q = 0; q < 8; ++q) {
-                        const float4 v = xl[((b * 2 + h) * 8 + q) * pairs + p];
-                        xv[b][4 * q + 0] = v.x; xv[b][4 * q + 1] = v.y;
-                        xv[b][4 * q + 2] = v.z; xv[b][4 * q + 3] = v.w;
-                    }
-                    xsum[b] = xs[(b * 2 + h) * pairs + p];
-                }
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    uint32_t nib[4];
-                    float d;
-                    if (h == 0) {
-                        // bytes 0-1 scale, bytes 2-17 nibbles: shift by 2 bytes
-                        d = kk::half_bits_to_float(wd[u][0] & 0xffffu);
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) nib[i] = kk::align_bytes(wd[u][i + 1], wd[u][i], 2);
-                    } else {
-                        // bytes 18-19 scale, bytes 20-35 nibbles: dword aligned
-                        d = kk::half_bits_to_float(wd[u][4] >> 16);
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) nib[i] = wd[u][5 + i];
-                    }
-#pragma unroll
-                    for (int b = 0; b < B; ++b) {
-                        float s_lo = 0.0f, s_hi = 0.0f;
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const uint32_t lo = nib[i] & 0x0f0f0f0fu;   // values 4i..4i+3
-                            const uint32_t hi = nib[i] & 0xf0f0f0f0u;   // 16 * values 16+4i..
-                            s_lo = fmaf(kk::ubyte_to_float<0>(lo), xv[b][4 * i + 0], s_lo);
-                            s_lo = fmaf(kk::ubyte_to_float<1>(lo), xv[b][4 * i + 1], s_lo);
-                            s_lo = fmaf(kk::ubyte_to_float<2>(lo), xv[b][4 * i + 2], s_lo);
-                            s_lo = fmaf(kk::ubyte_to_float<3>(lo), xv[b][4 * i + 3], s_lo);
-                            s_hi = fmaf(kk::ubyte_to_float<0>(hi), xv[b][16 + 4 * i + 0], s_hi);
-                            s_hi = fmaf(kk::ubyte_to_float<1>(hi), xv[b][16 + 4 * i + 1], s_hi);
-                            s_hi = fmaf(kk::ubyte_to_float<2>(hi), xv[b][16 + 4 * i + 2], s_hi);
-                            s_hi = fmaf(kk::ubyte_to_float<3>(hi), xv[b][16 + 4 * i + 3], s_hi);
-                        }
-                        float t = fmaf(s_hi, 0.0625f, s_lo);
-                        t = fmaf(-8.0f, xsum[b], t);
-                        acc[u][b] = fmaf(d, t, acc[u][b]);
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-#pragma unroll
-            for (int b = 0; b < B; ++b) {
-                const float v = kk::wave_sum(acc[u][b]);
-                if (lane == 0 && r0 + u < n) y[static_cast<size_t>(b) * y_stride + r0 + u] = v;
-            }
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Q4_0 streaming variant. Same lane ownership (pair p = lane + 64*j of every
-// row) and LDS activation layout as q4_gemv_pair, organised for HBM streaming:
-//   * every wave owns a balanced contiguous row range [r_begin, r_end);
-//   * work is a flat sequence of (chunk of U rows, pair slice j) items whose
-//     36-byte loads are double buffered: item i+1 is in flight while item i is
-//     decoded;
-//   * the first item's loads are issued right after the activation loads and
-//     before the activations are written to LDS, so the prologue overlaps;
-//   * row sums use DPP row reductions plus four lane reads.
-template <int B, int U, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void q4_gemv_stream(const uint8_t *__restrict__ w,
-                                                            const float *__restrict__ x,
-                                                            float *__restrict__ y, int k, int n, int y_stride) {
-    extern __shared__ float4 lds[];
-    constexpr int kGroupThreads = 64 * WAVES;
-    const int blocks = k >> 5;
-    const int pairs = blocks >> 1;
-    const int slices = (pairs + kWave - 1) / kWave;
-    const size_t row_bytes = static_cast<size_t>(blocks) * 18;
-    float4 *xl = lds;
-    float *xs = reinterpret_cast<float *>(lds + static_cast<size_t>(B) * 8 * blocks);
-
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = blockIdx.x * WAVES + (threadIdx.x >> 6);
-    const int waves = gridDim.x * WAVES;
-    const int r_begin = static_cast<int>(static_cast<long long>(n) * wave / waves);
-    const int r_end = static_cast<int>(static_cast<long long>(n) * (wave + 1) / waves);
-    const int chunks = (r_end - r_begin + U - 1) / U;
-    const int items = chunks * slices;
-
-    auto load_item = [&](int item, uint32_t (&buf)[U][9]) {
-        const int c = item / slices, j = item - c * slices;
-        const int p = lane + kWave * j;
-        const int r0 = r_begin + c * U;
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int r = min(r0 + u, r_end - 1);
-            if (p < pairs) {
-                const uint32_t *src = reinterpret_cast<const uint32_t *>(
-                    w + static_cast<size_t>(r) * row_bytes + static_cast<size_t>(p) * 36);
-                const kk::u32x4_a4 a = kk::load_u32x4(src);
-                const kk::u32x4_a4 b = kk::load_u32x4(src + 4);
-                buf[u][0] = a.x; buf[u][1] = a.y; buf[u][2] = a.z; buf[u][3] = a.w;
-                buf[u][4] = b.x; buf[u][5] = b.y; buf[u][6] = b.z; buf[u][7] = b.w;
-                buf[u][8] = src[8];
-            } else {
-#pragma unroll
-                for (int i = 0; i < 9; ++i) buf[u][i] = 0u;   // zero scale: contributes 0
-            }
-        }
-    };
-
-    // Activation loads first, then the first weight item, then the LDS writes:
-    // the weight loads stay in flight across the staging barrier.
-    constexpr int kStageMax = 1;   // blocks staged per thread per pass
-    uint32_t wa[U][9], wb[U][9];
-    for (int base = 0; base < B * blocks; base += kGroupThreads * kStageMax) {
-        float4 v[kStageMax][8];
-#pragma unroll
-        for (int s = 0; s < kStageMax; ++s) {
-            const int idx = base + s * kGroupThreads + threadIdx.x;
-            if (idx < B * blocks) {
-                const int b = idx / blocks, blk = idx - b * blocks;
-                const float4 *src = reinterpret_cast<const float4 *>(x + static_cast<size_t>(b) * k + blk * 32);
-#pragma unroll
-                for (int q = 0; q < 8; ++q) v[s][q] = src[q];
-            }
-        }
-        if (base == 0 && items > 0) load_item(0, wa);
-#pragma unroll
-        for (int s = 0; s < kStageMax; ++s) {
-            const int idx = base + s * kGroupThreads + threadIdx.x;
-            if (idx < B * blocks) {
-                const int b = idx / blocks, blk = idx - b * blocks;
-                const int p = blk >> 1, h = blk & 1;
-                float sum = 0.0f;
-#pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    xl[((b * 2 + h) * 8 + q) * pairs + p] = v[s][q];
-                    sum += (v[s][q].x + v[s][q].y) + (v[s][q].z + v[s][q].w);
-                }
-                xs[(b * 2 + h) * pairs + p] = sum;
-            }
-        }
-    }
-    __syncthreads();
-
-    float acc[U][B];
-    auto compute_item = [&](int item, const uint32_t (&buf)[U][9]) {
-        const int c = item / slices, j = item - c * slices;
-        if (j == 0) {
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-#pragma unroll
-                for (int b = 0; b < B; ++b) acc[u][b] = 0.0f;
-        }
-        const int p = min(lane + kWave * j, pairs - 1);   // idle lanes read a valid slot, add 0
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            float xv[B][32];
-            float xsum[B];
-#pragma unroll
-            for (int b = 0; b < B; ++b) {
-#pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    const float4 v = xl[((b * 2 + h) * 8 + q) * pairs + p];
-                    xv[b][4 * q + 0] = v.x; xv[b][4 * q + 1] = v.y;
-                    xv[b][4 * q + 2] = v.z; xv[b][4 * q + 3] = v.w;
-                }
-                xsum[b] = xs[(b * 2 + h) * pairs + p];
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                uint32_t nib[4];
-                float d;
-                if (h == 0) {
-                    d = kk::half_bits_to_float(buf[u][0] & 0xffffu);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) nib[i] = kk::align_bytes(buf[u][i + 1], buf[u][i], 2);
-                } else {
-                    d = kk::half_bits_to_float(buf[u][4] >> 16);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) nib[i] = buf[u][5 + i];
-                }
-#pragma unroll
-                for (int b = 0; b < B; ++b) {
-                    float s_lo = 0.0f, s_hi = 0.0f;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const uint32_t lo = nib[i] & 0x0f0f0f0fu;
-                        const uint32_t hi = nib[i] & 0xf0f0f0f0u;
-                        s_lo = fmaf(kk::ubyte_to_float<0>(lo), xv[b][4 * i + 0], s_lo);
-                        s_lo = fmaf(kk::ubyte_to_float<1>(lo), xv[b][4 * i + 1], s_lo);
-                        s_lo = fmaf(kk::ubyte_to_float<2>(lo), xv[b][4 * i + 2], s_lo);
-                        s_lo = fmaf(kk::ubyte_to_float<3>(lo), xv[b][4 * i + 3], s_lo);
-                        s_hi = fmaf(kk::ubyte_to_float<0>(hi), xv[b][16 + 4 * i + 0], s_hi);
-                        s_hi = fmaf(kk::ubyte_to_float<1>(hi), xv[b][16 + 4 * i + 1], s_hi);
-                        s_hi = fmaf(kk::ubyte_to_float<2>(hi), xv[b][16 + 4 * i + 2], s_hi);
-                        s_hi = fmaf(kk::ubyte_to_float<3>(hi), xv[b][16 + 4 * i + 3], s_hi);
-                    }
-                    float t = fmaf(s_hi, 0.0625f, s_lo);
-                    t = fmaf(-8.0f, xsum[b], t);
-                    acc[u][b] = fmaf(d, t, acc[u][b]);
-                }
-            }
-        }
-        if (j == slices - 1) {
-            const int r0 = r_begin + c * U;
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-#pragma unroll
-                for (int b = 0; b < B; ++b) {
-                    const float v = kk::wave_sum_uniform(acc[u][b]);
-                    if (lane == 0 && r0 + u < r_end) y[static_cast<size_t>(b) * y_stride + r0 + u] = v;
-                }
-            }
-        }
-    };
-
-    for (int item = 0; item < items; item += 2) {
-        if (item + 1 < items) load_item(item + 1, wb);
-        compute_item(item, wa);
-        if (item + 2 < items) load_item(item + 2, wa);
-        if (item + 1 < items) compute_item(item + 1, wb);
-    }
-}
-
-// ---------------------------------------------------------------------------
 // Q4_0 with integer block dot products (v_dot8_i32_i4).
 //
-// Each 32-value activation block is represented as X_j = rint(x_j * 2^(22-e)),
-// where 2^e > max|x| of the block (frexp exponent), i.e. a 23-bit signed
-// fixed-point value with block scale s = 2^(e-22); |x_j - s X_j| <= s/2 <=
-// max|x|*2^-22. X_j is written in six balanced base-16 digits in [-8, 7]:
-// Z = (X + 0x888888) ^ 0x888888 holds them directly as 4-bit two's-complement
-// nibbles. A weight nibble q becomes the signed value q - 8 by q ^ 8. Then
+// Each 32-value activation block is represented as X_j = rint(x_j * 2^(F-e)),
+// where 2^e > max|x| of the block (frexp exponent) and F = 4 * DIGITS - 2,
+// i.e. an (F+1)-bit signed fixed-point value with block scale s = 2^(e-F);
+// |x_j - s X_j| <= s/2 <= max|x| * 2^-F. X_j is written in DIGITS balanced
+// base-16 digits in [-8, 7] (kk::fixed_point_digits). A weight nibble q
+// becomes the signed value q - 8 by q ^ 8. Then
 //   S = sum_j (q_j - 8) X_j = sum_l 16^l sum_j (q_j - 8) digit_l(X_j)
-// is computed exactly in int32 (|S| <= 32*8*2^22 = 2^30) with 24 v_dot8
-// (8 products each) per block and row, accumulated from the top digit down
-// (Horner), and y += float(S) * (d * s). About 1.2 VALU ops per weight,
-// against about 2.4 for the F32 decode of q4_gemv_stream.
+// is computed exactly in int32 (|S| <= 32*8*2^F <= 2^30) with 4 * DIGITS
+// v_dot8 (8 products each) per block and row, accumulated from the top digit
+// down (Horner), and y += float(S) * (d * s).
+// Error: per element |e_j| <= m_b 2^-F with m_b the block's max |x| (2^(e-1)
+// <= m_b), so |sum_j w_j e_j| <= ||w|| ||e|| <= 2^-F sqrt(32) ||x|| ||w||:
+// 2.2e-5 ||x|| ||w|| for DIGITS = 5 (F = 18), 1.4e-6 for DIGITS = 6 (F = 22),
+// inside the 1e-4 ||x|| ||w|| bound of the F32-accumulate GEMV either way.
 //
 // Digit dwords are packed in the weight nibble order: dword i of a block's 16
 // nibble bytes holds values (4i, 16+4i, 4i+1, 16+4i+1, ..., 4i+3, 16+4i+3) in
 // nibbles 0..7, so digit dword D[i][l] holds digit l of the same values.
-// LDS layout per batch column b and block half h of pair p: six uint4 groups
-// of the 24 dwords (i*6 + l), stored [b][h][group][p] (lanes read
-// consecutive uint4: conflict-free), then the block scales [b][h][p].
-// A non-finite activation makes its block scale NaN: every output row of that
-// batch column becomes NaN.
+// LDS layout per batch column b and block half h of pair p: DIGITS uint4
+// groups of the 4 * DIGITS dwords (i * DIGITS + l), stored [b][h][group][p]
+// (lanes read consecutive uint4: conflict-free), then the block scales
+// [b][h][p]. A non-finite activation makes its block scale NaN: every output
+// row of that batch column becomes NaN.
 // Every global load is branch-free (clamped addresses, inactive lanes zero
 // their block scale) and the loop issues no vector stores (row results are
 // parked in LDS and written once, coalesced, at the end), so the waitcnt
-// counters stay exact and DEPTH items remain in flight while one is decoded.
-// All activation loads are issued before the first weight items (the memory
-// counter is in order), then converted while those weights are in flight.
+// counters stay exact. A wave issues its first DEPTH items at entry; when it
+// owns at most DEPTH items, all of its weight bytes are requested before its
+// first wait and no refill loads follow. All activation loads are issued
+// before the first weight items (the memory counter is in order), then
+// converted while those weights are in flight.
 constexpr int kDot8MaxRowsPerWave = 64;
+
+constexpr int dot8_block_lds_bytes(int digits) { return 16 * digits + 4; }
 
 // PASSES = activation staging passes: B * (K/32) * 4 <= PASSES * 64 * WAVES.
 // SLICES = ceil(K / 4096): 64-pair slices per row. Rows are split over the
@@ -358,7 +72,7 @@ constexpr int kDot8MaxRowsPerWave = 64;
 // PAIR (U = 2): an item is output row r of both the gate matrix w and the up
 // matrix w2, and the row result is SiLU(gate) * up (the swiglu kernel's
 // element function), so the pair reads X once and needs no second pass.
-template <int B, int U, int WAVES, int SLICES, int DEPTH, int PASSES, bool PAIR = false>
+template <int B, int U, int WAVES, int SLICES, int DEPTH, int PASSES, bool PAIR, int DIGITS>
 __global__ __launch_bounds__(64 * WAVES) void q4_gemv_dot8(const uint8_t *__restrict__ w,
                                                           const uint8_t *__restrict__ w2,
                                                           const float *__restrict__ x,
@@ -367,13 +81,14 @@ __global__ __launch_bounds__(64 * WAVES) void q4_gemv_dot8(const uint8_t *__rest
     extern __shared__ uint4 lds4[];
     constexpr int kGroupThreads = 64 * WAVES;
     constexpr bool ONE_SLICE = SLICES == 1;
+    constexpr int kFrac = 4 * DIGITS - 2;
     const int blocks = k >> 5;
     const int pairs = blocks >> 1;
     constexpr int slices = SLICES;
     const size_t row_bytes = static_cast<size_t>(blocks) * 18;
-    uint4 *digits = lds4;                                                                   // [B][2][6][pairs]
-    float *scales = reinterpret_cast<float *>(lds4 + static_cast<size_t>(B) * 12 * pairs);  // [B][2][pairs]
-    float *results = scales + static_cast<size_t>(B) * 2 * pairs;                           // [WAVES][B][64]
+    uint4 *digits = lds4;                                                                        // [B][2][DIGITS][pairs]
+    float *scales = reinterpret_cast<float *>(lds4 + static_cast<size_t>(B) * 2 * DIGITS * pairs);  // [B][2][pairs]
+    float *results = scales + static_cast<size_t>(B) * 2 * pairs;                                // [WAVES][B][64]
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
@@ -426,7 +141,7 @@ __global__ __launch_bounds__(64 * WAVES) void q4_gemv_dot8(const uint8_t *__rest
         load_item(d, ring[d]);
         __builtin_amdgcn_sched_barrier(0);   // item d's loads are issued before item d+1's
     }
-    // 3. activations -> block scale and six signed base-16 digit dwords
+    // 3. activations -> block scale and DIGITS signed base-16 digit dwords
 #pragma unroll
     for (int pass = 0; pass < PASSES; ++pass) {
         const int idx = pass * kGroupThreads + static_cast<int>(threadIdx.x);
@@ -445,10 +160,10 @@ __global__ __launch_bounds__(64 * WAVES) void q4_gemv_dot8(const uint8_t *__rest
         bad = fmaxf(bad, kk::dpp_move<0xb1>(bad));
         bad = fmaxf(bad, kk::dpp_move<0x4e>(bad));
         // 2^(e-1) <= m < 2^e (e = 0 for m == 0); e is kept >= -100 so that
-        // 2^(22-e) stays finite (blocks below 2^-100 lose relative precision only).
+        // 2^(F-e) stays finite (blocks below 2^-100 lose relative precision only).
         const int e = max(__builtin_amdgcn_frexp_expf(m), -100);
-        uint32_t dig[6];
-        kk::fixed_point_digits(v, ldexpf(1.0f, 22 - e), dig);
+        uint32_t dig[DIGITS];
+        kk::fixed_point_digits<DIGITS>(v, ldexpf(1.0f, kFrac - e), dig);
         if (idx < groups) {
             const int b = (B > 1 && idx >= blocks * 4) ? 1 : 0;
             const int rem = idx - b * blocks * 4;
@@ -456,19 +171,19 @@ __global__ __launch_bounds__(64 * WAVES) void q4_gemv_dot8(const uint8_t *__rest
             const int p = blk >> 1, h = blk & 1;
             uint32_t *dst = reinterpret_cast<uint32_t *>(digits);
 #pragma unroll
-            for (int l = 0; l < 6; ++l) {
-                const int pos = i * 6 + l;
-                dst[((static_cast<size_t>(b * 2 + h) * 6 + (pos >> 2)) * pairs + p) * 4 + (pos & 3)] = dig[l];
+            for (int l = 0; l < DIGITS; ++l) {
+                const int pos = i * DIGITS + l;
+                dst[((static_cast<size_t>(b * 2 + h) * DIGITS + (pos >> 2)) * pairs + p) * 4 + (pos & 3)] = dig[l];
             }
             if (i == 0)
-                scales[(b * 2 + h) * pairs + p] = bad != 0.0f ? __builtin_nanf("") : ldexpf(1.0f, e - 22);
+                scales[(b * 2 + h) * pairs + p] = bad != 0.0f ? __builtin_nanf("") : ldexpf(1.0f, e - kFrac);
         }
     }
     __syncthreads();
 
     // 4. decode: one item = U rows x one 64-pair slice
     float acc[U][B];
-    uint4 dg[B][2][6];
+    uint4 dg[B][2][DIGITS];
     float sc[B][2];
     auto read_slice = [&](int p) {
 #pragma unroll
@@ -476,7 +191,8 @@ __global__ __launch_bounds__(64 * WAVES) void q4_gemv_dot8(const uint8_t *__rest
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
 #pragma unroll
-                for (int g = 0; g < 6; ++g) dg[b][h][g] = digits[(static_cast<size_t>(b * 2 + h) * 6 + g) * pairs + p];
+                for (int g = 0; g < DIGITS; ++g)
+                    dg[b][h][g] = digits[(static_cast<size_t>(b * 2 + h) * DIGITS + g) * pairs + p];
                 sc[b][h] = scales[(b * 2 + h) * pairs + p];
             }
     };
@@ -511,23 +227,27 @@ __global__ __launch_bounds__(64 * WAVES) void q4_gemv_dot8(const uint8_t *__rest
                 d = live ? d : 0.0f;
 #pragma unroll
                 for (int b = 0; b < B; ++b) {
-                    const uint32_t dd[24] = {
-                        dg[b][h][0].x, dg[b][h][0].y, dg[b][h][0].z, dg[b][h][0].w, dg[b][h][1].x, dg[b][h][1].y,
-                        dg[b][h][1].z, dg[b][h][1].w, dg[b][h][2].x, dg[b][h][2].y, dg[b][h][2].z, dg[b][h][2].w,
-                        dg[b][h][3].x, dg[b][h][3].y, dg[b][h][3].z, dg[b][h][3].w, dg[b][h][4].x, dg[b][h][4].y,
-                        dg[b][h][4].z, dg[b][h][4].w, dg[b][h][5].x, dg[b][h][5].y, dg[b][h][5].z, dg[b][h][5].w};
-                    // six independent digit sums T_l, then S = sum_l 16^l T_l (|S| <= 2^30)
-                    int t[6];
+                    uint32_t dd[4 * DIGITS];
 #pragma unroll
-                    for (int l = 0; l < 6; ++l) {
+                    for (int g = 0; g < DIGITS; ++g) {
+                        dd[4 * g + 0] = dg[b][h][g].x;
+                        dd[4 * g + 1] = dg[b][h][g].y;
+                        dd[4 * g + 2] = dg[b][h][g].z;
+                        dd[4 * g + 3] = dg[b][h][g].w;
+                    }
+                    // DIGITS independent digit sums T_l, then S = sum_l 16^l T_l (|S| <= 2^30)
+                    int t[DIGITS];
+#pragma unroll
+                    for (int l = 0; l < DIGITS; ++l) {
                         t[l] = 0;
 #pragma unroll
                         for (int i = 0; i < 4; ++i)
-                            t[l] = __builtin_amdgcn_sdot8(static_cast<int>(q[i]), static_cast<int>(dd[i * 6 + l]), t[l], false);
+                            t[l] = __builtin_amdgcn_sdot8(static_cast<int>(q[i]), static_cast<int>(dd[i * DIGITS + l]),
+                                                          t[l], false);
                     }
-                    int s = t[5];
+                    int s = t[DIGITS - 1];
 #pragma unroll
-                    for (int l = 4; l >= 0; --l) s = (s << 4) + t[l];
+                    for (int l = DIGITS - 2; l >= 0; --l) s = (s << 4) + t[l];
                     acc[u][b] = fmaf(static_cast<float>(s), d * sc[b][h], acc[u][b]);
                 }
             }
@@ -554,15 +274,22 @@ __global__ __launch_bounds__(64 * WAVES) void q4_gemv_dot8(const uint8_t *__rest
         }
     };
 
-    // Ring of DEPTH items in flight: after item i is decoded its buffer is
-    // refilled with item i + DEPTH (clamped: past the end it re-reads the
-    // last item, which hits in cache).
-    for (int base = 0; base < items; base += DEPTH) {
+    if (items <= DEPTH) {
+        // every item is already in flight: consume them in issue order
 #pragma unroll
-        for (int d = 0; d < DEPTH; ++d) {
-            const int item = base + d;
-            if (item < items) compute_item(item, ring[d]);
-            load_item(item + DEPTH, ring[d]);
+        for (int d = 0; d < DEPTH; ++d)
+            if (d < items) compute_item(d, ring[d]);
+    } else {
+        // ring of DEPTH items in flight: after item i is decoded its buffer is
+        // refilled with item i + DEPTH (clamped: past the end it re-reads the
+        // last item, which hits in cache)
+        for (int base = 0; base < items; base += DEPTH) {
+#pragma unroll
+            for (int d = 0; d < DEPTH; ++d) {
+                const int item = base + d;
+                if (item < items) compute_item(item, ring[d]);
+                load_item(item + DEPTH, ring[d]);
+            }
         }
     }
 
@@ -740,10 +467,6 @@ DeviceInfo device_info() {
     return info;
 }
 
-int env_int(const char *name, int fallback) {
-    const char *value = std::getenv(name);
-    return value && *value ? std::atoi(value) : fallback;
-}
 
 // Workgroup count for a row-blocked kernel: enough waves for every row block
 // up to `per_cu` waves per CU.
@@ -753,57 +476,32 @@ int groups_for(int rowblocks, int cus, int per_cu_waves) {
     return static_cast<int>(std::max<long long>(1, (waves + kWavesPerGroup - 1) / kWavesPerGroup));
 }
 
-template <int B>
-hipError_t launch_q4_pair(const uint8_t *w, const float *x, float *y, int k, int n, int y_stride,
-                          hipStream_t stream, const DeviceInfo &info) {
-    constexpr int U = 4;
-    const size_t lds = static_cast<size_t>(B) * k * 4 + static_cast<size_t>(B) * (k / 32) * 4;
-    const int rowblocks = (n + U - 1) / U;
-    const int groups = groups_for(rowblocks, info.cus, env_int("KUNLUN_GEMV_WAVES_PER_CU", 8));
-    hipError_t rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&q4_gemv_pair<B, U>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    (void)rc;
-    hipLaunchKernelGGL((q4_gemv_pair<B, U>), dim3(groups), dim3(kThreads), lds, stream, w, x, y, k, n, y_stride);
-    return hipGetLastError();
-}
-
-template <int B, int U, int WAVES>
-hipError_t launch_q4_stream(const uint8_t *w, const float *x, float *y, int k, int n, int y_stride,
-                            hipStream_t stream, const DeviceInfo &info) {
-    const size_t lds = static_cast<size_t>(B) * k * 4 + static_cast<size_t>(B) * (k / 32) * 4;
-    const int per_cu = env_int("KUNLUN_GEMV_WAVES_PER_CU", 16);
-    const long long want = std::min<long long>(n, static_cast<long long>(info.cus) * per_cu);
+// One launch of q4_gemv_dot8 with WAVES waves per workgroup and up to
+// `per_cu` waves per CU (fewer when a wave would own no row).
+template <int B, int SLICES, int DEPTH, bool PAIR, int DIGITS, int WAVES>
+hipError_t launch_q4_dot8_cfg(const uint8_t *w, const uint8_t *w2, const float *x, float *y, int k, int n,
+                              int y_stride, hipStream_t stream, const DeviceInfo &info, int per_cu) {
+    constexpr int kU = PAIR ? 2 : 1;
+    constexpr int kPasses = (B * SLICES * 8 + WAVES - 1) / WAVES;   // B * K/8 staging groups <= B * SLICES * 512
+    const size_t lds = static_cast<size_t>(B) * (k / 32) * dot8_block_lds_bytes(DIGITS) +
+                       static_cast<size_t>(WAVES) * B * kDot8MaxRowsPerWave * 4;
+    long long want = std::min<long long>(n, static_cast<long long>(info.cus) * per_cu);
+    want = std::max<long long>(want, (n + kDot8MaxRowsPerWave - 1) / kDot8MaxRowsPerWave);
     const int groups = static_cast<int>(std::max<long long>(1, (want + WAVES - 1) / WAVES));
-    hipError_t rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&q4_gemv_stream<B, U, WAVES>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    (void)rc;
-    hipLaunchKernelGGL((q4_gemv_stream<B, U, WAVES>), dim3(groups), dim3(64 * WAVES), lds, stream, w, x, y, k, n,
-                       y_stride);
+    const int waves = groups * WAVES;
+    const int rows_base = n / waves, rows_rem = n % waves;
+    if (rows_base + (rows_rem ? 1 : 0) > kDot8MaxRowsPerWave) return hipErrorInvalidValue;
+    auto kernel = &q4_gemv_dot8<B, kU, WAVES, SLICES, DEPTH, kPasses, PAIR, DIGITS>;
+    // B * K <= 16384: at most 512 * 100 + 16 * 2 * 64 * 4 bytes, inside the 64 KiB default
+    hipLaunchKernelGGL(kernel, dim3(groups), dim3(64 * WAVES), lds, stream, w, w2, x, y, k, n, y_stride, rows_base,
+                       rows_rem);
     return hipGetLastError();
 }
 
 template <int B, int SLICES, int DEPTH, bool PAIR = false>
 hipError_t launch_q4_dot8_depth(const uint8_t *w, const uint8_t *w2, const float *x, float *y, int k, int n,
                                 int y_stride, hipStream_t stream, const DeviceInfo &info) {
-    constexpr int kWaves = 8, kU = PAIR ? 2 : 1;
-    constexpr int kPasses = B * SLICES;   // B * K/8 staging groups <= B * SLICES * 512
-    const size_t lds = static_cast<size_t>(B) * (k / 32) * 100 + static_cast<size_t>(kWaves) * B * kDot8MaxRowsPerWave * 4;
-    const int per_cu = env_int("KUNLUN_GEMV_WAVES_PER_CU", 8);
-    long long want = std::min<long long>(n, static_cast<long long>(info.cus) * per_cu);
-    want = std::max<long long>(want, (n + kDot8MaxRowsPerWave - 1) / kDot8MaxRowsPerWave);
-    const int groups = static_cast<int>(std::max<long long>(1, (want + kWaves - 1) / kWaves));
-    const int waves = groups * kWaves;
-    const int rows_base = n / waves, rows_rem = n % waves;
-    auto kernel = &q4_gemv_dot8<B, kU, kWaves, SLICES, DEPTH, kPasses, PAIR>;
-    static bool attribute_set = false;    // per instantiation
-    if (!attribute_set) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  64 * 1024);
-        attribute_set = true;
-    }
-    hipLaunchKernelGGL(kernel, dim3(groups), dim3(64 * kWaves), lds, stream, w, w2, x, y, k, n, y_stride, rows_base,
-                       rows_rem);
-    return hipGetLastError();
+    return launch_q4_dot8_cfg<B, SLICES, DEPTH, PAIR, 6, 8>(w, w2, x, y, k, n, y_stride, stream, info, 8);
 }
 
 template <int B, int SLICES, bool PAIR>
@@ -811,11 +509,8 @@ hipError_t launch_q4_dot8_slices(const uint8_t *w, const uint8_t *w2, const floa
                                  int y_stride, hipStream_t stream, const DeviceInfo &info) {
     // items in flight per wave: 3 single rows at batch 1; 2 when an item is
     // twice the work (two batch columns, or a gate/up row pair)
-    switch (env_int("KUNLUN_Q4_DEPTH", B == 2 || PAIR ? 2 : 3)) {
-    case 2: return launch_q4_dot8_depth<B, SLICES, 2, PAIR>(w, w2, x, y, k, n, y_stride, stream, info);
-    case 4: return launch_q4_dot8_depth<B, SLICES, 4, PAIR>(w, w2, x, y, k, n, y_stride, stream, info);
-    default: return launch_q4_dot8_depth<B, SLICES, 3, PAIR>(w, w2, x, y, k, n, y_stride, stream, info);
-    }
+    if (B == 2 || PAIR) return launch_q4_dot8_depth<B, SLICES, 2, PAIR>(w, w2, x, y, k, n, y_stride, stream, info);
+    return launch_q4_dot8_depth<B, SLICES, 3, PAIR>(w, w2, x, y, k, n, y_stride, stream, info);
 }
 
 // Q4_0 batch chunk of B (1 or 2) columns; B * K <= 16384. PAIR: w is the gate
@@ -839,7 +534,7 @@ hipError_t launch_dense(const uint8_t *w, const float *x, float *y, int k, int n
     constexpr int U = 4;
     const size_t lds = static_cast<size_t>(B) * k * 4;
     const int rowblocks = (n + U - 1) / U;
-    const int groups = groups_for(rowblocks, info.cus, env_int("KUNLUN_GEMV_WAVES_PER_CU", 8));
+    const int groups = groups_for(rowblocks, info.cus, 8);
     hipError_t rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&dense_gemv<B, U, F16>),
                                         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     (void)rc;
@@ -865,7 +560,7 @@ extern "C" int kk_dense_matmul(int type, const void *w, const float *x, float *y
     const uint8_t *wb = static_cast<const uint8_t *>(w);
     const uintptr_t wa = reinterpret_cast<uintptr_t>(w);
     const bool x16 = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
-    const bool force_general = env_int("KUNLUN_GEMV_GENERAL", 0) != 0;
+    const bool force_general = kk::tuning_or(kk::kGemvGeneral, 0) != 0;
 
     bool fast = false;
     if (!force_general && x16) {
@@ -879,8 +574,12 @@ extern "C" int kk_dense_matmul(int type, const void *w, const float *x, float *y
         hipLaunchKernelGGL(gemv_general, dim3(groups), dim3(kThreads), 0, stream, wb, type, x, y, k, n, batch);
         return hipGetLastError();
     }
-    const int q4_kernel = type == 2 ? env_int("KUNLUN_Q4_KERNEL", 0) : -1;   // 0 dot8, 1 stream, 2 pair
-    if (q4_kernel == 0) {
+    if (type == 2 && batch == 1 && kk::tuning_or(kk::kQ4GemvPlanes, 0) != 0 &&
+        kk_q4_gemv_planes_supported(w, x, k, n)) {
+        if (route) *route = "q4_gemv_planes";
+        return kk_q4_gemv_planes(w, x, y, k, n, info.cus, stream);
+    }
+    if (type == 2) {
         if (route) *route = "q4_gemv_dot8";
         const int pair_batch = k <= 8192 ? 2 : 1;   // staged digits: B * K <= 16384
         for (int b0 = 0; b0 < batch; b0 += pair_batch) {
@@ -893,44 +592,13 @@ extern "C" int kk_dense_matmul(int type, const void *w, const float *x, float *y
         }
         return hipSuccess;
     }
-    const bool q4_stream = q4_kernel == 1;
-    if (route) *route = type == 2 ? (q4_stream ? "q4_gemv_stream" : "q4_gemv_pair") : type == 1 ? "f16_gemv" : "f32_gemv";
-    if (q4_stream) {
-        const int u = env_int("KUNLUN_Q4_ROWS", 2), waves = env_int("KUNLUN_Q4_WAVES", 8);
-        const int sc = std::min(chunk, 2);
-        for (int b0 = 0; b0 < batch; b0 += sc) {
-            const int bc = std::min(sc, batch - b0);
-            const float *xc = x + static_cast<size_t>(b0) * k;
-            float *yc = y + static_cast<size_t>(b0) * n;
-            hipError_t rc;
-            if (bc == 1) {
-                if (u == 4) rc = waves == 4 ? launch_q4_stream<1, 4, 4>(wb, xc, yc, k, n, n, stream, info)
-                                            : launch_q4_stream<1, 4, 8>(wb, xc, yc, k, n, n, stream, info);
-                else if (u == 1) rc = waves == 4 ? launch_q4_stream<1, 1, 4>(wb, xc, yc, k, n, n, stream, info)
-                                                 : launch_q4_stream<1, 1, 8>(wb, xc, yc, k, n, n, stream, info);
-                else rc = waves == 4 ? launch_q4_stream<1, 2, 4>(wb, xc, yc, k, n, n, stream, info)
-                                     : launch_q4_stream<1, 2, 8>(wb, xc, yc, k, n, n, stream, info);
-            } else {
-                rc = waves == 4 ? launch_q4_stream<2, 2, 4>(wb, xc, yc, k, n, n, stream, info)
-                                : launch_q4_stream<2, 2, 8>(wb, xc, yc, k, n, n, stream, info);
-            }
-            if (rc != hipSuccess) return rc;
-        }
-        return hipSuccess;
-    }
+    if (route) *route = type == 1 ? "f16_gemv" : "f32_gemv";
     for (int b0 = 0; b0 < batch; b0 += chunk) {
         const int bc = std::min(chunk, batch - b0);
         const float *xc = x + static_cast<size_t>(b0) * k;
         float *yc = y + static_cast<size_t>(b0) * n;
         hipError_t rc = hipSuccess;
-        if (type == 2) {
-            switch (bc) {
-            case 1: rc = launch_q4_pair<1>(wb, xc, yc, k, n, n, stream, info); break;
-            case 2: rc = launch_q4_pair<2>(wb, xc, yc, k, n, n, stream, info); break;
-            case 3: rc = launch_q4_pair<3>(wb, xc, yc, k, n, n, stream, info); break;
-            default: rc = launch_q4_pair<4>(wb, xc, yc, k, n, n, stream, info); break;
-            }
-        } else if (type == 1) {
+        if (type == 1) {
             switch (bc) {
             case 1: rc = launch_dense<1, true>(wb, xc, yc, k, n, n, stream, info); break;
             case 2: rc = launch_dense<2, true>(wb, xc, yc, k, n, n, stream, info); break;
@@ -954,14 +622,16 @@ extern "C" int kk_q4_gemv_pair_swiglu_supported(const void *w_gate, const void *
                                                 int batch) {
     return w_gate && w_up && x && k > 0 && n > 0 && (k % 64) == 0 && k <= 16384 && batch >= 1 && batch <= 2 &&
            (reinterpret_cast<uintptr_t>(w_gate) & 3) == 0 && (reinterpret_cast<uintptr_t>(w_up) & 3) == 0 &&
-           (reinterpret_cast<uintptr_t>(x) & 15) == 0 && env_int("KUNLUN_GEMV_GENERAL", 0) == 0 &&
-           env_int("KUNLUN_Q4_KERNEL", 0) == 0;
+           (reinterpret_cast<uintptr_t>(x) & 15) == 0 && kk::tuning_or(kk::kGemvGeneral, 0) == 0;
 }
 
 extern "C" int kk_q4_gemv_pair_swiglu(const void *w_gate, const void *w_up, const float *x, float *y, int k, int n,
                                      int batch, hipStream_t stream) {
     if (!y || !kk_q4_gemv_pair_swiglu_supported(w_gate, w_up, x, k, n, batch)) return hipErrorInvalidValue;
     const DeviceInfo info = device_info();
+    if (batch == 1 && kk::tuning_or(kk::kQ4GemvPlanes, 0) != 0 && kk_q4_gemv_planes_supported(w_gate, x, k, n) &&
+        kk_q4_gemv_planes_supported(w_up, x, k, n))
+        return kk_q4_gemv_planes_pair_swiglu(w_gate, w_up, x, y, k, n, info.cus, stream);
     const uint8_t *wg = static_cast<const uint8_t *>(w_gate);
     const uint8_t *wu = static_cast<const uint8_t *>(w_up);
     const int pair_batch = k <= 8192 ? 2 : 1;   // staged digits: B * K <= 16384

@@ -16,6 +16,7 @@
 //   final    [4] f32           max0, max1
 #include "device_common.h"
 #include "launch.h"
+#include "tuning.h"
 
 #include <algorithm>
 #include <cstdlib>
@@ -705,11 +706,6 @@ __global__ __launch_bounds__(512) void i8_lds_gemm(const int8_t *__restrict__ co
     }
 }
 
-int env_int(const char *name, int fallback) {
-    const char *value = std::getenv(name);
-    return value && *value ? std::atoi(value) : fallback;
-}
-
 template <int MT, int NT>
 hipError_t launch_i8(const int8_t *codes, const int8_t *w, const float *scales, const float *maxima,
                      const float *final_max, float *y, int k, int n, int batch, hipStream_t stream) {
@@ -732,7 +728,7 @@ extern "C" int kk_i8_quantize(const float *x, int k, int batch, void *workspace,
     if (!x || !workspace || !status || k <= 0 || batch <= 0) return hipErrorInvalidValue;
     const Workspace ws = layout(workspace, k, batch);
     const size_t count = static_cast<size_t>(k) * batch;
-    const size_t fused_limit = std::min<size_t>(static_cast<size_t>(env_int("KUNLUN_I8_FUSED_QUANT_LIMIT", 65536)),
+    const size_t fused_limit = std::min<size_t>(static_cast<size_t>(kk::tuning_or(kk::kI8FusedQuantLimit, 65536)),
                                                 4 * kFusedThreads * kFusedGroups);
     if (count <= fused_limit) {
         hipLaunchKernelGGL(i8_quantize_fused, dim3(1), dim3(kFusedThreads), 0, stream, x, count, k, ws.codes,

@@ -3,11 +3,11 @@
 // kernels for the weight format (reference dispatch src/k200.cpp:187-247).
 #include "launch.h"
 #include "runtime_internal.h"
+#include "tuning.h"
 
 #include <algorithm>
 #include <climits>
 #include <cstdint>
-#include <cstdlib>
 
 namespace kunlun {
 namespace detail {
@@ -38,29 +38,24 @@ void * grow(int id, detail::DeviceContext & ctx, void *& ptr, size_t & size, siz
 // Smallest batch that uses the fp16-MFMA prefill GEMM (F16 and Q4_0 weights);
 // smaller batches keep the F32-accumulate GEMV kernels.
 int gemm_min_batch() {
-    const char * value = std::getenv("KUNLUN_GEMM_MIN_BATCH");
-    const int v = value && *value ? std::atoi(value) : 64;
+    const int v = kk::tuning(kk::kGemmMinBatch);
     return v > 0 ? v : 64;
 }
 
-// Batch range of the single-pass Q4_0 MFMA GEMV (KUNLUN_Q4_MFMA_MIN/MAX, within
-// 1..16). Below the minimum the batch-1 kernel's passes (two columns each) are
-// faster: the streamed kernel (K % 256 == 0, 16-byte aligned weights) wins from
-// 3 columns, the register-staged one from 5.
+// Batch range of the single-pass Q4_0 MFMA GEMV (within 1..16). Below the
+// minimum the batch-1 kernel's passes (two columns each) are faster: the
+// streamed kernel (K % 256 == 0, 16-byte aligned weights) wins from 3
+// columns, the register-staged one from 5.
 bool q4_mfma_batch(int batch, bool streamed) {
-    const char * lo = std::getenv("KUNLUN_Q4_MFMA_MIN");
-    const char * hi = std::getenv("KUNLUN_Q4_MFMA_MAX");
-    const int min_b = std::max(1, lo && *lo ? std::atoi(lo) : streamed ? 3 : 5);
-    const int max_b = std::min(16, hi && *hi ? std::atoi(hi) : 16);
+    const int min_b = std::max(1, kk::tuning_or(kk::kQ4MfmaMin, streamed ? 3 : 5));
+    const int max_b = std::min(16, kk::tuning_or(kk::kQ4MfmaMax, 16));
     return batch >= min_b && batch <= max_b;
 }
 
-// Batch range of the single-pass F32/F16 MFMA GEMV (KUNLUN_DENSE_MFMA_MIN/MAX, within 1..16).
+// Batch range of the single-pass F32/F16 MFMA GEMV (within 1..16).
 bool dense_mfma_batch(int batch) {
-    const char * lo = std::getenv("KUNLUN_DENSE_MFMA_MIN");
-    const char * hi = std::getenv("KUNLUN_DENSE_MFMA_MAX");
-    const int min_b = std::max(1, lo && *lo ? std::atoi(lo) : 2);
-    const int max_b = std::min(16, hi && *hi ? std::atoi(hi) : 16);
+    const int min_b = std::max(1, kk::tuning_or(kk::kDenseMfmaMin, 2));
+    const int max_b = std::min(16, kk::tuning_or(kk::kDenseMfmaMax, 16));
     return batch >= min_b && batch <= max_b;
 }
 

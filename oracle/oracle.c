@@ -357,6 +357,7 @@ int orc_i8_activation(const float *x, size_t count, int8_t *q0, int8_t *q1,
 /* Exact integer dot products out[r*n + c] = sum_j a[r,j] * w[c,j] (the raw
  * int8 x int8 FC products, reference src/k200.cpp:231). */
 void orc_i8_dots(const int8_t *a, int rows, const int8_t *w, int n, int k, int64_t *out) {
+#pragma omp parallel for schedule(static)
     for (int r = 0; r < rows; ++r) {
         const int8_t *ar = a + (size_t)r * k;
         for (int c = 0; c < n; ++c) {

@@ -46,3 +46,19 @@ def kl():
     import kunlunk200_lib_amd as kl
     kl.load()
     return kl
+
+
+@pytest.fixture
+def knobs():
+    """Sets library route/tile knobs (kunlun_set_tuning) for one test and
+    restores the environment's values afterwards."""
+    import kunlunk200_lib_amd as kl
+    touched = set()
+
+    def set_knob(name, value):
+        kl.set_tuning(name, value)
+        touched.add(name)
+
+    yield set_knob
+    for name in touched:
+        kl.set_tuning(name, None)

@@ -64,14 +64,14 @@ def test_gemm_extreme_rows(gpu, oracle):
     assert np.all(y[9] == 0)
 
 
-def test_gemm_matches_gemv_within_fp16(gpu, oracle, monkeypatch):
+def test_gemm_matches_gemv_within_fp16(gpu, oracle, knobs):
     # the same call below and above the GEMM batch threshold
     k, n, batch = 1024, 200, 64
     w = gaussian((n, k), 0.02, 8)
     x = gaussian((batch, k), 1.0, 9)
     payload, dec = weight_payload(kl.WeightType.q4_0, w, oracle)
     y_gemm, r1, _ = run_matmul(kl.WeightType.q4_0, payload, x, k, n, batch)
-    monkeypatch.setenv("KUNLUN_GEMM_MIN_BATCH", "100000")
+    knobs("KUNLUN_GEMM_MIN_BATCH", "100000")
     y_gemv, r2, _ = run_matmul(kl.WeightType.q4_0, payload, x, k, n, batch)
     assert r1 == "q4_gemm_mfma" and r2 != r1
     gold = oracle.gold(dec, x)
@@ -89,8 +89,8 @@ TILE_SHAPES = [(512, 700, 200), (256, 64, 64), (768, 1000, 129)]   # partial M/N
 
 @pytest.mark.parametrize("tile", TILES)
 @pytest.mark.parametrize("k,n,batch", TILE_SHAPES)
-def test_gemm_tile_variants(gpu, oracle, monkeypatch, tile, k, n, batch):
-    monkeypatch.setenv("KUNLUN_GEMM_TILE", tile)
+def test_gemm_tile_variants(gpu, oracle, knobs, tile, k, n, batch):
+    knobs("KUNLUN_GEMM_TILE", tile)
     seed = k + n + batch
     w = gaussian((n, k), 0.02, seed)
     x = gaussian((batch, k), 1.0, seed + 1)
@@ -117,7 +117,7 @@ def test_gemm_misaligned_weights(gpu, oracle, w_offset):
     assert guard_ok and finite and ok and rel <= 2e-3
 
 
-def test_gemm_tiles_agree_exactly(gpu, oracle, monkeypatch):
+def test_gemm_tiles_agree_exactly(gpu, oracle, knobs):
     # every tile shape sums each output in the same order: identical bits
     k, n, batch = 512, 384, 128
     w = gaussian((n, k), 0.02, 50)
@@ -125,7 +125,7 @@ def test_gemm_tiles_agree_exactly(gpu, oracle, monkeypatch):
     payload, _ = weight_payload(kl.WeightType.q4_0, w, oracle)
     outs = []
     for tile in TILES:
-        monkeypatch.setenv("KUNLUN_GEMM_TILE", tile)
+        knobs("KUNLUN_GEMM_TILE", tile)
         outs.append(run_matmul(kl.WeightType.q4_0, payload, x, k, n, batch)[0])
     for y in outs[1:]:
         assert np.array_equal(y.view(np.uint32), outs[0].view(np.uint32))

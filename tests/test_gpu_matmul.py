@@ -129,7 +129,7 @@ def test_q4_misaligned_weights_use_general_kernel(gpu, oracle):
     _, route = _dense_case(oracle, kl.WeightType.q4_0, w, x, k, n, batch, w_offset=2)
     assert route == "gemv_general"
     _, route = _dense_case(oracle, kl.WeightType.q4_0, w, x, k, n, batch, w_offset=0)
-    assert route in ("q4_gemv_dot8", "q4_mfma_gemv")
+    assert route in ("q4_gemv_planes", "q4_gemv_dot8", "q4_mfma_gemv")
 
 
 def test_unaligned_activation_uses_general_kernel(gpu, oracle):
@@ -176,7 +176,8 @@ def test_statistics_count_submissions(gpu, oracle):
 # (batch 1-8, 9-16, 17-32, 33-64); above: the LDS-staged GEMM when K % 128 == 0
 # (partial M and N tiles: 100, 130, 97 batch rows, N 300, 130), else the
 # register-tiled one (96, 70)
-I8_SHAPES = [(64, 3, 1), (1024, 512, 4), (4096, 4096, 1), (96, 17, 9), (4096, 1024, 32),
+I8_SHAPES = [(64, 3, 1), (1024, 512, 4), (4096, 4096, 1), (96, 17, 9), (4096, 1024, 32), (4096, 4096, 32),
+             (4096, 4096, 512),
              (16384, 64, 2), (2048, 300, 8), (1024, 256, 100), (2048, 96, 17), (256, 70, 40), (512, 200, 64),
              (512, 300, 130), (2048, 130, 97), (96, 40, 70)]
 
@@ -259,3 +260,57 @@ def test_rowwise_i8_nonfinite_activation_aborts_at_wait(gpu, k, batch):
     assert "NOT REJECTED" not in proc.stdout
     assert proc.returncode == -signal.SIGABRT, proc.stderr[-2000:]
     assert "non-finite" in proc.stderr
+
+
+# --- BASELINE configs on the route a default matmul takes ---------------------
+
+@pytest.mark.parametrize("k,n,batch,route", [
+    (4096, 32000, 1, "q4_gemv_dot8"),      # configs[1]: LM head
+    (4096, 14336, 2, "q4_gemv_dot8"),      # configs[2]: batch 2 (two columns per pass)
+    (4096, 14336, 4, "q4_mfma_gemv"),
+    (4096, 14336, 16, "q4_mfma_gemv"),
+])
+def test_q4_baseline_configs_default_route(gpu, oracle, k, n, batch, route):
+    seed = k * 3 + n + batch
+    w = gaussian((n, k), 0.02, seed)
+    x = gaussian((batch, k), 1.0, seed + 1)
+    _, got = _dense_case(oracle, kl.WeightType.q4_0, w, x, k, n, batch)
+    assert got == route
+
+
+@pytest.mark.parametrize("k,n", [(4096, 4096), (4096, 32000), (11008, 4096), (12288, 96), (256, 16)])
+def test_q4_planes_opt_in(gpu, oracle, knobs, k, n):
+    # the LDS-staged digit-plane batch-1 GEMV, taken under KUNLUN_Q4_GEMV_PLANES=1
+    knobs("KUNLUN_Q4_GEMV_PLANES", "1")
+    seed = 7 * k + n
+    w = gaussian((n, k), 0.02, seed)
+    x = gaussian((1, k), 1.0, seed + 1)
+    _, got = _dense_case(oracle, kl.WeightType.q4_0, w, x, k, n, 1)
+    assert got == "q4_gemv_planes"
+
+
+def two_fc_rowwise_i8(oracle, w, x):
+    """The reference's batch > 8 rowwise_i8 order (src/k200.cpp:233-239): two
+    int8 FCs with input maxima max0 and max1 and weight maxima 127, each
+    y_c = sum_k (q_x * m_c / 127) * (q_w * 127 / 127), added, then multiplied
+    by the row scales. The FC's own accumulation order is closed (XDNN); it is
+    taken here as the exact dot times m_c / 127 in FP64, rounded to F32."""
+    codes, scales = oracle.i8_rows(w)
+    q0, q1, m0, m1 = oracle.i8_activation(x)
+    fc0 = (oracle.i8_dots(q0, codes).astype(np.float64) * (np.float64(m0) / 127.0)).astype(np.float32)
+    fc1 = (oracle.i8_dots(q1, codes).astype(np.float64) * (np.float64(m1) / 127.0)).astype(np.float32)
+    return ((fc0 + fc1) * scales[None, :]).astype(np.float32)
+
+
+@pytest.mark.parametrize("k,n,batch", [(4096, 512, 9), (4096, 4096, 16), (1024, 512, 32)])
+def test_rowwise_i8_matches_two_fc_order(gpu, oracle, k, n, batch):
+    # reference bench/fused-bench.cpp:29-51: fused and two-FC results agree to
+    # NMSE <= 1e-8 (:48); batch > 8 is where the reference takes the two-FC order
+    w, _ = oracle.fused_bench_weights(k, n)
+    x = oracle.bench_input(k, batch)
+    y, _, guard_ok = run_matmul(kl.WeightType.rowwise_i8, None, x, k, n, batch, w_f32=w)
+    legacy = two_fc_rowwise_i8(oracle, w, x)
+    e = y.astype(np.float64) - legacy
+    nmse = float((e * e).sum() / max(float((legacy.astype(np.float64) ** 2).sum()), 1e-30))
+    print(f"  i8 vs two-FC k={k} n={n} b={batch}: nmse={nmse:.3g}", flush=True)
+    assert guard_ok and np.all(np.isfinite(y)) and nmse <= 1e-8

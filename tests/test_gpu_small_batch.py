@@ -21,8 +21,8 @@ def gaussian(shape, sigma, seed):
 
 
 @pytest.fixture(autouse=True)
-def mfma_from_batch_two(monkeypatch):
-    monkeypatch.setenv("KUNLUN_Q4_MFMA_MIN", "2")
+def mfma_from_batch_two(gpu, knobs):
+    knobs("KUNLUN_Q4_MFMA_MIN", "2")
 
 
 def q4_case(oracle, k, n, batch, seed, x=None):
@@ -71,10 +71,10 @@ def test_weights_off_16_bytes(gpu, oracle):
         assert guard_ok and res["finite"] and res["north_star"] and res["reference"]
 
 
-def test_default_batch_routing(gpu, oracle, monkeypatch):
+def test_default_batch_routing(gpu, oracle, knobs):
     # defaults: the streamed kernel (K % 256 == 0, 16-byte aligned weights)
     # from batch 3, the register-staged one from batch 5, batch-1 passes below
-    monkeypatch.delenv("KUNLUN_Q4_MFMA_MIN")
+    kl.set_tuning("KUNLUN_Q4_MFMA_MIN", None)
     cases = [(512, 3, 0, "q4_mfma_gemv"), (512, 2, 0, "q4_gemv_dot8"), (576, 3, 0, "q4_gemv_dot8"),
              (576, 5, 0, "q4_mfma_gemv"), (512, 4, 4, "q4_gemv_dot8")]
     for k, batch, w_offset, want in cases:
@@ -102,14 +102,14 @@ def test_extreme_rows(gpu, oracle):
     assert np.all(y[3] == 0.0)
 
 
-def test_matches_batch_one_kernel(gpu, oracle, monkeypatch):
+def test_matches_batch_one_kernel(gpu, oracle, knobs):
     # the same call with the MFMA GEMV disabled (pairs of dot8 columns)
     k, n, batch = 4096, 1000, 8
     w = gaussian((n, k), 0.02, 5)
     x = gaussian((batch, k), 1.0, 6)
     q4 = kl.quantize_q4_0(w)
     y_mfma, r1, _ = run_matmul(kl.WeightType.q4_0, q4, x, k, n, batch)
-    monkeypatch.setenv("KUNLUN_Q4_MFMA_MIN", "17")
+    knobs("KUNLUN_Q4_MFMA_MIN", "17")
     y_dot8, r2, _ = run_matmul(kl.WeightType.q4_0, q4, x, k, n, batch)
     assert r1 == "q4_mfma_gemv" and r2 == "q4_gemv_dot8"
     dec = oracle.q4_decode(q4, k, n)
@@ -142,12 +142,12 @@ def test_dense_mfma(gpu, oracle, type_, k, n, batch):
     assert guard_ok and res["finite"] and res["north_star"] and res["reference"]
 
 
-def test_dense_mfma_matches_vector_kernel(gpu, oracle, monkeypatch):
+def test_dense_mfma_matches_vector_kernel(gpu, oracle, knobs):
     for type_ in (kl.WeightType.f16, kl.WeightType.f32):
         y1, r1, _, _, payload, x = dense_case(oracle, type_, 2048, 700, 8, 41)
-        monkeypatch.setenv("KUNLUN_DENSE_MFMA_MIN", "17")
+        knobs("KUNLUN_DENSE_MFMA_MIN", "17")
         y2, r2, _ = run_matmul(type_, payload, x, 2048, 700, 8)
-        monkeypatch.delenv("KUNLUN_DENSE_MFMA_MIN")
+        kl.set_tuning("KUNLUN_DENSE_MFMA_MIN", None)
         assert r1.endswith("mfma_gemv") and not r2.endswith("mfma_gemv")
         # both accumulate exact products in F32, in different orders
         scale = np.abs(y2).max()
