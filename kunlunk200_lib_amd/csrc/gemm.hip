@@ -134,11 +134,25 @@ void launch_x_to_f16(bool permute, const float *x, int batch, int k, int m_pad, 
 }
 
 // ---------------------------------------------------------------------------
+// Subnormal block scales. For an F16 scale d below 2^-14 (exponent field 0)
+// the fp16 product (q - 8) / 8 * d lies on the 2^-24 grid of F16 subnormals
+// and keeps only a few bits. The decode goes on as for any block and only
+// sets `tiny` (one class test; the flag is a lane mask in SGPRs); a workgroup
+// that met such a block adds the difference between its exact F32 values and
+// what the decode made of them in its epilogue (tiny_scale_dots).
+__device__ __forceinline__ void note_tiny_scale(uint32_t bits, bool &tiny) {
+    union { uint16_t u; _Float16 h; } du;
+    du.u = static_cast<uint16_t>(bits);
+    tiny = tiny || __builtin_amdgcn_classh(du.h, 0x090);   // -subnormal | +subnormal
+}
+
 // Q4_0 decode to fp16 (q - 8) * d / 8 (the 1/8 keeps |value| <= 65504 for
-// any F16 scale). dd = d / 8 in both halves (zero for a dead block).
-__device__ __forceinline__ half2v q4_scale8(uint32_t bits, bool live) {
+// any F16 scale). dd = d / 8 in both halves (zero for a dead block); a live
+// block's subnormal scale sets `tiny`.
+__device__ __forceinline__ half2v q4_scale8(uint32_t bits, bool live, bool &tiny) {
     union { uint16_t u; _Float16 h; } du;
     du.u = static_cast<uint16_t>(bits & 0xffffu);
+    if (live) note_tiny_scale(bits, tiny);
     const _Float16 d8 = live ? static_cast<_Float16>(du.h * static_cast<_Float16>(0.125f)) : static_cast<_Float16>(0.0f);
     return half2v{d8, d8};
 }
@@ -167,8 +181,9 @@ __device__ __forceinline__ half8 decode_q4_dword(uint32_t n, half2v dd) {
 
 // Half a block (nibble dwords 2*half, 2*half+1 -> 16 values); e = the 18
 // block bytes as 5 dwords.
-__device__ __forceinline__ void decode_q4_half(const uint32_t (&e)[5], int half, bool live, half8 (&out)[2]) {
-    const half2v dd = q4_scale8(e[0], live);
+__device__ __forceinline__ void decode_q4_half(const uint32_t (&e)[5], int half, bool live, half8 (&out)[2],
+                                               bool &tiny) {
+    const half2v dd = q4_scale8(e[0], live, tiny);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const uint32_t lo = half ? e[2 + j] : e[j], hi = half ? e[3 + j] : e[1 + j];
@@ -211,6 +226,49 @@ __device__ __forceinline__ half8 decode_q4_scaled(uint32_t n, uint32_t dbits) {
     o[0] = h0[0]; o[1] = h0[1]; o[2] = h1[0]; o[3] = h1[1];
     o[4] = h2[0]; o[5] = h2[1]; o[6] = h3[0]; o[7] = h3[1];
     return o;
+}
+
+// The correction for blocks with subnormal scales (note_tiny_scale): for
+// weight row `wrow` (`blocks` Q4_0 blocks) and the R activation rows
+// row_of(0 .. R-1) of x16 (block order, row stride k_pad), adds to out[r] the
+// sum over the row's blocks with a subnormal scale d = +-m * 2^-24 of
+// x16 . (v - decode(v)), v = (q - 8) / 8 * d in F32 and decode(nibble dword,
+// scale bits) the fp16 values the kernel's decode gave them (each one
+// rounding of the exact (q - 8) / 8 * d, so the same in any context). v,
+// decode(v) (both on the 2^-27 grid, below 2^-13) and their difference are
+// exact in F32; the products and sums round. A cold path (byte loads, one
+// block and one nibble dword at a time).
+template <int R, typename RowOf, typename Decode>
+__device__ void tiny_scale_dots(const uint8_t *wrow, int blocks, const _Float16 *x16, int k_pad, RowOf row_of,
+                                Decode decode, float (&out)[R]) {
+#pragma unroll 1
+    for (int b = 0; b < blocks; ++b) {
+        const uint8_t *blk = wrow + 18 * b;
+        const uint32_t bits = blk[0] | (static_cast<uint32_t>(blk[1]) << 8);
+        if ((bits & 0x7c00u) != 0 || (bits & 0x3ffu) == 0) continue;
+        const float d = ldexpf(static_cast<float>(bits & 0x3ffu), -27) * ((bits & 0x8000u) ? -1.0f : 1.0f);   // d / 8
+#pragma unroll 1
+        for (int i = 0; i < 4; ++i) {   // nibble dword i -> block-order positions 8i .. 8i+7
+            const uint8_t *nb = blk + 2 + 4 * i;
+            const uint32_t nib = nb[0] | static_cast<uint32_t>(nb[1]) << 8 | static_cast<uint32_t>(nb[2]) << 16 |
+                                 static_cast<uint32_t>(nb[3]) << 24;
+            const half8 dec = decode(nib, bits);
+            float wv[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const uint32_t byte = nb[(t & 1) << 1 | (t & 2) >> 1];   // bytes 0, 2, 1, 3
+                const uint32_t q = t < 4 ? byte & 15u : byte >> 4;
+                wv[t] = (static_cast<float>(q) - 8.0f) * d - static_cast<float>(dec[t]);
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const half8 xv = *reinterpret_cast<const half8 *>(x16 + static_cast<size_t>(row_of(r)) * k_pad +
+                                                                  32 * b + 8 * i);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) out[r] += static_cast<float>(xv[t]) * wv[t];
+            }
+        }
+    }
 }
 
 // Workgroup tile 128 (M) x BN (N) x 128 (K) per step, 8 waves: two
@@ -311,6 +369,7 @@ __global__ __launch_bounds__(kGemmThreads) void mfma_gemm(const uint8_t *__restr
     uint32_t b_reg[kStages][kBWords];
     uint32_t shift_reg[kStages];
     bool live_reg[kStages];
+    bool tiny = false;   // Q4_0: set once this thread skipped a block with a subnormal scale
 
     auto load = [&](int step, int set) {
         const int ks = min(step, steps - 1);              // past the end: reload the last step
@@ -369,12 +428,12 @@ __global__ __launch_bounds__(kGemmThreads) void mfma_gemm(const uint8_t *__restr
             half8 *bd = reinterpret_cast<half8 *>(b_lds + qb_row * kLdsStride + qb_blk * 32 + qb_half * 16);
             if constexpr (BN == 128) {
                 half8 lo[2], hi[2];
-                decode_q4_half(e, 0, live_reg[set], lo);
-                decode_q4_half(e, 1, live_reg[set], hi);
+                decode_q4_half(e, 0, live_reg[set], lo, tiny);
+                decode_q4_half(e, 1, live_reg[set], hi, tiny);
                 bd[0] = lo[0]; bd[1] = lo[1]; bd[2] = hi[0]; bd[3] = hi[1];
             } else {
                 half8 out[2];
-                decode_q4_half(e, qb_half, live_reg[set], out);
+                decode_q4_half(e, qb_half, live_reg[set], out, tiny);
                 bd[0] = out[0]; bd[1] = out[1];
             }
         }
@@ -444,9 +503,35 @@ __global__ __launch_bounds__(kGemmThreads) void mfma_gemm(const uint8_t *__restr
 #pragma unroll
                 for (int r = 0; r < 16; ++r) red[(((sw * 2 + it) * kNT + jt) * 16 + r) * kWave + lane] = acc[it][jt][r];
     }
-    __syncthreads();
+    const bool any_tiny = __syncthreads_or(tiny) != 0;   // workgroup-uniform
     if (kh == 1) return;
     const float wscale = F16W ? 1.0f : 8.0f;
+    // Q4_0 blocks with subnormal scales (skipped by the decode) into acc, in
+    // F32: lane column n of MFMA tile jt, rows m(it, r).
+    if (!F16W && any_tiny) {
+#pragma unroll
+        for (int jt = 0; jt < kNT; ++jt) {
+            const int j = wn * (BN / 2) + jt * 32 + (lane & 31);            // B tile row
+            const int n = PAIR ? n0 + wn * 32 + (lane & 31) : n0 + j;
+            if (n >= n_rows) continue;
+            const uint8_t *wrow = (PAIR && jt == 1 ? w2 : w) + static_cast<size_t>(n) * row_bytes;
+#pragma unroll
+            for (int it = 0; it < 2; ++it) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {   // D regs 4c .. 4c+3: rows 8c + 4(lane/32) + 0..3
+                    auto row_of = [&](int r) { return m0 + wm * 64 + it * 32 + 8 * c + 4 * (lane >> 5) + r; };
+                    float fix[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                    auto decode = [](uint32_t nib, uint32_t bits) {
+                        bool unused = false;
+                        return decode_q4_dword(nib, q4_scale8(bits, true, unused));
+                    };
+                    tiny_scale_dots<4>(wrow, blocks, x16, k_pad, row_of, decode, fix);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[it][jt][4 * c + r] += fix[r];
+                }
+            }
+        }
+    }
     if constexpr (PAIR) {
         const int n = n0 + wn * 32 + (lane & 31);
 #pragma unroll
@@ -636,6 +721,7 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
     for (int i = 0; i < S::RG; ++i)
 #pragma unroll
         for (int j = 0; j < S::CG; ++j) acc[i][j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    bool tiny = false;   // set once this lane skipped a block with a subnormal scale
 
     // One stage: this k-group's two K32 slices. Operand reads run one MFMA
     // group ahead (the next two A row tiles, or the next slice's weight bytes
@@ -668,7 +754,10 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
         read_b(b_lds, j0, nib, sbits);
         half8 a0 = read_a(a_lds, j0, 0), a1 = read_a(a_lds, j0, 1);
 #pragma unroll
-        for (int cg = 0; cg < S::CG; ++cg) b0[cg] = decode_q4_scaled(nib[cg], sbits[cg]);
+        for (int cg = 0; cg < S::CG; ++cg) {
+            note_tiny_scale(sbits[cg], tiny);
+            b0[cg] = decode_q4_scaled(nib[cg], sbits[cg]);
+        }
         // Block j0: the first MFMA group also reads block j1's weight bytes,
         // and each later group decodes some of them after issuing its MFMAs
         // (the decode overlaps MFMA execution instead of stalling it).
@@ -693,8 +782,10 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int cg = 0; cg < S::CG; ++cg)
-                if (grp > 0 && (cg + 1 < S::RG / 2 ? cg + 1 : S::RG / 2 - 1) == grp)
+                if (grp > 0 && (cg + 1 < S::RG / 2 ? cg + 1 : S::RG / 2 - 1) == grp) {
+                    note_tiny_scale(sbits[cg], tiny);
                     b1[cg] = decode_q4_scaled(nib[cg], sbits[cg]);
+                }
             a0 = n0;
             a1 = n1;
         }
@@ -767,7 +858,28 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
                 for (int r = 0; r < 4; ++r)
                     tile_lds[(rg * 16 + 4 * g + r) * kTs + wn * WN + cg * 16 + c16] = acc[rg][cg][r];
     }
-    __syncthreads();
+    if (__syncthreads_or(tiny)) {   // workgroup-uniform
+        // Q4_0 blocks with subnormal scales (skipped by the decode), in F32,
+        // into k-group 1's sums: work item -> B row j of the tile and
+        // activation rows 8p .. 8p+7.
+        static_assert(BM % 8 == 0, "fixup rows");
+        for (int item = threadIdx.x; item < S::BN * (BM / 8); item += kQlThreads) {
+            const int j = item % S::BN, p8 = item / S::BN;
+            const int h = PAIR ? j / (S::BN / 2) : 0, jr = PAIR ? j % (S::BN / 2) : j;   // matrix, row in it
+            const int col = PAIR ? (jr / (WN / 2)) * WN + h * (WN / 2) + jr % (WN / 2) : j;   // tile column
+            if (n0 + jr >= n_rows) continue;
+            const uint8_t *wrow = (h ? w2 : w) + static_cast<size_t>(n0 + jr) * row_bytes;
+            auto row_of = [&](int r) { return m0 + 8 * p8 + r; };
+            float fix[8];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) fix[r] = 0.0f;
+            auto decode = [](uint32_t nib, uint32_t bits) { return decode_q4_scaled(nib, bits); };
+            tiny_scale_dots<8>(wrow, static_cast<int>(row_bytes / 18), x16, k_pad, row_of, decode, fix);
+#pragma unroll
+            for (int r = 0; r < 8; ++r) tile_lds[(8 * p8 + r) * kTs + col] += fix[r];
+        }
+        __syncthreads();
+    }
     if constexpr (PAIR) {
         // SiLU(gate) * up into acc's gate slots, then (after every read of the
         // tile) into output columns 0 .. BN/2

@@ -92,9 +92,13 @@ def test_f16_nonfinite_rows(gpu, batch, route):
 
 # --- Q4_0 with F16-subnormal block scales ----------------------------------------
 
-def q4_subnormal(k, n, seed, mixed):
+def q4_subnormal(k, n, seed, mixed, tiny=False, low_normal=False):
     """Q4_0 rows with subnormal scales (|d| < 2^-14) in every block, or in
-    every other block beside normal scales near 0.0075 when `mixed`."""
+    every other block beside normal scales near 0.0075 when `mixed`. `tiny`
+    draws every scale from the far end instead: subnormals m * 2^-24 with
+    m = 1..15 (then (q - 8) / 8 * d is itself a fraction of the smallest
+    F16 subnormal), or with `low_normal` normals below 2^-11 (exponent
+    fields 1..3), where (q - 8) / 8 * d falls below the F16 normal range."""
     rng = np.random.default_rng(seed)
     blocks = k // 32
     q4 = np.empty((n, blocks, 18), np.uint8)
@@ -102,6 +106,12 @@ def q4_subnormal(k, n, seed, mixed):
         (rng.integers(0, 2, size=(n, blocks), dtype=np.uint16) << 15)
     # the smallest magnitudes too: exact powers 2^-24 .. 2^-15
     sub[:, ::7] = (np.uint16(1) << rng.integers(0, 10, size=sub[:, ::7].shape, dtype=np.uint16))
+    if tiny:
+        sign = rng.integers(0, 2, size=(n, blocks), dtype=np.uint16) << 15
+        small = rng.integers(1, 16, size=(n, blocks), dtype=np.uint16)
+        low = (rng.integers(1, 4, size=(n, blocks), dtype=np.uint16) << 10) | \
+            rng.integers(0, 1024, size=(n, blocks), dtype=np.uint16)
+        sub = (low if low_normal else small) | sign
     if mixed:
         normal = (rng.standard_normal((n, blocks)) * 0.0075).astype(np.float16).view(np.uint16)
         sub[:, 1::2] = normal[:, 1::2]
@@ -131,14 +141,17 @@ Q4_ROUTES = [
 ]
 
 
-@pytest.mark.parametrize("mixed", [False, True], ids=["all_subnormal", "mixed"])
+@pytest.mark.parametrize("scales", ["all_subnormal", "mixed", "tiny", "tiny_mixed", "low_normal"])
 @pytest.mark.parametrize("k,batch,w_offset,route,tol", Q4_ROUTES,
                          ids=[f"{r}-k{k}-b{b}-o{o}" for k, b, o, r, _ in Q4_ROUTES])
-def test_q4_subnormal_scales(gpu, oracle, knobs, k, batch, w_offset, route, tol, mixed):
+def test_q4_subnormal_scales(gpu, oracle, knobs, k, batch, w_offset, route, tol, scales):
     if route == "q4_gemv_planes":
         knobs("KUNLUN_Q4_GEMV_PLANES", "1")
     n = 160
-    q4 = q4_subnormal(k, n, k + batch + int(mixed), mixed)
+    mixed = scales.endswith("mixed")
+    tiny = scales.startswith("tiny") or scales == "low_normal"
+    q4 = q4_subnormal(k, n, k + batch + int(mixed) + 2 * len(scales), mixed, tiny=tiny,
+                      low_normal=scales == "low_normal")
     dec = oracle.q4_decode(q4, k, n)
     x = np.random.default_rng(k * batch).standard_normal((batch, k)).astype(np.float32)
     y, got_route, guard_ok = run_matmul(kl.WeightType.q4_0, q4, x, k, n, batch, w_offset=w_offset)
@@ -146,7 +159,7 @@ def test_q4_subnormal_scales(gpu, oracle, knobs, k, batch, w_offset, route, tol,
     gold = oracle.gold(dec, x, threads=16)
     assert np.all(np.isfinite(y))
     ok, ratio = gemm_bound_ok(y, gold, dec, x, tol)
-    print(f"  q4 subnormal scales {route} k={k} b={batch} mixed={mixed}: max err / bound = {ratio:.3g}",
+    print(f"  q4 subnormal scales {route} k={k} b={batch} {scales}: max err / bound = {ratio:.3g}",
           flush=True)
     assert ok, f"{route}: error {ratio:.3g} x the bound {tol} * ||x|| * ||w||"
     if tol == 1e-4:
