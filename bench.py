@@ -1,21 +1,31 @@
 #!/usr/bin/env python3
 """Q4_0 GEMV bandwidth benchmark of the KunlunK200 matmul path on one MI355X.
 
-Workload: one Llama-7B-style decode layer set at
-batch 1, Q4_0 weights from N(0, 0.02) quantized with the ggml closed form,
-F32 activations N(0, 1): K4096->N12288 (QKV), K4096->N11008 x2 (gate, up),
-K11008->N4096 (down), K4096->N32000 (LM head). One step = the five
-kunlun::matmul() calls. Three distinct device copies of the set (3 x 178 MB)
-rotate so the 256 MB Infinity Cache cannot hold the weights.
+Workload (the metric's own shape, the gate GEMV of BASELINE.json configs[1]):
+one step = one kunlun::matmul() of Q4_0 K4096 x N11008 at batch 1, weights
+from N(0, 0.02) quantized with the ggml closed form, F32 activations N(0, 1).
+Distinct device copies of the matrix (>= 640 MB in all) rotate so the 256 MB
+Infinity Cache cannot hold the weights. value = algorithmic bytes of a step /
+step time, bytes per GEMV = n*(k/32)*18 + 4*b*k + 4*b*n. Timing uses HIP events
+recorded on the library's own stream around K steps (after 200 ms of untimed
+steps and W warm-up steps).
 
-value = algorithmic bytes of a step / step time, bytes per GEMV =
-n*(k/32)*18 + 4*b*k + 4*b*n. Timing uses HIP events recorded on the library's
-own stream around K steps (after 200 ms of untimed steps and W warm-up
-steps). copy_ceiling: the runtime's device-to-device copy moving the gate and
-LM-head GEMVs' bytes, a ceiling reference at their size. roofline: the dominant
-kernel, the K4096xN11008 GEMV, timed alone the same way. cpu_baseline: the
-reference's CPU oracle (bench/native-q4-reference.h, FP64, 6 OpenMP threads)
-on the K4096xN11008 GEMV, repeated for about --cpu-seconds.
+Beside it, on the same rotating copies:
+  layer_set     the whole decode layer set of configs[1] (K4096->N12288 QKV,
+                K4096->N11008 x2 gate/up, K11008->N4096 down, K4096->N32000
+                LM head), five matmul() calls per step, and each shape alone
+                in per_shape, with configs[0] (K4096 x N4096) beside them.
+  read_ceiling  read-only streaming kernels (libkunlunk200_stream.so) reading
+                25.4 MB, 73.9 MB and 268 MB once per launch over rotating
+                buffers of >= 640 MB: the measured HBM read ceiling at the
+                GEMVs' sizes. roofline reports the GEMV's fraction of the spec
+                peak and of this ceiling.
+  cpu_baseline  the reference's CPU path on the K4096 x N11008 GEMV (decoded
+                F32 weights, FP64 sums) at 1 thread (the oracle's restatement of
+                bench/library-bench.cpp:121-122), 6 threads (the reference's own
+                bench/native-q4-reference.h:98-108, compiled under oracle/_ref)
+                and nproc threads (the restatement), each repeated for about
+                --cpu-seconds, with the host CPU model.
 """
 from __future__ import annotations
 
@@ -37,6 +47,8 @@ METRIC = "Q4_0 GEMV GB/s (% HBM peak) K4096×N11008 batch1; GEMM TFLOP/s at batc
 HBM_PEAK_GBPS = 8000.0
 LAYER = [("qkv", 4096, 12288), ("gate", 4096, 11008), ("up", 4096, 11008), ("down", 11008, 4096),
          ("lm_head", 4096, 32000)]
+CONFIG0 = ("cfg0", 4096, 4096)          # configs[0]: k200-bench matmul q4_0 0 4096 4096 1
+SHAPES = LAYER + [CONFIG0]
 DOMINANT = ("gate", 4096, 11008)
 COPIES = 3
 ROTATE_BYTES = 640 * 1000 * 1000     # > 2x the 256 MB Infinity Cache
@@ -86,34 +98,73 @@ def upload_q4_matrix(buf: kl.Buffer, k: int, n: int, seed: int) -> None:
         buf.upload(kl.quantize_q4_0(w), offset=r0 * row_bytes)
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo", encoding="utf-8") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def host_threads() -> int:
+    """CPUs this process may run on (the box's share, not the machine's count)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
 def cpu_baseline(seconds: float) -> dict | None:
+    """The reference CPU path on the dominant GEMV at 1, 6 and nproc threads; the 6-thread
+    figure (the reference's own setting) is the headline `value`."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import _oracle
     _, k, n = DOMINANT
     rng = np.random.Generator(np.random.PCG64(99))
     w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
-    dec = _oracle.Oracle().q4_decode(kl.quantize_q4_0(w), k, n)
+    orc = _oracle.Oracle()
+    dec = orc.q4_decode(kl.quantize_q4_0(w), k, n)
     x = rng.standard_normal((1, k), dtype=np.float32)
     ref = _oracle.ReferenceOracle.load()
-    if ref is not None:
-        run, kind, cores = (lambda: ref.reference(dec, x)), "reference", 6
-        what = "kref_reference = reference bench/native-q4-reference.h:98-108 (FP64, 6 OpenMP threads)"
-    else:
-        orc = _oracle.Oracle()
-        run, kind, cores = (lambda: orc.gold(dec, x, threads=6)), "port", 6
-        what = "oracle orc_gold (FP64 restatement of library-bench.cpp:121-122, 6 OpenMP threads)"
-    run()
-    reps, start = 0, time.perf_counter()
-    while True:
+    nproc = host_threads()
+
+    def timed_calls(run) -> tuple:
         run()
-        reps += 1
-        elapsed = time.perf_counter() - start
-        if elapsed >= seconds or reps >= 10000:
-            break
-    per_call = elapsed / reps
-    return {"value": round(q4_bytes(k, n) / per_call / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": kind,
-            "sample": f"{what}; K{k}xN{n} batch 1 decoded Q4_0 weights, {reps} calls in {elapsed:.1f} s, "
-                      f"{per_call * 1e3:.3f} ms/call, host cpus={os.cpu_count()}"}
+        reps, start = 0, time.perf_counter()
+        while True:
+            run()
+            reps += 1
+            elapsed = time.perf_counter() - start
+            if elapsed >= seconds or reps >= 10000:
+                return reps, elapsed
+
+    runs = [(1, "port", "oracle orc_gold: FP64 restatement of bench/library-bench.cpp:121-122, 1 thread",
+             lambda: orc.gold(dec, x, threads=1))]
+    if ref is not None:
+        runs.append((6, "reference", "kref_reference: the reference's bench/native-q4-reference.h:98-108 "
+                     "compiled as is (FP64, 6 OpenMP threads)", lambda: ref.reference(dec, x)))
+    else:
+        runs.append((6, "port", "oracle orc_gold, 6 threads (oracle/_ref not built)",
+                     lambda: orc.gold(dec, x, threads=6)))
+    runs.append((nproc, "port", f"oracle orc_gold, {nproc} threads (this process's CPUs)",
+                 lambda: orc.gold(dec, x, threads=nproc)))
+    by_threads = []
+    for threads, kind, what, run in runs:
+        reps, elapsed = timed_calls(run)
+        per_call = elapsed / reps
+        by_threads.append({"threads": threads, "kind": kind, "what": what,
+                           "gbps": round(q4_bytes(k, n) / per_call / 1e9, 4),
+                           "ms_per_call": round(per_call * 1e3, 3), "calls": reps,
+                           "seconds": round(elapsed, 2)})
+        log(f"cpu baseline {threads} thread(s): {per_call * 1e3:.3f} ms/call")
+    head = by_threads[1]
+    return {"value": head["gbps"], "unit": "GB/s", "cores": head["threads"], "kind": head["kind"],
+            "sample": f"{head['what']}; K{k}xN{n} batch 1, decoded Q4_0 weights, {head['calls']} calls in "
+                      f"{head['seconds']} s ({head['ms_per_call']} ms/call); 1/6/nproc-thread runs in by_threads",
+            "cpu_model": cpu_model(), "host_cpus": nproc, "by_threads": by_threads}
 
 
 COPY_BYTES = 512 << 20
@@ -175,6 +226,61 @@ def copy_ceiling_leg(events, stream, device: int, reps: int) -> dict:
         out[f"{name}_k{k}_n{n}"] = {"moved_bytes": 2 * half, "us": round(ms * 1e3, 3),
                                     "gbps": round(2 * half / (ms * 1e-3) / 1e9, 1),
                                     "host_us": round(host_s / reps * 1e6, 3)}
+    return out
+
+
+READ_SIZES = (("gate_gemv", q4_bytes(4096, 11008)), ("lm_head_gemv", q4_bytes(4096, 32000)),
+              ("256mib", 256 << 20))
+READ_WAVES = (2048, 4096, 8192)          # 8, 16 and 32 waves per CU
+READ_VARIANTS = ((0, "grid_stride"), (1, "all_issued"), (2, "all_issued_nt"))
+
+
+def read_ceiling_leg(events, stream, device: int, reps: int) -> dict:
+    """Measured HBM read ceiling: kk_stream_read (kunlunk200_lib_amd/csrc/stream_read.hip) reads
+    each size once per launch from a buffer slot that rotates over >= ROTATE_BYTES, for every
+    variant and grid size that fits (at most 64 KiB per wave); `best` is the fastest."""
+    lib = ctypes.CDLL(os.path.join(ROOT, "kunlunk200_lib_amd", "lib", "libkunlunk200_stream.so"))
+    lib.kk_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int,
+                                   ctypes.c_void_p, ctypes.c_void_p]
+    lib.kk_stream_read.restype = ctypes.c_int
+    out_word = kl.Buffer(device, 256)
+    out = {}
+    for name, size in READ_SIZES:
+        size = size // 16 * 16
+        slot = (size + 255) & ~255
+        slots = max(2, -(-ROTATE_BYTES // slot))
+        buf = kl.Buffer(device, slot * slots)
+        buf.upload(np.zeros(1, np.uint32))
+        runs = []
+        for variant, vname in READ_VARIANTS:
+            for waves in READ_WAVES:
+                if variant > 0 and -(-size // waves) > 64 * 1024:
+                    continue
+
+                def one(i, variant=variant, waves=waves):
+                    rc = lib.kk_stream_read(ctypes.c_void_p(buf.data + (i % slots) * slot), size, variant, waves,
+                                            ctypes.c_void_p(out_word.data), ctypes.c_void_p(stream))
+                    if rc != 0:
+                        raise RuntimeError(f"kk_stream_read({name}, variant {variant}, waves {waves}) -> {rc}")
+                with kl.runtime_mutex():
+                    kl.select(device)
+                    for i in range(slots + 2):
+                        one(i)
+                    kl.check(kl.wait())
+                    start, stop = events.create(), events.create()
+                    events.record(start, stream)
+                    for i in range(reps):
+                        one(i)
+                    events.record(stop, stream)
+                    us = events.elapsed_ms(start, stop) / reps * 1e3
+                    kl.check(kl.wait())
+                runs.append({"variant": vname, "waves": waves, "us": round(us, 3),
+                             "gbps": round(size / (us * 1e-6) / 1e9, 1)})
+        buf.close()
+        best = min(runs, key=lambda r: r["us"])
+        out[name] = {"bytes": size, "rotating_slots": slots, "best": best, "runs": runs}
+        log(f"read ceiling {name}: {best['us']} us, {best['gbps']} GB/s ({best['variant']}, {best['waves']} waves)")
+    out_word.close()
     return out
 
 
@@ -509,15 +615,17 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--kernel-reps", type=int, default=300, help="launches of the dominant GEMV for roofline")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=5.0, help="seconds per CPU-baseline thread count")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gemm-reps", type=int, default=50, help="timed batch-512 GEMM calls per shape (0: skip)")
     ap.add_argument("--small-reps", type=int, default=100, help="timed calls per small-batch config (0: skip)")
     ap.add_argument("--native-reps", type=int, default=100, help="timed native_q4_matmul calls per shape (0: skip)")
     ap.add_argument("--common-reps", type=int, default=50, help="timed common_q4_matmul calls per shape (0: skip)")
     ap.add_argument("--i8-reps", type=int, default=50, help="timed rowwise_i8 matmul calls per case (0: skip)")
-    ap.add_argument("--only", choices=[name for name, _, _ in LAYER] + ["gemm", "copy", "small", "native", "common", "i8"],
-                    help="profiling aid: time only this GEMV's launch loop, the GEMM leg, or (copy) a "
+    ap.add_argument("--read-reps", type=int, default=200, help="timed launches per read-ceiling run (0: skip)")
+    ap.add_argument("--only", choices=[name for name, _, _ in SHAPES] + ["gemm", "copy", "small", "native", "common",
+                                                                          "i8", "read"],
+                    help="profiling aid: time only this GEMV's launch loop, one leg, or (copy) a "
                          f"{COPY_BYTES >> 20} MiB device-to-device copy that calibrates the traffic counters")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -547,6 +655,9 @@ def main() -> int:
     if args.only == "native":
         print(json.dumps({"native_q4": native_leg(events, stream, device, args.native_reps)}), flush=True)
         return 0
+    if args.only == "read":
+        print(json.dumps({"read_ceiling": read_ceiling_leg(events, stream, device, args.read_reps)}), flush=True)
+        return 0
     if args.only == "copy":
         print(json.dumps({"copy": copy_leg(events, stream, device),
                           "copy_ceiling": copy_ceiling_leg(events, stream, device, 300)}), flush=True)
@@ -556,7 +667,7 @@ def main() -> int:
     # copies[name][c]: distinct device copies of each matrix, at least
     # ROTATE_BYTES per shape, so every launch reads its weights from HBM.
     copies = {}
-    for i, (name, k, n) in enumerate(LAYER):
+    for i, (name, k, n) in enumerate(SHAPES):
         if args.only and name != args.only:
             continue
         nbytes = n * (k // 32) * 18
@@ -573,7 +684,7 @@ def main() -> int:
         copies[name] = bufs
     rng = np.random.Generator(np.random.PCG64(7))
     xs, ys = {}, {}
-    for name, k, n in LAYER:
+    for name, k, n in SHAPES:
         xb = kl.Buffer(device, 4 * k)
         xb.upload(rng.standard_normal(k, dtype=np.float32))
         xs[name] = xb
@@ -607,7 +718,7 @@ def main() -> int:
         return ms
 
     if args.only:
-        name, k, n = next(item for item in LAYER if item[0] == args.only)
+        name, k, n = next(item for item in SHAPES if item[0] == args.only)
 
         def only(i):
             kl.matmul(kernel, device, ys[name].data, weights(name, i), xs[name].data, k, n, 1, kl.WeightType.q4_0)
@@ -616,6 +727,11 @@ def main() -> int:
                           "host_us_per_call": round(host_us["only"], 3),
                           "gbps": round(q4_bytes(k, n) / (ms * 1e-3) / 1e9, 1), "route": kernel.route}), flush=True)
         return 0
+
+    dname, dk, dn = DOMINANT
+
+    def gate_step(i: int) -> None:
+        kl.matmul(kernel, device, ys[dname].data, weights(dname, i), xs[dname].data, dk, dn, 1, kl.WeightType.q4_0)
 
     # settle: untimed layer-set steps for SETTLE_MS of wall time before the
     # warm-up steps, so the timed region does not start while the GPU is still
@@ -630,12 +746,17 @@ def main() -> int:
                 step(settle_steps + i)
             settle_steps += 50
             kl.check(kl.wait())
-    log("timing the layer set")
+    log("timing the K4096xN11008 GEMV steps")
     wall0 = time.perf_counter()
-    step_ms = timed(step, args.steps, args.warmup) / args.steps
+    step_ms = timed(gate_step, args.steps, args.warmup, "step") / args.steps
     wall_ms = (time.perf_counter() - wall0) * 1e3
-    step_bytes = sum(q4_bytes(k, n) for _, k, n in LAYER)
+    step_bytes = q4_bytes(dk, dn)
     value = step_bytes / (step_ms * 1e-3) / 1e9
+    gate_route = kernel.route
+
+    log("timing the layer set")
+    layer_ms = timed(step, args.steps, args.warmup) / args.steps
+    layer_bytes = sum(q4_bytes(k, n) for _, k, n in LAYER)
 
     # Spread: SPREAD_LOOPS more event-timed loops of SPREAD_LAUNCHES launches
     # each (an event per launch would make the loop host-bound and time the
@@ -644,7 +765,7 @@ def main() -> int:
         return [timed(fn, SPREAD_LAUNCHES, 2) / SPREAD_LAUNCHES * 1e3 for _ in range(SPREAD_LOOPS)]
 
     per_shape = {}
-    for name, k, n in LAYER:
+    for name, k, n in SHAPES:
         def one(i, name=name, k=k, n=n):
             kl.matmul(kernel, device, ys[name].data, weights(name, i), xs[name].data, k, n, 1, kl.WeightType.q4_0)
         ms = timed(one, args.kernel_reps, 5) / args.kernel_reps
@@ -652,11 +773,11 @@ def main() -> int:
         spread = loop_means(one)
         per_shape[f"{name}_k{k}_n{n}"] = {"us": round(ms * 1e3, 3), "gbps": round(gbps, 1),
                                            "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "route": kernel.route,
+                                           "rotating_copies": len(copies[name]),
                                            "loop_mean_us": {"loops": SPREAD_LOOPS, "launches": SPREAD_LAUNCHES,
                                                             "median": round(float(np.median(spread)), 3),
                                                             "min": round(min(spread), 3),
                                                             "max": round(max(spread), 3)}}
-    dname, dk, dn = DOMINANT
     dom = per_shape[f"{dname}_k{dk}_n{dn}"]
     achieved = dom["gbps"]
 
@@ -666,6 +787,8 @@ def main() -> int:
     common = common_leg(events, stream, device, args.common_reps) if args.common_reps > 0 else None
     i8 = i8_leg(kernel, events, stream, device, args.i8_reps) if args.i8_reps > 0 else None
     ceiling = copy_ceiling_leg(events, stream, device, args.kernel_reps)
+    read = read_ceiling_leg(events, stream, device, args.read_reps) if args.read_reps > 0 else None
+    read_gbps = read["gate_gemv"]["best"]["gbps"] if read else None
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     result = {
         "metric": METRIC,
@@ -681,15 +804,16 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic: Q4_0 from seeded N(0,0.02) (ggml closed form), X ~ N(0,1) f32",
         "config": {
-            "workload": "llama7b-decode-layer-q4_0-gemv-b1 (BASELINE configs[1])",
-            "shapes_k_n": [[k, n] for _, k, n in LAYER],
+            "workload": "q4_0-gemv-k4096-n11008-b1 (the metric's shape; the gate GEMV of BASELINE configs[1])",
+            "k": dk,
+            "n": dn,
             "batch": 1,
             "bytes_per_step": step_bytes,
-            "rotating_copies_per_shape": {name: len(bufs) for name, bufs in copies.items()},
-            "weight_set_mb": round(sum(n * (k // 32) * 18 for _, k, n in LAYER) / 1e6, 1),
-            "route": dom["route"],
+            "hbm_frac": round(value / HBM_PEAK_GBPS, 4),
+            "rotating_copies": len(copies[dname]),
+            "route": gate_route,
             "wall_ms_timed_region": round(wall_ms, 3),
-            "settle": {"ms": SETTLE_MS, "untimed_steps": settle_steps},
+            "settle": {"ms": SETTLE_MS, "untimed_layer_set_steps": settle_steps},
         },
         "roofline": {
             "bound": "hbm",
@@ -702,9 +826,19 @@ def main() -> int:
             "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT) if measured_traffic() else None,
             "bytes_per_launch": q4_bytes(dk, dn),
             "avg_launch_us": dom["us"],
+            "read_ceiling_gbps": read_gbps,
+            "frac_of_read_ceiling": round(achieved / read_gbps, 4) if read_gbps else None,
         },
         "cpu_baseline": cpu,
+        "layer_set": {
+            "shapes_k_n": [[k, n] for _, k, n in LAYER],
+            "ms_per_step": round(layer_ms, 6),
+            "bytes_per_step": layer_bytes,
+            "gbps": round(layer_bytes / (layer_ms * 1e-3) / 1e9, 1),
+            "weight_set_mb": round(sum(n * (k // 32) * 18 for _, k, n in LAYER) / 1e6, 1),
+        },
         "per_shape": per_shape,
+        "read_ceiling": read,
         "copy_ceiling": ceiling,
         "gemm_b512": gemm,
         "small_batch": small,
