@@ -173,7 +173,8 @@ TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "q4_gemv_dot8_k4096_n11008_traf
 
 def copy_leg(events, stream, device: int, reps: int = 10) -> dict:
     """A plain device-to-device copy of COPY_BYTES: its FETCH_SIZE and WRITE_SIZE per dispatch
-    calibrate the counters (the copy reads and writes exactly COPY_BYTES)."""
+    calibrate the counters (the copy reads and writes exactly COPY_BYTES). Each copy completes
+    before the next is submitted, so `us` includes the host round trip."""
     src, dst = kl.Buffer(device, COPY_BYTES), kl.Buffer(device, COPY_BYTES)
     with kl.runtime_mutex():
         kl.select(device)
@@ -187,46 +188,6 @@ def copy_leg(events, stream, device: int, reps: int = 10) -> dict:
     src.close()
     dst.close()
     return {"bytes": COPY_BYTES, "reps": reps, "us": round(ms * 1e3, 2)}
-
-
-COPY_CEILING = (("gate", 4096, 11008), ("lm_head", 4096, 32000))
-
-
-def copy_ceiling_leg(events, stream, device: int, reps: int) -> dict:
-    """What the runtime's own device-to-device copy takes to move as many HBM bytes as a
-    GEMV of these shapes reads: half the GEMV's bytes copied (read + written), source and
-    destination each rotating over >= ROTATE_BYTES so neither stays in the Infinity Cache.
-    `us` is per copy over `reps` copies in one event pair; `host_us` is the host's wall time
-    per copy submission (a loop whose host_us reaches us is host-bound)."""
-    out = {}
-    for name, k, n in COPY_CEILING:
-        half = (q4_bytes(k, n) // 2 + 255) & ~255
-        slots = max(2, -(-ROTATE_BYTES // half))
-        src, dst = kl.Buffer(device, half * slots), kl.Buffer(device, half * slots)
-
-        def one(i):
-            kl.check(kl.copy(dst.data + (i % slots) * half, src.data + ((7 * i + 3) % slots) * half, half,
-                             kl.CopyKind.device_to_device))
-        with kl.runtime_mutex():
-            kl.select(device)
-            for i in range(5):
-                one(i)
-            kl.check(kl.wait())
-            start, stop = events.create(), events.create()
-            t0 = time.perf_counter()
-            events.record(start, stream)
-            for i in range(reps):
-                one(i)
-            events.record(stop, stream)
-            host_s = time.perf_counter() - t0
-            ms = events.elapsed_ms(start, stop) / reps
-            kl.check(kl.wait())
-        src.close()
-        dst.close()
-        out[f"{name}_k{k}_n{n}"] = {"moved_bytes": 2 * half, "us": round(ms * 1e3, 3),
-                                    "gbps": round(2 * half / (ms * 1e-3) / 1e9, 1),
-                                    "host_us": round(host_s / reps * 1e6, 3)}
-    return out
 
 
 READ_SIZES = (("gate_gemv", q4_bytes(4096, 11008)), ("lm_head_gemv", q4_bytes(4096, 32000)),
@@ -659,8 +620,7 @@ def main() -> int:
         print(json.dumps({"read_ceiling": read_ceiling_leg(events, stream, device, args.read_reps)}), flush=True)
         return 0
     if args.only == "copy":
-        print(json.dumps({"copy": copy_leg(events, stream, device),
-                          "copy_ceiling": copy_ceiling_leg(events, stream, device, 300)}), flush=True)
+        print(json.dumps({"copy": copy_leg(events, stream, device)}), flush=True)
         return 0
 
     log("generating and uploading weights")
@@ -786,7 +746,6 @@ def main() -> int:
     native = native_leg(events, stream, device, args.native_reps) if args.native_reps > 0 else None
     common = common_leg(events, stream, device, args.common_reps) if args.common_reps > 0 else None
     i8 = i8_leg(kernel, events, stream, device, args.i8_reps) if args.i8_reps > 0 else None
-    ceiling = copy_ceiling_leg(events, stream, device, args.kernel_reps)
     read = read_ceiling_leg(events, stream, device, args.read_reps) if args.read_reps > 0 else None
     read_gbps = read["gate_gemv"]["best"]["gbps"] if read else None
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
@@ -839,7 +798,6 @@ def main() -> int:
         },
         "per_shape": per_shape,
         "read_ceiling": read,
-        "copy_ceiling": ceiling,
         "gemm_b512": gemm,
         "small_batch": small,
         "native_q4": native,

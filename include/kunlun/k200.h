@@ -33,10 +33,12 @@ void diagnostic_tensor(const char * name, const int64_t * dimensions = nullptr);
 void require(bool condition);
 int device_count(int * count);                       // reference k200.h:15
 void select(int device);                             // reference k200.h:16
-// Completes every operation submitted to the selected device (reference k200.h:17).
+// Completes every operation on the selected device, the library's and any
+// other HIP work of the process (hipDeviceSynchronize; reference k200.h:17).
 int wait();
 enum CopyKind { host_to_device, device_to_host, device_to_device };
-// Submits a copy on the selected device; wait() completes it (reference k200.h:18-19).
+// Copies on the selected device after the library's submitted work there and
+// completes before returning, in every direction (reference k200.h:18-19).
 int copy(void * dst, const void * src, size_t bytes, CopyKind kind);
 // Device-to-device copy between GPUs; completes before returning (reference k200.h:20).
 void peer(int dst_device, void * dst, int src_device, const void * src, size_t bytes);

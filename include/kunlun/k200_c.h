@@ -54,9 +54,11 @@ void kunlun_diagnostic_tensor(const char *name, const int64_t *dimensions);
 int kunlun_device_count(int *count);
 /* select() (reference include/kunlun/k200.h:16). */
 void kunlun_select(int device);
-/* wait() (reference include/kunlun/k200.h:17); returns a HIP status. */
+/* wait() (reference include/kunlun/k200.h:17): completes all work on the
+ * selected device (hipDeviceSynchronize); returns a HIP status. */
 int kunlun_wait(void);
-/* copy() (reference include/kunlun/k200.h:19); kind is a KUNLUN_*_TO_* value. */
+/* copy() (reference include/kunlun/k200.h:19); kind is a KUNLUN_*_TO_* value.
+ * Runs after the library's submitted work and completes before returning. */
 int kunlun_copy(void *dst, const void *src, size_t bytes, int kind);
 /* peer() (reference include/kunlun/k200.h:20). */
 void kunlun_peer(int dst_device, void *dst, int src_device, const void *src, size_t bytes);

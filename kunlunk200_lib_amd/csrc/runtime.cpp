@@ -142,9 +142,10 @@ int wait() {
     hipError_t status = hipGetDevice(&device);
     if (status != hipSuccess) return (int)status;
     detail::DeviceContext & ctx = detail::contexts[device];
-    if (!ctx.ready) return (int)hipDeviceSynchronize();
-    status = hipStreamSynchronize(ctx.stream);
-    if (status != hipSuccess) return (int)status;
+    // Every stream of the device, as the reference's xpu_wait() (reference
+    // src/k200.cpp:68): the library's own stream and the caller's HIP work.
+    status = hipDeviceSynchronize();
+    if (status != hipSuccess || !ctx.ready) return (int)status;
     if (ctx.status_pending) {
         int word = 0;
         status = hipMemcpy(&word, ctx.status, sizeof(word), hipMemcpyDeviceToHost);
@@ -169,8 +170,11 @@ int copy(void * dst, const void * src, size_t bytes, CopyKind kind) {
     const hipMemcpyKind direction = kind == host_to_device   ? hipMemcpyHostToDevice
                                     : kind == device_to_host ? hipMemcpyDeviceToHost
                                                              : hipMemcpyDeviceToDevice;
+    // Ordered after the library's submitted work on this device and complete
+    // on return in every direction, as the reference's synchronous
+    // xpu_memcpy (reference src/k200.cpp:69-75).
     hipError_t status = hipMemcpyAsync(dst, src, bytes, direction, ctx.stream);
-    if (status == hipSuccess && kind != device_to_device) status = hipStreamSynchronize(ctx.stream);
+    if (status == hipSuccess) status = hipStreamSynchronize(ctx.stream);
     return (int)status;
 }
 
