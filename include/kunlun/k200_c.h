@@ -208,7 +208,8 @@ void kunlun_matmul_swiglu(kunlun_kernel *kernel, int device, void *y, const void
 /* Route and tile knobs of matmul. Each knob is named by its environment
  * variable (KUNLUN_GEMM_MIN_BATCH, KUNLUN_Q4_MFMA_MIN, KUNLUN_Q4_MFMA_MAX,
  * KUNLUN_DENSE_MFMA_MIN, KUNLUN_DENSE_MFMA_MAX, KUNLUN_GEMM_TILE (BMxWN),
- * KUNLUN_GEMM_BN, KUNLUN_GEMV_GENERAL, KUNLUN_I8_FUSED_QUANT_LIMIT), which
+ * KUNLUN_GEMM_BN, KUNLUN_GEMV_GENERAL, KUNLUN_I8_FUSED_QUANT_LIMIT,
+ * KUNLUN_Q4_GEMV_PLANES), which
  * the library reads once, at the first matmul. kunlun_set_tuning sets a knob
  * from text in the variable's syntax; a NULL value restores the value read
  * from the environment. Returns 0, or -1 for an unknown name or a malformed
@@ -216,6 +217,27 @@ void kunlun_matmul_swiglu(kunlun_kernel *kernel, int device, void *y, const void
  * built-in choice) or -2 for an unknown name. */
 int kunlun_set_tuning(const char *name, const char *value);
 int kunlun_get_tuning(const char *name);
+
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): kunlun_matmul for KUNLUN_F32, KUNLUN_F16 and KUNLUN_Q4_0
+ * weights on the same routes and kernels, that allocates nothing. The
+ * scratch of the routes that need it (the batch >= 64 fp16-MFMA GEMM and the
+ * Q4_0 MFMA GEMV) is a fixed device array of KUNLUN_NOALLOC_SCRATCH_BYTES per
+ * GPU, held until the process ends; a call that needs more returns
+ * KUNLUN_NOALLOC_TOO_LARGE (the GEMM needs about 2 * batch * K bytes, so
+ * batch * K <= 8M fits). The caller passes device pointers for y, w and x
+ * and the stream to submit on (NULL: the null stream); `route` (optional)
+ * receives the kernel route's name. Makes `device` current for the calling
+ * thread and takes no library lock; completion is the caller's (stream or
+ * device synchronization). Calls that overlap on one GPU share its scratch
+ * array and race. Returns 0, KUNLUN_NOALLOC_INVALID for an argument
+ * kunlun_matmul would reject or an unsupported type (rowwise INT8), or a
+ * HIP status. */
+#define KUNLUN_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+enum { KUNLUN_NOALLOC_INVALID = -1, KUNLUN_NOALLOC_TOO_LARGE = -2 };
+int kunlun_matmul_noalloc(int device, void *y, const void *w, const void *x, int k, int n, int batch, int type,
+                          void *stream, const char **route);
 
 #ifdef __cplusplus
 }

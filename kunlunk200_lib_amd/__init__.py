@@ -63,6 +63,8 @@ C_FUNCTIONS = [
     ("kunlun_stream", _c_void_p, [_c_int]),
     ("kunlun_kernel_route", ctypes.c_char_p, [_c_void_p]),
     ("kunlun_set_tuning", _c_int, [ctypes.c_char_p, ctypes.c_char_p]),
+    ("kunlun_matmul_noalloc", _c_int, [_c_int, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int,
+                                       _c_void_p, ctypes.POINTER(ctypes.c_char_p)]),
     ("kunlun_get_tuning", _c_int, [ctypes.c_char_p]),
     ("kunlun_elementwise", None, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
                                   _c_int, ctypes.c_float]),
@@ -630,6 +632,19 @@ def version() -> str:
 
 def matmul_count(device: int) -> int:
     return load().kunlun_matmul_count(int(device))
+
+
+NOALLOC_SCRATCH_BYTES = 16 << 20
+NOALLOC_INVALID, NOALLOC_TOO_LARGE = -1, -2
+
+
+def matmul_noalloc(device: int, y, w, x, k: int, n: int, batch: int, type: WeightType, stream=None):
+    """kunlun_matmul_noalloc: matmul for F32/F16/Q4_0 without device allocation (no reference
+    counterpart). Submits on `stream` (None: the null stream); returns (status, route)."""
+    route = ctypes.c_char_p()
+    rc = load().kunlun_matmul_noalloc(int(device), _ptr(y), _ptr(w), _ptr(x), int(k), int(n), int(batch),
+                                      int(type), _ptr(stream), ctypes.byref(route))
+    return rc, (route.value.decode() if route.value else None)
 
 
 def set_tuning(name: str, value) -> None:

@@ -35,6 +35,13 @@ void * grow(int id, detail::DeviceContext & ctx, void *& ptr, size_t & size, siz
     return ptr;
 }
 
+} // namespace
+} // namespace kunlun
+
+namespace kk {
+
+// Route predicates, shared with the allocation-free entry point (noalloc.hip).
+//
 // Smallest batch that uses the fp16-MFMA prefill GEMM (F16 and Q4_0 weights);
 // smaller batches keep the F32-accumulate GEMV kernels.
 int gemm_min_batch() {
@@ -58,6 +65,15 @@ bool dense_mfma_batch(int batch) {
     const int max_b = std::min(16, kk::tuning_or(kk::kDenseMfmaMax, 16));
     return batch >= min_b && batch <= max_b;
 }
+
+} // namespace kk
+
+namespace kunlun {
+using kk::dense_mfma_batch;
+using kk::gemm_min_batch;
+using kk::q4_mfma_batch;
+
+namespace {
 
 // The reference's matmul argument rules (reference src/k200.cpp:271-275):
 // supported type, K % 32 == 0, K <= 16384, products that fit int, and a

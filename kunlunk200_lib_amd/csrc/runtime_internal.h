@@ -36,6 +36,19 @@ void note_route(const char * route);
 
 } // namespace detail
 
+} // namespace kunlun
+
+namespace kk {
+// matmul's route predicates (matmul.cpp): the smallest batch on the fp16-MFMA
+// GEMM, and the batch ranges of the Q4_0 (streamed: K % 256 == 0 and 16-byte
+// aligned weights) and the F32/F16 single-pass MFMA GEMVs.
+int gemm_min_batch();
+bool q4_mfma_batch(int batch, bool streamed);
+bool dense_mfma_batch(int batch);
+} // namespace kk
+
+namespace kunlun {
+
 struct Kernel::Impl {
     int id = -1;
     void * i8_workspace = nullptr;      // rowwise_i8 activation codes and maxima
