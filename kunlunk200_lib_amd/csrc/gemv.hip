@@ -275,10 +275,12 @@ __global__ __launch_bounds__(64 * WAVES) void q4_gemv_dot8(const uint8_t *__rest
     };
 
     if (items <= DEPTH) {
-        // every item is already in flight: consume them in issue order
+        // every item is already in flight: consume them in issue order. Items
+        // past the wave's own (clamped loads of its last item) are computed
+        // too and their results dropped (no row below `rows`), so the path has
+        // no branch and each item waits only for its own loads.
 #pragma unroll
-        for (int d = 0; d < DEPTH; ++d)
-            if (d < items) compute_item(d, ring[d]);
+        for (int d = 0; d < DEPTH; ++d) compute_item(d, ring[d]);
     } else {
         // ring of DEPTH items in flight: after item i is decoded its buffer is
         // refilled with item i + DEPTH (clamped: past the end it re-reads the
@@ -291,6 +293,10 @@ __global__ __launch_bounds__(64 * WAVES) void q4_gemv_dot8(const uint8_t *__rest
                 load_item(item + DEPTH, ring[d]);
             }
         }
+        // the ring's last refills (clamped re-reads) end here, so that where
+        // this path joins the other the compiler's memory-counter waits of the
+        // other path stay exact
+        __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
     }
 
     // 5. row results: one coalesced store per batch column
@@ -498,6 +504,10 @@ hipError_t launch_q4_dot8_cfg(const uint8_t *w, const uint8_t *w2, const float *
     return hipGetLastError();
 }
 
+// Six activation digits (F = 22). Five (F = 18) meet the 1e-4 ||x|| ||w||
+// bound and run 5-8% faster, but miss the reference's own 1e-3 (1 + |gold|)
+// tolerance on its large-magnitude fixture activations (pattern 4), which
+// the F32-exact reference kernel meets.
 template <int B, int SLICES, int DEPTH, bool PAIR = false>
 hipError_t launch_q4_dot8_depth(const uint8_t *w, const uint8_t *w2, const float *x, float *y, int k, int n,
                                 int y_stride, hipStream_t stream, const DeviceInfo &info) {
@@ -507,9 +517,14 @@ hipError_t launch_q4_dot8_depth(const uint8_t *w, const uint8_t *w2, const float
 template <int B, int SLICES, bool PAIR>
 hipError_t launch_q4_dot8_slices(const uint8_t *w, const uint8_t *w2, const float *x, float *y, int k, int n,
                                  int y_stride, hipStream_t stream, const DeviceInfo &info) {
-    // items in flight per wave: 3 single rows at batch 1; 2 when an item is
-    // twice the work (two batch columns, or a gate/up row pair)
-    if (B == 2 || PAIR) return launch_q4_dot8_depth<B, SLICES, 2, PAIR>(w, w2, x, y, k, n, y_stride, stream, info);
+    // items in flight per wave: 3 single-column items, 2 when an item is twice
+    // the work (two batch columns, or a gate/up row pair) or when a wave owns
+    // at most 2 items (then all of them are in flight and a third would be a
+    // wasted re-read: 4.48 vs 4.9 us at K4096 x N4096). 8 waves per CU.
+    const long long waves = std::max<long long>(1, std::min<long long>(n, static_cast<long long>(info.cus) * 8));
+    const long long items = (n + waves - 1) / waves * SLICES;
+    if (B == 2 || PAIR || items <= 2)
+        return launch_q4_dot8_depth<B, SLICES, 2, PAIR>(w, w2, x, y, k, n, y_stride, stream, info);
     return launch_q4_dot8_depth<B, SLICES, 3, PAIR>(w, w2, x, y, k, n, y_stride, stream, info);
 }
 
