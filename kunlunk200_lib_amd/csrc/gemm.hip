@@ -228,44 +228,71 @@ __device__ __forceinline__ half8 decode_q4_scaled(uint32_t n, uint32_t dbits) {
     return o;
 }
 
-// The correction for blocks with subnormal scales (note_tiny_scale): for
-// weight row `wrow` (`blocks` Q4_0 blocks) and the R activation rows
-// row_of(0 .. R-1) of x16 (block order, row stride k_pad), adds to out[r] the
-// sum over the row's blocks with a subnormal scale d = +-m * 2^-24 of
-// x16 . (v - decode(v)), v = (q - 8) / 8 * d in F32 and decode(nibble dword,
-// scale bits) the fp16 values the kernel's decode gave them (each one
-// rounding of the exact (q - 8) / 8 * d, so the same in any context). v,
-// decode(v) (both on the 2^-27 grid, below 2^-13) and their difference are
-// exact in F32; the products and sums round. A cold path (byte loads, one
-// block and one nibble dword at a time).
+// Blocks with subnormal scales (note_tiny_scale), found and corrected only
+// in a workgroup that met one. kTinyMaskWords words per B-tile row mark its
+// blocks with a subnormal scale (K <= 16384: at most 512 blocks).
+constexpr int kTinyMaskWords = 16;
+
+// All `threads` threads of the workgroup: masks[j * kTinyMaskWords + b / 32]
+// bit b % 32 is set when block b of tile row j (row_ptr(j); nullptr past the
+// matrix) has a subnormal scale. Two workgroup barriers.
+template <typename RowPtr>
+__device__ void build_tiny_masks(int rows, int blocks, RowPtr row_ptr, uint32_t *masks, int threads) {
+    for (int i = threadIdx.x; i < rows * kTinyMaskWords; i += threads) masks[i] = 0u;
+    __syncthreads();
+    for (int i = threadIdx.x; i < rows * blocks; i += threads) {
+        const int j = i / blocks, b = i - j * blocks;
+        const uint8_t *wrow = row_ptr(j);
+        if (!wrow) continue;
+        const uint32_t bits = wrow[18 * b] | (static_cast<uint32_t>(wrow[18 * b + 1]) << 8);
+        if ((bits & 0x7c00u) == 0 && (bits & 0x3ffu) != 0)
+            atomicOr(&masks[j * kTinyMaskWords + (b >> 5)], 1u << (b & 31));
+    }
+    __syncthreads();
+}
+
+// The correction for the marked blocks of one weight row `wrow` (mask: its
+// kTinyMaskWords words) and the R activation rows row_of(0 .. R-1) of x16
+// (block order, row stride k_pad): adds to out[r], block by block in
+// increasing order, x16 . (v - decode(v)) with v = (q - 8) / 8 * d in F32,
+// d = +-m * 2^-24 the block's subnormal scale, and decode(nibble dword, scale
+// bits) the fp16 values the kernel's decode gave the block (each one rounding
+// of the exact (q - 8) / 8 * d, so the same in any context). v, decode(v)
+// (both on the 2^-27 grid, below 2^-13) and their difference are exact in
+// F32; the products and sums round.
 template <int R, typename RowOf, typename Decode>
-__device__ void tiny_scale_dots(const uint8_t *wrow, int blocks, const _Float16 *x16, int k_pad, RowOf row_of,
-                                Decode decode, float (&out)[R]) {
+__device__ void tiny_scale_dots(const uint8_t *wrow, const uint32_t *mask, int blocks, const _Float16 *x16, int k_pad,
+                                RowOf row_of, Decode decode, float (&out)[R]) {
 #pragma unroll 1
-    for (int b = 0; b < blocks; ++b) {
-        const uint8_t *blk = wrow + 18 * b;
-        const uint32_t bits = blk[0] | (static_cast<uint32_t>(blk[1]) << 8);
-        if ((bits & 0x7c00u) != 0 || (bits & 0x3ffu) == 0) continue;
-        const float d = ldexpf(static_cast<float>(bits & 0x3ffu), -27) * ((bits & 0x8000u) ? -1.0f : 1.0f);   // d / 8
+    for (int word = 0; word < (blocks + 31) / 32; ++word) {
+        uint32_t bitsleft = mask[word];
 #pragma unroll 1
-        for (int i = 0; i < 4; ++i) {   // nibble dword i -> block-order positions 8i .. 8i+7
-            const uint8_t *nb = blk + 2 + 4 * i;
-            const uint32_t nib = nb[0] | static_cast<uint32_t>(nb[1]) << 8 | static_cast<uint32_t>(nb[2]) << 16 |
-                                 static_cast<uint32_t>(nb[3]) << 24;
-            const half8 dec = decode(nib, bits);
-            float wv[8];
+        while (bitsleft) {
+            const int b = 32 * word + __builtin_ctz(bitsleft);
+            bitsleft &= bitsleft - 1u;
+            const uint8_t *blk = wrow + 18 * b;
+            const uint32_t bits = blk[0] | (static_cast<uint32_t>(blk[1]) << 8);
+            const float d = ldexpf(static_cast<float>(bits & 0x3ffu), -27) * ((bits & 0x8000u) ? -1.0f : 1.0f);   // d / 8
+#pragma unroll 1
+            for (int i = 0; i < 4; ++i) {   // nibble dword i -> block-order positions 8i .. 8i+7
+                const uint8_t *nb = blk + 2 + 4 * i;
+                const uint32_t nib = nb[0] | static_cast<uint32_t>(nb[1]) << 8 | static_cast<uint32_t>(nb[2]) << 16 |
+                                     static_cast<uint32_t>(nb[3]) << 24;
+                const half8 dec = decode(nib, bits);
+                float wv[8];
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const uint32_t byte = nb[(t & 1) << 1 | (t & 2) >> 1];   // bytes 0, 2, 1, 3
-                const uint32_t q = t < 4 ? byte & 15u : byte >> 4;
-                wv[t] = (static_cast<float>(q) - 8.0f) * d - static_cast<float>(dec[t]);
-            }
+                for (int t = 0; t < 8; ++t) {
+                    const uint32_t byte = nb[(t & 1) << 1 | (t & 2) >> 1];   // bytes 0, 2, 1, 3
+                    const uint32_t q = t < 4 ? byte & 15u : byte >> 4;
+                    wv[t] = (static_cast<float>(q) - 8.0f) * d - static_cast<float>(dec[t]);
+                }
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const half8 xv = *reinterpret_cast<const half8 *>(x16 + static_cast<size_t>(row_of(r)) * k_pad +
-                                                                  32 * b + 8 * i);
+                for (int r = 0; r < R; ++r) {
+                    const half8 xv = *reinterpret_cast<const half8 *>(x16 + static_cast<size_t>(row_of(r)) * k_pad +
+                                                                      32 * b + 8 * i);
 #pragma unroll
-                for (int t = 0; t < 8; ++t) out[r] += static_cast<float>(xv[t]) * wv[t];
+                    for (int t = 0; t < 8; ++t) out[r] += static_cast<float>(xv[t]) * wv[t];
+                }
             }
         }
     }
@@ -504,10 +531,18 @@ __global__ __launch_bounds__(kGemmThreads) void mfma_gemm(const uint8_t *__restr
                 for (int r = 0; r < 16; ++r) red[(((sw * 2 + it) * kNT + jt) * 16 + r) * kWave + lane] = acc[it][jt][r];
     }
     const bool any_tiny = __syncthreads_or(tiny) != 0;   // workgroup-uniform
+    // subnormal-scale block masks of the B tile rows, after the k-group exchange
+    uint32_t *tiny_masks = reinterpret_cast<uint32_t *>(red + 2 * 4 * kNT * 16 * kWave);
+    static_assert(2 * 4 * kNT * 16 * kWave * 4 + BN * kTinyMaskWords * 4 <= gemm_lds_bytes<BN>(), "mask space");
+    if (!F16W && any_tiny)
+        build_tiny_masks(BN, blocks, [&](int j) -> const uint8_t * {
+            const int n = n0 + b_column(j);
+            return n < n_rows ? (b_matrix(j) ? w2 : w) + static_cast<size_t>(n) * row_bytes : nullptr;
+        }, tiny_masks, kGemmThreads);
     if (kh == 1) return;
     const float wscale = F16W ? 1.0f : 8.0f;
-    // Q4_0 blocks with subnormal scales (skipped by the decode) into acc, in
-    // F32: lane column n of MFMA tile jt, rows m(it, r).
+    // Q4_0 blocks with subnormal scales (given the decode's fp16 rounding)
+    // corrected in F32 into acc: lane column n of MFMA tile jt, rows m(it, r).
     if (!F16W && any_tiny) {
 #pragma unroll
         for (int jt = 0; jt < kNT; ++jt) {
@@ -515,6 +550,7 @@ __global__ __launch_bounds__(kGemmThreads) void mfma_gemm(const uint8_t *__restr
             const int n = PAIR ? n0 + wn * 32 + (lane & 31) : n0 + j;
             if (n >= n_rows) continue;
             const uint8_t *wrow = (PAIR && jt == 1 ? w2 : w) + static_cast<size_t>(n) * row_bytes;
+            const uint32_t *mask = tiny_masks + j * kTinyMaskWords;
 #pragma unroll
             for (int it = 0; it < 2; ++it) {
 #pragma unroll
@@ -525,7 +561,7 @@ __global__ __launch_bounds__(kGemmThreads) void mfma_gemm(const uint8_t *__restr
                         bool unused = false;
                         return decode_q4_dword(nib, q4_scale8(bits, true, unused));
                     };
-                    tiny_scale_dots<4>(wrow, blocks, x16, k_pad, row_of, decode, fix);
+                    tiny_scale_dots<4>(wrow, mask, blocks, x16, k_pad, row_of, decode, fix);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) acc[it][jt][4 * c + r] += fix[r];
                 }
@@ -859,22 +895,30 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
                     tile_lds[(rg * 16 + 4 * g + r) * kTs + wn * WN + cg * 16 + c16] = acc[rg][cg][r];
     }
     if (__syncthreads_or(tiny)) {   // workgroup-uniform
-        // Q4_0 blocks with subnormal scales (skipped by the decode), in F32,
-        // into k-group 1's sums: work item -> B row j of the tile and
-        // activation rows 8p .. 8p+7.
+        // Q4_0 blocks with subnormal scales (given the decode's fp16
+        // rounding) corrected in F32 into k-group 1's sums: the marked blocks
+        // of each B tile row j, for activation rows 8p .. 8p+7 per work item.
         static_assert(BM % 8 == 0, "fixup rows");
+        static_assert(S::XferBytes + S::BN * kTinyMaskWords * 4 <= S::RingBytes, "mask space");
+        uint32_t *tiny_masks = reinterpret_cast<uint32_t *>(ql_lds + S::XferBytes);
+        const int nblocks = static_cast<int>(row_bytes / 18);
+        build_tiny_masks(S::BN, nblocks, [&](int j) -> const uint8_t * {
+            const int h = PAIR ? j / (S::BN / 2) : 0, jr = PAIR ? j % (S::BN / 2) : j;
+            return n0 + jr < n_rows ? (h ? w2 : w) + static_cast<size_t>(n0 + jr) * row_bytes : nullptr;
+        }, tiny_masks, kQlThreads);
         for (int item = threadIdx.x; item < S::BN * (BM / 8); item += kQlThreads) {
             const int j = item % S::BN, p8 = item / S::BN;
             const int h = PAIR ? j / (S::BN / 2) : 0, jr = PAIR ? j % (S::BN / 2) : j;   // matrix, row in it
             const int col = PAIR ? (jr / (WN / 2)) * WN + h * (WN / 2) + jr % (WN / 2) : j;   // tile column
             if (n0 + jr >= n_rows) continue;
             const uint8_t *wrow = (h ? w2 : w) + static_cast<size_t>(n0 + jr) * row_bytes;
+            const uint32_t *mask = tiny_masks + j * kTinyMaskWords;
             auto row_of = [&](int r) { return m0 + 8 * p8 + r; };
             float fix[8];
 #pragma unroll
             for (int r = 0; r < 8; ++r) fix[r] = 0.0f;
             auto decode = [](uint32_t nib, uint32_t bits) { return decode_q4_scaled(nib, bits); };
-            tiny_scale_dots<8>(wrow, static_cast<int>(row_bytes / 18), x16, k_pad, row_of, decode, fix);
+            tiny_scale_dots<8>(wrow, mask, nblocks, x16, k_pad, row_of, decode, fix);
 #pragma unroll
             for (int r = 0; r < 8; ++r) tile_lds[(8 * p8 + r) * kTs + col] += fix[r];
         }
