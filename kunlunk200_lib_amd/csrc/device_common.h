@@ -6,6 +6,16 @@
 
 namespace kk {
 
+// Workgroup barrier for LDS data only: waits for this wave's LDS operations
+// (lgkmcnt) but not for its global loads, which stay in flight across it.
+// (__syncthreads also waits for every outstanding global load of the wave.)
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+
 constexpr int kWave = 64;
 
 // IEEE binary16 bits -> binary32 (v_cvt_f32_f16): exact, subnormals included,

@@ -54,13 +54,15 @@ __device__ __forceinline__ void flag_nonfinite(int *status) {
 }
 
 // Block-wide max over float values held by each thread; result on all threads.
-template <int Threads>
+// LDS_ONLY: the barriers wait for LDS operations only, so global loads issued
+// before the call stay in flight.
+template <int Threads, bool LDS_ONLY = false>
 __device__ float block_max(float v, float *scratch) {
     v = kk::wave_max(v);
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    __syncthreads();
+    if (LDS_ONLY) kk::lds_barrier(); else __syncthreads();
     if (lane == 0) scratch[wave] = v;
-    __syncthreads();
+    if (LDS_ONLY) kk::lds_barrier(); else __syncthreads();
     float m = 0.0f;
 #pragma unroll
     for (int i = 0; i < Threads / kWave; ++i) m = fmaxf(m, scratch[i]);
@@ -449,17 +451,18 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void i8_gemv_ksplit(const int8_
 // so the 16 MFMA rows read distinct banks, then runs the K-split product of
 // i8_gemv_ksplit<1> with A read from LDS.
 constexpr int kFusedGemvCount = 16384;
-constexpr int kFusedGemvGroups = kFusedGemvCount / 4 / (kGemvWaves * kWave);   // 8 float4 per thread
-__global__ __launch_bounds__(kGemvWaves * kWave) void i8_gemv_fused(const float *__restrict__ x,
+template <int WAVES>
+__global__ __launch_bounds__(WAVES * kWave) void i8_gemv_fused(const float *__restrict__ x,
                                                                    const int8_t *__restrict__ w,
                                                                    const float *__restrict__ scales,
                                                                    const float *__restrict__ maxima,
                                                                    float *__restrict__ y, int k, int n, int batch,
                                                                    int *status) {
-    constexpr int kThreadsF = kGemvWaves * kWave;
-    __shared__ float scratch[kGemvWaves];
+    constexpr int kThreadsF = WAVES * kWave;
+    constexpr int kFusedGemvGroups = kFusedGemvCount / 4 / kThreadsF;   // float4 per thread
+    __shared__ float scratch[WAVES];
     __shared__ __align__(16) int8_t table[2 * kFusedGemvCount + 16 * 16];   // [2 batch][k + 16]
-    __shared__ int32x4 part[kGemvWaves - 1][kWave];
+    __shared__ int32x4 part[WAVES - 1][kWave];
     const int lane = threadIdx.x & (kWave - 1);
     const int wid = threadIdx.x >> 6;
     const int g = lane >> 4, c = lane & 15;
@@ -468,20 +471,21 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void i8_gemv_fused(const float 
     const int groups4 = batch * k / 4;
     const int n0 = blockIdx.x * 16;
     const int steps = (k + 63) / 64;
-    const int per = (steps + kGemvWaves - 1) / kGemvWaves;
+    const int per = (steps + WAVES - 1) / WAVES;
     const int s0 = wid * per, s1 = min(steps, s0 + per);
     const int8_t *brow = w + static_cast<size_t>(min(n0 + c, n - 1)) * k;
     constexpr int kChunk = 8;
+    // branch-free (clamped address, zeroed after the load), so that the
+    // memory-counter waits stay exact and the chunk stays in flight across the
+    // quantization below
     auto load_b = [&](int sc, int32x4 (&bf)[kChunk]) {
 #pragma unroll
         for (int t = 0; t < kChunk; ++t) {
             const int kk0 = (sc + t) * 64 + 16 * g;
-            if (sc + t < s1 && kk0 < k) {
-                const kk::u32x4_a4 b = kk::load_u32x4(reinterpret_cast<const uint32_t *>(brow + kk0));
-                bf[t] = int32x4{static_cast<int>(b.x), static_cast<int>(b.y), static_cast<int>(b.z), static_cast<int>(b.w)};
-            } else {
-                bf[t] = int32x4{0, 0, 0, 0};
-            }
+            const bool live = sc + t < s1 && kk0 < k;
+            const kk::u32x4_a4 b = kk::load_u32x4(reinterpret_cast<const uint32_t *>(brow + min(kk0, k - 16)));
+            bf[t] = live ? int32x4{static_cast<int>(b.x), static_cast<int>(b.y), static_cast<int>(b.z), static_cast<int>(b.w)}
+                         : int32x4{0, 0, 0, 0};
         }
     };
 
@@ -492,7 +496,7 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void i8_gemv_fused(const float 
 #pragma unroll
     for (int t = 0; t < kFusedGemvGroups; ++t) {
         const int q = static_cast<int>(threadIdx.x) + kThreadsF * t;
-        v[t] = q < groups4 ? load_x4(x, q) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        v[t] = load_x4(x, min(q, groups4 - 1));   // branch-free, as the weight loads; slots past X unused
     }
     __builtin_amdgcn_sched_barrier(0);
     int32x4 bf[kChunk];
@@ -502,11 +506,14 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void i8_gemv_fused(const float 
     bool bad = false;
 #pragma unroll
     for (int t = 0; t < kFusedGemvGroups; ++t) {
-        bad |= !finite4(v[t]);
-        m = fmaxf(m, absmax4(v[t]));
+        const bool in_x = static_cast<int>(threadIdx.x) + kThreadsF * t < groups4;
+        bad |= in_x && !finite4(v[t]);
+        m = fmaxf(m, in_x ? absmax4(v[t]) : 0.0f);
     }
     if (bad) flag_nonfinite(status);
-    float max0 = block_max<kThreadsF>(m, scratch);
+    // the barriers of the quantization wait for LDS only: the weight chunk
+    // stays in flight until its MFMAs
+    float max0 = block_max<kThreadsF, true>(m, scratch);
     if (max0 == 0.0f) max0 = 1.0f;
     float m1 = 0.0f;
 #pragma unroll
@@ -520,7 +527,7 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void i8_gemv_fused(const float 
         m1 = fmaxf(m1, fmaxf(fmaxf(fabsf(residual_of(v[t].x, a, max0)), fabsf(residual_of(v[t].y, b, max0))),
                              fmaxf(fabsf(residual_of(v[t].z, cc, max0)), fabsf(residual_of(v[t].w, d, max0)))));
     }
-    float max1 = block_max<kThreadsF>(m1, scratch);
+    float max1 = block_max<kThreadsF, true>(m1, scratch);
     if (max1 == 0.0f) max1 = 1.0f;
 #pragma unroll
     for (int t = 0; t < kFusedGemvGroups; ++t) {
@@ -531,7 +538,7 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void i8_gemv_fused(const float 
         *reinterpret_cast<uint32_t *>(table + (2 * row + 1) * stride + j) =
             pack_codes(q1(v[t].x), q1(v[t].y), q1(v[t].z), q1(v[t].w));
     }
-    __syncthreads();
+    kk::lds_barrier();
 
     // 2. K-split int8 MFMA product (A from the table)
     const int8_t *arow = table + (c < rows ? c : 0) * stride;
@@ -550,7 +557,7 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void i8_gemv_fused(const float 
     __syncthreads();
     if (wid > 0) return;
 #pragma unroll
-    for (int vv = 0; vv < kGemvWaves - 1; ++vv) acc += part[vv][lane];
+    for (int vv = 0; vv < WAVES - 1; ++vv) acc += part[vv][lane];
     const int r = n0 + c;
     if (r >= n) return;
     const float scale0 = max0 / 127.0f;
@@ -562,6 +569,142 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void i8_gemv_fused(const float 
         const int b = 2 * g + h;
         if (b < batch) y[static_cast<size_t>(b) * n + r] = combine(acc[2 * h], acc[2 * h + 1], wmax, scale0, scale1, rs);
     }
+}
+
+// ---------------------------------------------------------------------------
+// Batch-1 rowwise_i8 GEMV for K <= 1024 * CH (K % 32 == 0). A workgroup of 8
+// waves
+//  1. issues the loads of X (8 values per thread), then those of each
+//     wave's R weight rows at most (a row is CH fully coalesced 1 KB loads:
+//     lane l reads bytes 1024 i + 16 l);
+//  2. quantizes X in the reference's two passes (reference
+//     src/k200.cpp:212-225) with workgroup maxima into an LDS code table;
+//     its barriers wait for LDS only, so the weights stay in flight;
+//  3. per wave and row: int32 dot products of the row's bytes with the
+//     lane's codes (read once from the table, v_dot4_i32_i8), wave sums and
+//     the combine (reference kernels/kunlun-combine.xpu:10-19). The int32
+//     sums are exact in any order, so Y equals the MFMA routes' bit for bit.
+// All global loads are branch-free (clamped addresses; code slots past K are
+// zero, rows past the wave's own are dropped).
+__device__ __forceinline__ int wave_sum_int(int v) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, kWave);
+    return v;
+}
+
+constexpr int kRowsThreads = 512;
+constexpr int kRowsWaves = kRowsThreads / kWave;
+
+template <int CH, int R>
+__global__ __launch_bounds__(kRowsThreads) void i8_gemv_rows(const float *__restrict__ x,
+                                                             const int8_t *__restrict__ w,
+                                                             const float *__restrict__ scales,
+                                                             const float *__restrict__ maxima,
+                                                             float *__restrict__ y, int k, int n, int rows_base,
+                                                             int rows_rem, int *status) {
+    static_assert(CH * 1024 <= 8 * kRowsThreads, "X: 8 values per thread");
+    __shared__ float scratch[kRowsWaves];
+    __shared__ __align__(16) uint32_t codes[2][CH * 256];   // q0, q1 rows of CH KiB
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = blockIdx.x * kRowsWaves + (threadIdx.x >> 6);
+    const int r_begin = wave * rows_base + min(wave, rows_rem);
+    const int rows = rows_base + (wave < rows_rem ? 1 : 0);     // 0 .. R
+    // 1. activations (thread t: values 8t .. 8t+7), then the weight rows: loads
+    //    return in issue order, so X arrives first and is quantized while the
+    //    rows are still in flight
+    const int x0 = min(8 * static_cast<int>(threadIdx.x), k - 8);
+    const float4 xa = load_x4(x + x0, 0), xb = load_x4(x + x0, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    kk::u32x4_a4 wv[R][CH];
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        const int r = max(0, min(r_begin + min(j, rows - 1), n - 1));
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int off = min(1024 * i + 16 * lane, k - 16);
+            wv[j][i] = kk::load_u32x4(reinterpret_cast<const uint32_t *>(w + static_cast<size_t>(r) * k + off));
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const bool in_k = 8 * static_cast<int>(threadIdx.x) < k;
+    float v[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+    // 2. two-pass quantization, workgroup maxima over LDS-only barriers
+    float m = 0.0f;
+    bool bad = false;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        v[t] = in_k ? v[t] : 0.0f;
+        bad |= !isfinite(v[t]);
+        m = fmaxf(m, fabsf(v[t]));
+    }
+    if (bad) flag_nonfinite(status);
+    float max0 = block_max<kRowsThreads, true>(m, scratch);
+    if (max0 == 0.0f) max0 = 1.0f;
+    int q0[8];
+    float m1 = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        q0[t] = quant_primary(v[t], max0);
+        v[t] = residual_of(v[t], q0[t], max0);
+        m1 = fmaxf(m1, fabsf(v[t]));
+    }
+    float max1 = block_max<kRowsThreads, true>(m1, scratch);
+    if (max1 == 0.0f) max1 = 1.0f;
+    if (2 * static_cast<int>(threadIdx.x) < CH * 256) {           // code dwords 2t, 2t+1 (zero past K)
+        codes[0][2 * threadIdx.x] = pack_codes(q0[0], q0[1], q0[2], q0[3]);
+        codes[0][2 * threadIdx.x + 1] = pack_codes(q0[4], q0[5], q0[6], q0[7]);
+        codes[1][2 * threadIdx.x] = pack_codes(quant_residual(v[0], max1), quant_residual(v[1], max1),
+                                               quant_residual(v[2], max1), quant_residual(v[3], max1));
+        codes[1][2 * threadIdx.x + 1] = pack_codes(quant_residual(v[4], max1), quant_residual(v[5], max1),
+                                                   quant_residual(v[6], max1), quant_residual(v[7], max1));
+    }
+    kk::lds_barrier();
+    // 3. the lane's codes (16 per chunk and component), then the rows
+    uint4 c0[CH], c1[CH];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+        c0[i] = *reinterpret_cast<const uint4 *>(&codes[0][256 * i + 4 * lane]);
+        c1[i] = *reinterpret_cast<const uint4 *>(&codes[1][256 * i + 4 * lane]);
+    }
+    const float scale0 = max0 / 127.0f;
+    const float scale1 = max1 / 127.0f;
+    const float wmax = maxima[0] / 127.0f;
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        int p = 0, q = 0;
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const bool live = 1024 * i + 16 * lane < k;         // clamped slots: zero codes already, weights not
+            const uint32_t a0 = live ? c0[i].x : 0u, a1 = live ? c0[i].y : 0u, a2 = live ? c0[i].z : 0u,
+                           a3 = live ? c0[i].w : 0u;
+            const uint32_t b0 = live ? c1[i].x : 0u, b1 = live ? c1[i].y : 0u, b2 = live ? c1[i].z : 0u,
+                           b3 = live ? c1[i].w : 0u;
+            p = __builtin_amdgcn_sdot4(static_cast<int>(wv[j][i][0]), static_cast<int>(a0), p, false);
+            p = __builtin_amdgcn_sdot4(static_cast<int>(wv[j][i][1]), static_cast<int>(a1), p, false);
+            p = __builtin_amdgcn_sdot4(static_cast<int>(wv[j][i][2]), static_cast<int>(a2), p, false);
+            p = __builtin_amdgcn_sdot4(static_cast<int>(wv[j][i][3]), static_cast<int>(a3), p, false);
+            q = __builtin_amdgcn_sdot4(static_cast<int>(wv[j][i][0]), static_cast<int>(b0), q, false);
+            q = __builtin_amdgcn_sdot4(static_cast<int>(wv[j][i][1]), static_cast<int>(b1), q, false);
+            q = __builtin_amdgcn_sdot4(static_cast<int>(wv[j][i][2]), static_cast<int>(b2), q, false);
+            q = __builtin_amdgcn_sdot4(static_cast<int>(wv[j][i][3]), static_cast<int>(b3), q, false);
+        }
+        p = wave_sum_int(p);
+        q = wave_sum_int(q);
+        const int r = r_begin + j;
+        if (lane == 0 && j < rows && r < n) y[r] = combine(p, q, wmax, scale0, scale1, scales[r]);
+    }
+}
+
+template <int CH, int R>
+hipError_t launch_i8_rows(const float *x, const int8_t *w, const float *scales, const float *maxima, float *y, int k,
+                          int n, int waves, int *status, hipStream_t stream) {
+    const int groups = (waves + kRowsWaves - 1) / kRowsWaves;
+    const int all = groups * kRowsWaves;                        // every wave of the grid takes rows
+    const int rows_base = n / all, rows_rem = n % all;
+    if (rows_base + (rows_rem ? 1 : 0) > R) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((i8_gemv_rows<CH, R>), dim3(groups), dim3(kRowsThreads), 0, stream, x, w, scales, maxima, y, k,
+                       n, rows_base, rows_rem, status);
+    return hipGetLastError();
 }
 
 // Batch > 64, K % 128 == 0: LDS-staged int8 GEMM. Workgroup tile: 128 code
@@ -791,6 +934,31 @@ extern "C" int kk_i8_matmul(const void *workspace, const int8_t *w, const float 
     return launch_i8<4, 4>(ws.codes, w, scales, maxima, ws.final_max, y, k, n, batch, stream);
 }
 
+extern "C" int kk_i8_gemv_rows_supported(int k, int batch) {
+    return batch == 1 && k >= 32 && (k % 32) == 0 && k <= 4096;
+}
+
+// Waves: 8 per CU (measured at K4096 x N4096: 6.3 us; 16 and 32 per CU with
+// one row each: 6.8 and 6.9 us), more when a wave would own more than 4 rows;
+// 2 rows in flight per wave where that covers them.
+extern "C" int kk_i8_gemv_rows(const float *x, const int8_t *w, const float *scales, const float *maxima, float *y,
+                               int k, int n, int cus, int *status, hipStream_t stream) {
+    if (!x || !w || !scales || !maxima || !y || !status || n <= 0 || cus <= 0 || !kk_i8_gemv_rows_supported(k, 1))
+        return hipErrorInvalidValue;
+    const int waves = static_cast<int>(std::min<long long>(n, std::max<long long>(static_cast<long long>(cus) * 8,
+                                                                                  (n + 3) / 4)));
+    const int per_wave = (n + waves - 1) / waves;
+    const int ch = (k + 1023) / 1024;
+#define KK_I8_ROWS(CH)                                                                                   \
+    if (ch <= CH) return per_wave <= 2 ? launch_i8_rows<CH, 2>(x, w, scales, maxima, y, k, n, waves, status, stream) \
+                                       : launch_i8_rows<CH, 4>(x, w, scales, maxima, y, k, n, waves, status, stream);
+    KK_I8_ROWS(1)
+    KK_I8_ROWS(2)
+    KK_I8_ROWS(4)
+#undef KK_I8_ROWS
+    return hipErrorInvalidValue;
+}
+
 extern "C" int kk_i8_gemv_fused_supported(int k, int batch) {
     return k > 0 && (k % 32) == 0 && batch >= 1 && batch <= 8 && static_cast<long long>(batch) * k <= kFusedGemvCount;
 }
@@ -799,7 +967,7 @@ extern "C" int kk_i8_gemv_fused(const float *x, const int8_t *w, const float *sc
                                 int k, int n, int batch, int *status, hipStream_t stream) {
     if (!x || !w || !scales || !maxima || !y || !status || n <= 0 || !kk_i8_gemv_fused_supported(k, batch))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(i8_gemv_fused, dim3((n + 15) / 16), dim3(kGemvWaves * kWave), 0, stream, x, w, scales, maxima,
-                       y, k, n, batch, status);
+    hipLaunchKernelGGL(i8_gemv_fused<kGemvWaves>, dim3((n + 15) / 16), dim3(kGemvWaves * kWave), 0, stream, x, w,
+                       scales, maxima, y, k, n, batch, status);
     return hipGetLastError();
 }

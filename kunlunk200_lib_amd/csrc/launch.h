@@ -100,6 +100,11 @@ int kk_common_gemm(const void *w, const void *tiled, const void *row_scales, flo
 // rowwise_i8 at batch 1..8 with batch * K <= 16384, quantization and product
 // in one launch (no workspace); the non-finite activation flag goes to
 // `status` as kk_i8_quantize's does.
+// Batch-1 rowwise_i8 (K % 32 == 0, K <= 4096): each wave quantizes X itself and
+// streams whole weight rows with coalesced loads; int32 dot products by v_dot4.
+int kk_i8_gemv_rows_supported(int k, int batch);
+int kk_i8_gemv_rows(const float *x, const int8_t *w, const float *scales, const float *maxima, float *y, int k, int n,
+                    int cus, int *status, hipStream_t stream);
 int kk_i8_gemv_fused_supported(int k, int batch);
 int kk_i8_gemv_fused(const float *x, const int8_t *w, const float *scales, const float *maxima, float *y, int k, int n,
                      int batch, int *status, hipStream_t stream);

@@ -122,6 +122,17 @@ void matmul(Kernel & kernel, int id, void * y, const void * w, const void * x, i
     impl.id = id;
     if (type == WeightType::rowwise_i8) {
         require(((uintptr_t)w & 3) == 0 && ((uintptr_t)scales & 3) == 0 && ((uintptr_t)maximum & 3) == 0);
+        if (kk_i8_gemv_rows_supported(k, batch)) {
+            detail::check_hip((hipError_t)kk_i8_gemv_rows(static_cast<const float *>(x), static_cast<const int8_t *>(w),
+                                                          scales, maximum, static_cast<float *>(y), k, n, ctx.cus,
+                                                          ctx.status, ctx.stream),
+                              "kk_i8_gemv_rows");
+            ctx.status_pending = true;
+            impl.route = "i8_rows_gemv";
+            detail::last_route = impl.route;
+            detail::count_matmul(id);
+            return;
+        }
         if (kk_i8_gemv_fused_supported(k, batch)) {
             detail::check_hip((hipError_t)kk_i8_gemv_fused(static_cast<const float *>(x),
                                                            static_cast<const int8_t *>(w), scales, maximum,
