@@ -89,6 +89,26 @@ __device__ __forceinline__ int round_clamp(float value, int limit) {
     return q;
 }
 
+// Eight Q4_0 values of nibble dword `qs` (its bytes j = 0..3 hold values j in
+// the low nibble and 16 + j in the high nibble) as exact fp16 q - 8, in the
+// order (0, 2, 1, 3, 16, 18, 17, 19): (0x6400 | q) is 1024 + q, and one packed
+// add of -1032 per pair.
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ half8 q4_dword_halves(uint32_t qs) {
+    typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+    union { uint32_t u; half2v h; } p0, p1, p2, p3;
+    p0.u = (qs & 0x000f000fu) | 0x64006400u;
+    p1.u = ((qs >> 8) & 0x000f000fu) | 0x64006400u;
+    p2.u = ((qs >> 4) & 0x000f000fu) | 0x64006400u;
+    p3.u = ((qs >> 12) & 0x000f000fu) | 0x64006400u;
+    const half2v off = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
+    const half2v a = p0.h + off, b = p1.h + off, c = p2.h + off, d = p3.h + off;
+    half8 out;
+    out[0] = a[0]; out[1] = a[1]; out[2] = b[0]; out[3] = b[1];
+    out[4] = c[0]; out[5] = c[1]; out[6] = d[0]; out[7] = d[1];
+    return out;
+}
+
 // 16-byte load from an address that is only 4-byte aligned (global_load_dwordx4).
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 __device__ __forceinline__ u32x4_a4 load_u32x4(const uint32_t *p) {

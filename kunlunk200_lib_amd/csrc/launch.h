@@ -57,6 +57,14 @@ size_t kk_q4_mfma_gemv_workspace_bytes(int k);
 int kk_q4_mfma_gemv(const void *w, const float *x, float *y, int k, int n, int batch, void *workspace, int cus,
                     hipStream_t stream);
 
+// Q4_0 GEMV for batch 1..16 on fp16 MFMA with block-diagonal activation
+// operands (one pass over W, lanes streaming whole block pairs, no
+// workspace): K % 64 == 0, 4-byte aligned weights, 16-byte aligned X, and
+// the activation fragments of all of K in LDS (ceil(K/1024)*4 steps x
+// ceil(batch/4) x 4480 bytes <= 160 KiB); `cus` sizes the grid.
+int kk_q4_bdiag_gemv_supported(const void *w, const float *x, int k, int n, int batch);
+int kk_q4_bdiag_gemv(const void *w, const float *x, float *y, int k, int n, int batch, int cus, hipStream_t stream);
+
 // F32 (type 0) / F16 (type 1) GEMV for batch 1..16 on fp32 MFMA, one pass over
 // W; 16-byte aligned weights and activations.
 int kk_dense_mfma_gemv(int type, const void *w, const float *x, float *y, int k, int n, int batch,

@@ -59,6 +59,12 @@ bool q4_mfma_batch(int batch, bool streamed) {
     return batch >= min_b && batch <= max_b;
 }
 
+// Batch range of the block-diagonal Q4_0 MFMA GEMV (the single-pass kernel's
+// range, unless KUNLUN_Q4_BDIAG=0 leaves it to the LDS-staged kernels).
+bool q4_bdiag_batch(int batch) {
+    return kk::tuning_or(kk::kQ4Bdiag, 1) != 0 && q4_mfma_batch(batch, true);
+}
+
 // Batch range of the single-pass F32/F16 MFMA GEMV (within 1..16).
 bool dense_mfma_batch(int batch) {
     const int min_b = std::max(1, kk::tuning_or(kk::kDenseMfmaMin, 2));
@@ -166,6 +172,12 @@ void matmul(Kernel & kernel, int id, void * y, const void * w, const void * x, i
                                                          static_cast<float *>(y), k, n, batch, ctx.stream),
                           "kk_dense_mfma_gemv");
         impl.route = type == WeightType::f16 ? "f16_mfma_gemv" : "f32_mfma_gemv";
+    } else if (type == WeightType::q4_0 && kk::q4_bdiag_batch(batch) &&
+               kk_q4_bdiag_gemv_supported(w, static_cast<const float *>(x), k, n, batch)) {
+        detail::check_hip((hipError_t)kk_q4_bdiag_gemv(w, static_cast<const float *>(x), static_cast<float *>(y), k, n,
+                                                       batch, ctx.cus, ctx.stream),
+                          "kk_q4_bdiag_gemv");
+        impl.route = "q4_bdiag_gemv";
     } else if (type == WeightType::q4_0 && q4_mfma_batch(batch, k % 256 == 0 && ((uintptr_t)w & 15) == 0) &&
                k % 64 == 0 && ((uintptr_t)w & 3) == 0) {
         grow(id, ctx, impl.gemm_workspace, impl.gemm_workspace_size, kk_q4_mfma_gemv_workspace_bytes(k));

@@ -135,20 +135,8 @@ __global__ __launch_bounds__(kPrepassThreads) void x_to_frag(const float *__rest
 // ---------------------------------------------------------------------------
 // B fragment of lane (row n, group g) from nibble dword g of a block:
 // positions (4g, 4g+2, 4g+1, 4g+3, 16+4g, 16+4g+2, 16+4g+1, 16+4g+3), each
-// the exact fp16 q - 8 via (0x6400 | q) - 1032.
-__device__ __forceinline__ half8 decode_nibbles(uint32_t qs) {
-    union { uint32_t u; half2v h; } p0, p1, p2, p3;
-    p0.u = (qs & 0x000f000fu) | 0x64006400u;
-    p1.u = ((qs >> 8) & 0x000f000fu) | 0x64006400u;
-    p2.u = ((qs >> 4) & 0x000f000fu) | 0x64006400u;
-    p3.u = ((qs >> 12) & 0x000f000fu) | 0x64006400u;
-    const half2v off = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
-    const half2v a = p0.h + off, b = p1.h + off, c = p2.h + off, d = p3.h + off;
-    half8 out;
-    out[0] = a[0]; out[1] = a[1]; out[2] = b[0]; out[3] = b[1];
-    out[4] = c[0]; out[5] = c[1]; out[6] = d[0]; out[7] = d[1];
-    return out;
-}
+// the exact fp16 q - 8.
+__device__ __forceinline__ half8 decode_nibbles(uint32_t qs) { return kk::q4_dword_halves(qs); }
 
 // Workgroup barrier without a memory fence. The LDS reads of a wave are
 // complete when it reaches the barrier (their values feed the MFMAs before

@@ -3,8 +3,8 @@
 // graph capture, tight serving loops). It takes the routes and kernels of
 // kunlun::matmul (matmul.cpp); the routes that need device memory beyond the
 // inputs and outputs -- the fp16-MFMA prefill GEMM (fp16 activations and row
-// scales, kk_gemm_workspace_bytes) and the Q4_0 MFMA GEMV (activation
-// fragments, kk_q4_mfma_gemv_workspace_bytes) -- take it from `scratch`, a
+// scales, kk_gemm_workspace_bytes) and the LDS-staged Q4_0 MFMA GEMV
+// (activation fragments, kk_q4_mfma_gemv_workspace_bytes) -- take it from `scratch`, a
 // file-scope device array of kScratchBytes, instead of a Kernel's workspace.
 //
 // Every GPU the library runs on holds its own copy of the array until the
@@ -100,6 +100,9 @@ extern "C" int kunlun_matmul_noalloc(int device, void *y, const void *w, const v
     } else if ((type == 0 || type == 1) && kk::dense_mfma_batch(batch) && (wa & 15) == 0 && (xa & 15) == 0) {
         rc = static_cast<hipError_t>(kk_dense_mfma_gemv(type, w, xf, yf, k, n, batch, s));
         taken = type == 1 ? "f16_mfma_gemv" : "f32_mfma_gemv";
+    } else if (type == 2 && kk::q4_bdiag_batch(batch) && kk_q4_bdiag_gemv_supported(w, xf, k, n, batch)) {
+        rc = static_cast<hipError_t>(kk_q4_bdiag_gemv(w, xf, yf, k, n, batch, d.cus, s));
+        taken = "q4_bdiag_gemv";
     } else if (type == 2 && kk::q4_mfma_batch(batch, k % 256 == 0 && (wa & 15) == 0) && k % 64 == 0 &&
                (wa & 3) == 0) {
         const size_t need = kk_q4_mfma_gemv_workspace_bytes(k);

@@ -44,6 +44,7 @@ namespace kk {
 // aligned weights) and the F32/F16 single-pass MFMA GEMVs.
 int gemm_min_batch();
 bool q4_mfma_batch(int batch, bool streamed);
+bool q4_bdiag_batch(int batch);
 bool dense_mfma_batch(int batch);
 } // namespace kk
 

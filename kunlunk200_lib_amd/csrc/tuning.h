@@ -17,6 +17,7 @@ enum Knob {
     kGemvGeneral,         // KUNLUN_GEMV_GENERAL=1: every GEMV on the general kernel
     kI8FusedQuantLimit,   // KUNLUN_I8_FUSED_QUANT_LIMIT: single-workgroup quantizer limit
     kQ4GemvPlanes,        // KUNLUN_Q4_GEMV_PLANES=1: batch-1 Q4_0 GEMV on the LDS-staged digit-plane kernel
+    kQ4Bdiag,             // KUNLUN_Q4_BDIAG=0: the Q4_0 MFMA GEMV batch range on the LDS-staged kernels instead
     kKnobCount
 };
 

@@ -129,7 +129,7 @@ def test_q4_misaligned_weights_use_general_kernel(gpu, oracle):
     _, route = _dense_case(oracle, kl.WeightType.q4_0, w, x, k, n, batch, w_offset=2)
     assert route == "gemv_general"
     _, route = _dense_case(oracle, kl.WeightType.q4_0, w, x, k, n, batch, w_offset=0)
-    assert route in ("q4_gemv_planes", "q4_gemv_dot8", "q4_mfma_gemv")
+    assert route in ("q4_gemv_planes", "q4_gemv_dot8", "q4_bdiag_gemv", "q4_mfma_gemv")
 
 
 def test_unaligned_activation_uses_general_kernel(gpu, oracle):
@@ -267,8 +267,9 @@ def test_rowwise_i8_nonfinite_activation_aborts_at_wait(gpu, k, batch):
 @pytest.mark.parametrize("k,n,batch,route", [
     (4096, 32000, 1, "q4_gemv_dot8"),      # configs[1]: LM head
     (4096, 14336, 2, "q4_gemv_dot8"),      # configs[2]: batch 2 (two columns per pass)
-    (4096, 14336, 4, "q4_mfma_gemv"),
-    (4096, 14336, 16, "q4_mfma_gemv"),
+    (4096, 14336, 4, "q4_bdiag_gemv"),     # activation fragments of all of K fit in LDS
+    (4096, 14336, 8, "q4_bdiag_gemv"),
+    (4096, 14336, 16, "q4_mfma_gemv"),     # they do not: the LDS-staged kernel
 ])
 def test_q4_baseline_configs_default_route(gpu, oracle, k, n, batch, route):
     seed = k * 3 + n + batch

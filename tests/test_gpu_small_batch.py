@@ -1,28 +1,62 @@
-"""GPU parity of the single-pass small-batch Q4_0 GEMV (batch 2..16, fp16
-MFMA with hi/lo activations): BASELINE configs[2] shapes, K chunk tails, N
-tails, extreme and zero activation rows, against the FP64 gold of the exactly
-decoded weights (reference bench/library-bench.cpp:121-122) with the
-f32-accumulate bound |err| <= 1e-4 * ||x_b|| * ||w_r||.
+"""GPU parity of the single-pass small-batch Q4_0 GEMVs (batch 2..16, fp16
+MFMA with hi/lo activations): the block-diagonal kernel (q4_bdiag_gemv,
+where the activation fragments of all of K fit in LDS) and the LDS-staged
+kernels (q4_mfma_gemv, everywhere else and under KUNLUN_Q4_BDIAG=0), on
+BASELINE configs[2] shapes, K chunk tails, N tails, extreme and zero
+activation rows, against the FP64 gold of the exactly decoded weights
+(reference bench/library-bench.cpp:121-122) with the f32-accumulate bound
+|err| <= 1e-4 * ||x_b|| * ||w_r||.
 """
 import numpy as np
 import pytest
 
-# The MFMA GEMV takes batch 3..16 (streamed kernel) or 5..16 by default; tests
-# reach the smaller batches through KUNLUN_Q4_MFMA_MIN (read per call).
+# The MFMA GEMVs take batch 3..16 by default (the register-staged one from
+# 5); tests reach the smaller batches through KUNLUN_Q4_MFMA_MIN.
 
 import kunlunk200_lib_amd as kl
 from gpu_util import check_f32_accumulate, run_matmul
 
 pytestmark = pytest.mark.gpu
 
+KERNELS = ["bdiag", "lds"]
+
 
 def gaussian(shape, sigma, seed):
     return (np.random.default_rng(seed).standard_normal(shape) * sigma).astype(np.float32)
 
 
+def bdiag_fits(k, batch):
+    """Whether q4_bdiag_gemv takes (k, batch) (K % 64 == 0 assumed): for some
+    T in 1, 2, 4, 8, 16 tiles per workgroup (16 / T K-parts per tile, none of
+    them padding only), the per-wave steps (4 block pairs each) stay within 4
+    (1 from column group 3), 4480 LDS bytes per step and column group plus
+    4 KiB per group fit 160 KiB, and at most 4 activation items per thread."""
+    q = (batch + 3) // 4
+    need = (k + 255) // 256
+    for t in (1, 2, 4, 8, 16):
+        parts = 16 // t
+        spw = (need + parts - 1) // parts
+        steps = parts * spw
+        lds = steps * q * 4480 + 4096 * q
+        items = (4 * q * steps * 32 + 1023) // 1024
+        if spw <= (1 if q > 2 else 4) and lds <= 160 * 1024 and items <= 4 and (parts <= need or t == 16):
+            return True
+    return False
+
+
+def expected_route(kernel, k, batch):
+    return "q4_bdiag_gemv" if kernel == "bdiag" and bdiag_fits(k, batch) else "q4_mfma_gemv"
+
+
 @pytest.fixture(autouse=True)
 def mfma_from_batch_two(gpu, knobs):
     knobs("KUNLUN_Q4_MFMA_MIN", "2")
+
+
+@pytest.fixture(params=KERNELS)
+def kernel(request, knobs):
+    knobs("KUNLUN_Q4_BDIAG", "1" if request.param == "bdiag" else "0")
+    return request.param
 
 
 def q4_case(oracle, k, n, batch, seed, x=None):
@@ -39,25 +73,29 @@ def q4_case(oracle, k, n, batch, seed, x=None):
 
 
 @pytest.mark.parametrize("batch", [2, 4, 8, 16])
-def test_config2_shapes(gpu, oracle, batch):
+def test_config2_shapes(gpu, oracle, kernel, batch):
     y, route, guard_ok, res = q4_case(oracle, 4096, 14336, batch, 100 + batch)
-    assert route == "q4_mfma_gemv"
+    assert route == expected_route(kernel, 4096, batch)
     assert guard_ok and res["finite"] and res["north_star"] and res["reference"]
 
 
-# streamed kernel with 16-block stages: K % 512 == 0 (1024, 2048, 4096, 16384);
-# 8-block stages: K % 256 == 0 only (11008); register-staged: the rest
+# LDS-staged kernels: 16-block stages for K % 512 == 0 (1024, 2048, 4096,
+# 16384), 8-block stages for K % 256 == 0 only (11008), register-staged for the
+# rest; block-diagonal kernel: partial last steps (4160, 576) and the tile and
+# K-part splits of 1, 2 and 4 tiles per workgroup
 @pytest.mark.parametrize("k,n,batch", [(64, 1, 2), (64, 17, 16), (4160, 33, 3), (11008, 4096, 4), (16384, 70, 16),
-                                       (1024, 16, 5), (2048, 1000, 9), (4096, 4096, 15)])
-def test_tails(gpu, oracle, k, n, batch):
+                                       (1024, 16, 5), (2048, 1000, 9), (4096, 4096, 15), (576, 130, 12),
+                                       (8192, 300, 4), (2048, 5000, 16), (4096, 4200, 7)])
+def test_tails(gpu, oracle, kernel, k, n, batch):
     y, route, guard_ok, res = q4_case(oracle, k, n, batch, k + n + batch)
-    assert route == "q4_mfma_gemv"
+    assert route == expected_route(kernel, k, batch)
     assert guard_ok and res["finite"] and res["north_star"] and res["reference"]
 
 
-def test_weights_off_16_bytes(gpu, oracle):
+def test_weights_off_16_bytes(gpu, oracle, kernel):
     # K % 256 == 0 streams through LDS when the weights are 16-byte aligned;
-    # 4-byte aligned weights take the chunked kernel: same bound either way
+    # 4-byte aligned weights take the chunked kernel (the block-diagonal one
+    # takes both): same bound either way
     k, n, batch = 2048, 300, 7
     w = gaussian((n, k), 0.02, 91)
     x = gaussian((batch, k), 1.0, 92)
@@ -67,16 +105,22 @@ def test_weights_off_16_bytes(gpu, oracle):
     for w_offset in (0, 4):
         y, route, guard_ok = run_matmul(kl.WeightType.q4_0, q4, x, k, n, batch, w_offset=w_offset)
         res = check_f32_accumulate(y, gold, dec, x)
-        assert route == "q4_mfma_gemv"
+        assert route == expected_route(kernel, k, batch)
         assert guard_ok and res["finite"] and res["north_star"] and res["reference"]
 
 
-def test_default_batch_routing(gpu, oracle, knobs):
-    # defaults: the streamed kernel (K % 256 == 0, 16-byte aligned weights)
-    # from batch 3, the register-staged one from batch 5, batch-1 passes below
+def test_default_batch_routing(gpu, oracle, kernel):
+    # defaults: the block-diagonal kernel from batch 3 where it fits;
+    # otherwise (and under KUNLUN_Q4_BDIAG=0) the streamed kernel (K % 256 ==
+    # 0, 16-byte aligned weights) from batch 3, the register-staged one from
+    # batch 5, batch-1 passes below
     kl.set_tuning("KUNLUN_Q4_MFMA_MIN", None)
-    cases = [(512, 3, 0, "q4_mfma_gemv"), (512, 2, 0, "q4_gemv_dot8"), (576, 3, 0, "q4_gemv_dot8"),
-             (576, 5, 0, "q4_mfma_gemv"), (512, 4, 4, "q4_gemv_dot8")]
+    if kernel == "bdiag":
+        cases = [(512, 3, 0, "q4_bdiag_gemv"), (512, 2, 0, "q4_gemv_dot8"), (576, 3, 0, "q4_bdiag_gemv"),
+                 (576, 5, 0, "q4_bdiag_gemv"), (512, 4, 4, "q4_bdiag_gemv"), (4096, 16, 0, "q4_mfma_gemv")]
+    else:
+        cases = [(512, 3, 0, "q4_mfma_gemv"), (512, 2, 0, "q4_gemv_dot8"), (576, 3, 0, "q4_gemv_dot8"),
+                 (576, 5, 0, "q4_mfma_gemv"), (512, 4, 4, "q4_gemv_dot8")]
     for k, batch, w_offset, want in cases:
         w = gaussian((70, k), 0.02, k + batch)
         x = gaussian((batch, k), 1.0, k + batch + 1)
@@ -89,7 +133,7 @@ def test_default_batch_routing(gpu, oracle, knobs):
         assert guard_ok and res["finite"] and res["north_star"] and res["reference"]
 
 
-def test_extreme_rows(gpu, oracle):
+def test_extreme_rows(gpu, oracle, kernel):
     k, n, batch = 4096, 300, 6
     x = gaussian((batch, k), 1.0, 77)
     x[1] *= 1e6
@@ -97,12 +141,12 @@ def test_extreme_rows(gpu, oracle):
     x[3] = 0.0
     x[4, ::7] *= 1000.0           # a row with a wide dynamic range
     y, route, guard_ok, res = q4_case(oracle, k, n, batch, 78, x=x)
-    assert route == "q4_mfma_gemv"
+    assert route == expected_route(kernel, k, batch)
     assert guard_ok and res["finite"] and res["north_star"]
     assert np.all(y[3] == 0.0)
 
 
-def test_matches_batch_one_kernel(gpu, oracle, knobs):
+def test_matches_batch_one_kernel(gpu, oracle, knobs, kernel):
     # the same call with the MFMA GEMV disabled (pairs of dot8 columns)
     k, n, batch = 4096, 1000, 8
     w = gaussian((n, k), 0.02, 5)
@@ -111,7 +155,7 @@ def test_matches_batch_one_kernel(gpu, oracle, knobs):
     y_mfma, r1, _ = run_matmul(kl.WeightType.q4_0, q4, x, k, n, batch)
     knobs("KUNLUN_Q4_MFMA_MIN", "17")
     y_dot8, r2, _ = run_matmul(kl.WeightType.q4_0, q4, x, k, n, batch)
-    assert r1 == "q4_mfma_gemv" and r2 == "q4_gemv_dot8"
+    assert r1 == expected_route(kernel, k, batch) and r2 == "q4_gemv_dot8"
     dec = oracle.q4_decode(q4, k, n)
     xn = np.linalg.norm(x.astype(np.float64), axis=1)[:, None]
     wn = np.linalg.norm(dec.astype(np.float64), axis=1)[None, :]
