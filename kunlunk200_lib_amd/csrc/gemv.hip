@@ -68,11 +68,15 @@ constexpr int dot8_block_lds_bytes(int digits) { return 16 * digits + 4; }
 
 // PASSES = activation staging passes: B * (K/32) * 4 <= PASSES * 64 * WAVES.
 // SLICES = ceil(K / 4096): 64-pair slices per row. Rows are split over the
-// grid's waves as base or base+1 contiguous rows (rem waves get one more).
+// grid's waves as base or base+1 contiguous rows (rem waves get one more),
+// or, STRIDED, wave w of the grid's nw waves takes rows w, w + nw, w + 2 nw,
+// ...: then the i-th items of all waves are consecutive rows, so the grid
+// streams the matrix front to back (at N11008 and N32000 5-9% faster than
+// contiguous ranges whenever a wave's rows do not all fit in its ring).
 // PAIR (U = 2): an item is output row r of both the gate matrix w and the up
 // matrix w2, and the row result is SiLU(gate) * up (the swiglu kernel's
 // element function), so the pair reads X once and needs no second pass.
-template <int B, int U, int WAVES, int SLICES, int DEPTH, int PASSES, bool PAIR, int DIGITS>
+template <int B, int U, int WAVES, int SLICES, int DEPTH, int PASSES, bool PAIR, int DIGITS, bool STRIDED>
 __global__ __launch_bounds__(64 * WAVES) void q4_gemv_dot8(const uint8_t *__restrict__ w,
                                                           const uint8_t *__restrict__ w2,
                                                           const float *__restrict__ x,
@@ -93,9 +97,11 @@ __global__ __launch_bounds__(64 * WAVES) void q4_gemv_dot8(const uint8_t *__rest
     const int lane = threadIdx.x & (kWave - 1);
     const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
     const int wave = blockIdx.x * WAVES + wid;
-    const int r_begin = wave * rows_base + min(wave, rows_rem);
-    const int rows = rows_base + (wave < rows_rem ? 1 : 0);   // 0 <= rows <= kDot8MaxRowsPerWave
-    const int r_end = r_begin + rows;
+    const int nwaves = gridDim.x * WAVES;
+    const int r_begin = STRIDED ? wave : wave * rows_base + min(wave, rows_rem);
+    const int rows = STRIDED ? (wave < n ? (n - 1 - wave) / nwaves + 1 : 0)
+                             : rows_base + (wave < rows_rem ? 1 : 0);   // 0 <= rows <= kDot8MaxRowsPerWave
+    const int row_step = STRIDED ? nwaves : 1;
     static_assert(!PAIR || U == 2, "a pair item is one gate row and one up row");
     const int chunks = PAIR ? rows : (rows + U - 1) / U;
     const int items = chunks * slices;
@@ -108,7 +114,8 @@ __global__ __launch_bounds__(64 * WAVES) void q4_gemv_dot8(const uint8_t *__rest
         const int p = min(lane + kWave * j, pairs - 1);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int r = max(0, min(min(r_begin + (PAIR ? c : c * U + u), r_end - 1), n - 1));
+            const int ordinal = max(0, min(PAIR ? c : c * U + u, rows - 1));
+            const int r = min(r_begin + ordinal * row_step, n - 1);
             const uint8_t *base = PAIR && u == 1 ? w2 : w;
             const uint32_t *src = reinterpret_cast<const uint32_t *>(
                 base + static_cast<size_t>(r) * row_bytes + static_cast<size_t>(p) * 36);
@@ -304,7 +311,8 @@ __global__ __launch_bounds__(64 * WAVES) void q4_gemv_dot8(const uint8_t *__rest
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int b = 0; b < B; ++b)
-        if (lane < rows) y[static_cast<size_t>(b) * y_stride + r_begin + lane] = my_results[b * kDot8MaxRowsPerWave + lane];
+        if (lane < rows)
+            y[static_cast<size_t>(b) * y_stride + r_begin + lane * row_step] = my_results[b * kDot8MaxRowsPerWave + lane];
 }
 
 // ---------------------------------------------------------------------------
@@ -484,7 +492,7 @@ int groups_for(int rowblocks, int cus, int per_cu_waves) {
 
 // One launch of q4_gemv_dot8 with WAVES waves per workgroup and up to
 // `per_cu` waves per CU (fewer when a wave would own no row).
-template <int B, int SLICES, int DEPTH, bool PAIR, int DIGITS, int WAVES>
+template <int B, int SLICES, int DEPTH, bool PAIR, int DIGITS, int WAVES, bool STRIDED = false>
 hipError_t launch_q4_dot8_cfg(const uint8_t *w, const uint8_t *w2, const float *x, float *y, int k, int n,
                               int y_stride, hipStream_t stream, const DeviceInfo &info, int per_cu) {
     constexpr int kU = PAIR ? 2 : 1;
@@ -497,7 +505,7 @@ hipError_t launch_q4_dot8_cfg(const uint8_t *w, const uint8_t *w2, const float *
     const int waves = groups * WAVES;
     const int rows_base = n / waves, rows_rem = n % waves;
     if (rows_base + (rows_rem ? 1 : 0) > kDot8MaxRowsPerWave) return hipErrorInvalidValue;
-    auto kernel = &q4_gemv_dot8<B, kU, WAVES, SLICES, DEPTH, kPasses, PAIR, DIGITS>;
+    auto kernel = &q4_gemv_dot8<B, kU, WAVES, SLICES, DEPTH, kPasses, PAIR, DIGITS, STRIDED>;
     // B * K <= 16384: at most 512 * 100 + 16 * 2 * 64 * 4 bytes, inside the 64 KiB default
     hipLaunchKernelGGL(kernel, dim3(groups), dim3(64 * WAVES), lds, stream, w, w2, x, y, k, n, y_stride, rows_base,
                        rows_rem);
@@ -517,6 +525,24 @@ hipError_t launch_q4_dot8_depth(const uint8_t *w, const uint8_t *w2, const float
 template <int B, int SLICES, bool PAIR>
 hipError_t launch_q4_dot8_slices(const uint8_t *w, const uint8_t *w2, const float *x, float *y, int k, int n,
                                  int y_stride, hipStream_t stream, const DeviceInfo &info) {
+    if constexpr (B == 1 && !PAIR) {
+        // single column. K <= 4096: 4 waves per CU, each with all of its rows
+        // in flight when they fit a 4-item ring (contiguous ranges), else a
+        // 3-item ring over strided rows (K4096: N4096 3.9 against 4.8 us with
+        // 8 waves per CU, N11008 6.9 against 7.3 us, N32000 13.6 against
+        // 14.9 us). Longer rows: 8 waves per CU over strided rows (K11008 x
+        // N4096: 7.9 against 8.5 us).
+        if (SLICES == 1) {
+            const long long waves = std::max<long long>(1, std::min<long long>(n, static_cast<long long>(info.cus) * 4));
+            if ((n + waves - 1) / waves <= 4)
+                return launch_q4_dot8_cfg<1, 1, 4, false, 6, 4>(w, w2, x, y, k, n, y_stride, stream, info, 4);
+            return launch_q4_dot8_cfg<1, 1, 3, false, 6, 4, true>(w, w2, x, y, k, n, y_stride, stream, info, 4);
+        }
+        const long long waves = std::max<long long>(1, std::min<long long>(n, static_cast<long long>(info.cus) * 8));
+        if ((n + waves - 1) / waves * SLICES <= 2)
+            return launch_q4_dot8_cfg<1, SLICES, 2, false, 6, 8>(w, w2, x, y, k, n, y_stride, stream, info, 8);
+        return launch_q4_dot8_cfg<1, SLICES, 3, false, 6, 8, true>(w, w2, x, y, k, n, y_stride, stream, info, 8);
+    }
     // items in flight per wave: 3 single-column items, 2 when an item is twice
     // the work (two batch columns, or a gate/up row pair) or when a wave owns
     // at most 2 items (then all of them are in flight and a third would be a
