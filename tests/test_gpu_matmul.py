@@ -92,6 +92,7 @@ SHAPES = [
     (32, 1, 1), (64, 7, 1), (96, 17, 3), (256, 65, 4), (512, 300, 2), (4096, 4096, 1),
     (4096, 11008, 1), (11008, 4096, 1), (4096, 12288, 1), (4096, 1024, 8), (4096, 512, 16),
     (4096, 64, 5), (16384, 96, 1), (16384, 40, 3), (14336, 256, 2),
+    (512, 130, 17), (1024, 70, 22),   # F32/F16 above 16 columns: passes of 4 columns (and a last single one)
 ]
 
 
