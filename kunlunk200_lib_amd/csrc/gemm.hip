@@ -815,13 +815,19 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
                 acc[rg][cg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b0[cg], acc[rg][cg], 0, 0, 0);
                 acc[rg + 1][cg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b0[cg], acc[rg + 1][cg], 0, 0, 0);
             }
-            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int cg = 0; cg < S::CG; ++cg)
                 if (grp > 0 && (cg + 1 < S::RG / 2 ? cg + 1 : S::RG / 2 - 1) == grp) {
                     note_tiny_scale(sbits[cg], tiny);
                     b1[cg] = decode_q4_scaled(nib[cg], sbits[cg]);
                 }
+            // one MFMA, then up to 3 VALU (the decode), alternately
+#pragma unroll
+            for (int m = 0; m < 2 * S::CG; ++m) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
             a0 = n0;
             a1 = n1;
         }
