@@ -26,6 +26,7 @@
 // scale.
 #include "device_common.h"
 #include "launch.h"
+#include "tuning.h"
 
 #include <algorithm>
 
@@ -690,6 +691,226 @@ __global__ __launch_bounds__(kWave * kDenseWaves) void dense_mfma_gemv(const uin
     }
 }
 
+// F16 weights, batch 2..8, K <= 4096: the weights streamed as the batch-1
+// GEMV reads them. An item is one 1 KiB chunk (512 values) of one row, so
+// every load instruction covers 1 KiB of contiguous row bytes. A workgroup
+// owns T 16-row tiles and wave w takes chunk w of every tile row, keeping
+// kF16sDepth items in flight. Each arrived item goes into the wave's own LDS
+// area (lane l: bytes 16 l .. 16 l + 15, zero past the row end; row stride
+// 1040 B), and when a tile's 16 rows are there, lane (n, g) reads 16-byte
+// piece 4j + g of row n (conflict-free at that stride): the B operand of
+// v_mfma_f32_16x16x32_f16 for K32 slice j of the chunk.
+// The A operand, held in registers for the whole launch: row r of it is
+// column r of X (r < 8) as the fp16 hi part, and column r - 8 as the lo
+// part, of x * 2^s. The power of two 2^s, per column and chunk, brings the
+// chunk's max |x| below 2^14, and |x 2^s - hi - lo| <= 2^-22 |x 2^s| + 2^-25
+// (the lo part may be an fp16 subnormal).
+// fp16 x fp16 products are exact in F32, so D[r][n] are exact products
+// summed in F32; the hi and lo rows of a column are added and the sum
+// multiplied by 2^-s.
+// X is read lane-contiguously (lane l: column l / 8, 16 B at 16 (l % 8)
+// within each 128 B of the chunk; lanes that read different rows of X in one
+// instruction cost one cache-tag lookup each) and moved into the A layout
+// with ds_bpermute: lane (r, g) takes values 8g + 4h .. 8g + 4h + 3 (h = r / 8)
+// of column r % 8, converts them to hi and lo, keeps its own half (hi for
+// r < 8, lo otherwise) and trades the other with lane r ^ 8 by DPP.
+// An F16 weight that is Inf or NaN times a lo part of 0 would give NaN
+// where the F32 product gives +-Inf. With finite X the split products stay
+// below 2^39 in magnitude, so a tile's sums are all finite exactly when its
+// weights are; a tile with a non-finite sum, or whose chunk of X holds a
+// non-finite value, is recomputed on an exact path: v_mfma_f32_16x16x4_f32
+// on the F32 activations (reloaded) and the widened staged weights, the
+// products of dense_mfma_gemv.
+// The waves' tile sums meet in LDS and are added in wave order.
+constexpr int kF16sWaves = 8;
+constexpr int kF16sDepth = 16;
+constexpr int kF16sRowStride = 1040;
+constexpr int kF16sStageBytes = 16 * kF16sRowStride;
+constexpr int kF16sMaxTiles = 4;
+constexpr int kF16sLdsBytes = kF16sWaves * kF16sStageBytes + kF16sMaxTiles * kF16sWaves * 32 * 16;
+
+__global__ __launch_bounds__(kWave * kF16sWaves) void f16_stream_gemv(const uint8_t *__restrict__ w,
+                                                                     const float *__restrict__ x,
+                                                                     float *__restrict__ y, int k, int n, int batch,
+                                                                     int tiles_per_group) {
+    extern __shared__ __align__(16) uint8_t fs_lds[];
+    typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    constexpr int kXor8 = 0x128;                                  // DPP row_ror:8, lane r ^ 8 within 16
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+    const int r16 = lane & 15, g = lane >> 4;
+    const bool hi_row = r16 < 8;
+    const uint32_t row_bytes = static_cast<uint32_t>(k) * 2;
+    const int tiles = (n + 15) / 16;
+    const int tile0 = blockIdx.x * tiles_per_group;
+    const int items = tiles_per_group * 16;
+    const int c = wid;                                           // this wave's chunk
+    const int jlive = __builtin_amdgcn_readfirstlane(max(0, min(16, (k - c * 512) / 32)));   // K32 slices in K
+    uint8_t *stage = fs_lds + wid * kF16sStageBytes;
+    float4v *partial = reinterpret_cast<float4v *>(fs_lds + kF16sWaves * kF16sStageBytes);   // [T][waves][32]
+
+    // 1. X, lane-contiguous: lane l holds values c*512 + 32 j + 4 (l % 8) .. + 3 of column l / 8
+    float xv[16][4];
+    {
+        const int lc = lane >> 3, q = lane & 7;
+        const bool lc_live = lc < batch;
+        const float *xl = x + static_cast<size_t>(min(lc, batch - 1)) * k;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int k0 = c * 512 + 32 * j + 4 * q;
+            const bool live = lc_live && k0 < k;
+            const float4 a = *reinterpret_cast<const float4 *>(xl + (live ? k0 : 0));
+            xv[j][0] = live ? a.x : 0.0f; xv[j][1] = live ? a.y : 0.0f;
+            xv[j][2] = live ? a.z : 0.0f; xv[j][3] = live ? a.w : 0.0f;
+        }
+    }
+    // 2. the first items (issued after X: the memory counter is in order)
+    __builtin_amdgcn_sched_barrier(0);
+    auto load_item = [&](int item, u32x4 &v) {
+        const int it = min(item, items - 1);
+        const int i = it & 15, t = it >> 4;
+        const int tile = min(tile0 + t, tiles - 1);
+        const int r = min(tile * 16 + i, n - 1);
+        const uint32_t off = min(static_cast<uint32_t>(c) * 1024u + 16u * lane, row_bytes - 16u);
+        v = *reinterpret_cast<const u32x4 *>(w + static_cast<size_t>(r) * row_bytes + off);
+    };
+    u32x4 ring[kF16sDepth];
+#pragma unroll
+    for (int d = 0; d < kF16sDepth; ++d) {
+        load_item(d, ring[d]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // 3. X into the A layout; the chunk's scale per column; hi/lo fragments
+    {
+        const int src = ((r16 & 7) * 8 + 2 * g + (r16 >> 3)) * 4;
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                xv[j][t] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(xv[j][t])));
+    }
+    float m = 0.0f, bad = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const float a = fabsf(xv[j][t]);
+            bad = (a <= 3.402823466e38f) ? bad : 1.0f;
+            m = fmaxf(m, a);
+        }
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), kXor8, 0xf, 0xf, false)));
+    m = fmaxf(m, __shfl_xor(m, 16, kWave));
+    m = fmaxf(m, __shfl_xor(m, 32, kWave));
+    const bool x_bad = __builtin_amdgcn_ballot_w64(bad != 0.0f) != 0;   // wave-uniform
+    const int e = max(min(__builtin_amdgcn_frexp_expf(m), 128), -110);   // m < 2^e; 2^(14-e) and 2^(e-14) stay normal
+    const float to_f16 = ldexpf(1.0f, 14 - e);
+    const float inv_self = ldexpf(1.0f, e - 14);
+    float inv[8];
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc) inv[cc] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv_self), cc));
+    half8 af[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        half4 hh, ll;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const float v = xv[j][t] * to_f16;
+            const _Float16 h = static_cast<_Float16>(v);
+            hh[t] = h;
+            ll[t] = static_cast<_Float16>(v - static_cast<float>(h));
+        }
+        // hi lanes keep their hi parts and take the partner's (values 4..7); lo lanes the reverse
+        const u32x2 send = hi_row ? __builtin_bit_cast(u32x2, ll) : __builtin_bit_cast(u32x2, hh);
+        u32x2 recv;
+        recv[0] = __builtin_amdgcn_update_dpp(0, static_cast<int>(send[0]), kXor8, 0xf, 0xf, false);
+        recv[1] = __builtin_amdgcn_update_dpp(0, static_cast<int>(send[1]), kXor8, 0xf, 0xf, false);
+        const half4 other = __builtin_bit_cast(half4, recv);
+        const half4 first = hi_row ? hh : other, last = hi_row ? other : ll;   // values 0..3, 4..7
+        af[j][0] = first[0]; af[j][1] = first[1]; af[j][2] = first[2]; af[j][3] = first[3];
+        af[j][4] = last[0]; af[j][5] = last[1]; af[j][6] = last[2]; af[j][7] = last[3];
+    }
+
+    auto tile_compute = [&](int t) {
+        float4v d = {0.0f, 0.0f, 0.0f, 0.0f};
+        bool tile_bad = x_bad;
+        if (!tile_bad) {
+            float4v acc[4] = {};
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                if (j < jlive) {
+                    const half8 b = *reinterpret_cast<const half8 *>(stage + r16 * kF16sRowStride + (4 * j + g) * 16);
+                    acc[j & 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[j], b, acc[j & 3], 0, 0, 0);
+                }
+            const float4v sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+            const bool nf = !(fabsf(sum[0]) <= 3.402823466e38f && fabsf(sum[1]) <= 3.402823466e38f &&
+                              fabsf(sum[2]) <= 3.402823466e38f && fabsf(sum[3]) <= 3.402823466e38f);
+            tile_bad = __builtin_amdgcn_ballot_w64(nf) != 0;               // wave-uniform
+            // lane (n, g): g < 2 hold the hi rows of columns 4g .. 4g+3, lane + 32 their lo rows
+            float4v lo;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) lo[r] = __shfl_xor(sum[r], 32, kWave);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) d[r] = (sum[r] + lo[r]) * inv[(4 * g + r) & 7];
+        }
+        if (tile_bad) {
+            // exact path: F32 activations of column r16 (< 8; rows 8..15 zero)
+            const bool live_row = r16 < batch && r16 < 8;
+            const float *xr = x + static_cast<size_t>(min(r16, batch - 1)) * k;
+            float4v a32[4] = {};
+            for (int j = 0; j < jlive; ++j) {
+                const int k0 = c * 512 + 32 * j + 8 * g;
+                const float4 xa = *reinterpret_cast<const float4 *>(xr + (live_row ? k0 : 0));
+                const float4 xb = *reinterpret_cast<const float4 *>(xr + (live_row ? k0 : 0) + 4);
+                const float xs[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+                const u32x4 p = *reinterpret_cast<const u32x4 *>(stage + r16 * kF16sRowStride + (4 * j + g) * 16);
+#pragma unroll
+                for (int e2 = 0; e2 < 4; ++e2) {
+                    a32[(2 * e2) & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                        live_row ? xs[2 * e2] : 0.0f, kk::half_bits_to_float(p[e2] & 0xffffu), a32[(2 * e2) & 3], 0, 0, 0);
+                    a32[(2 * e2 + 1) & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                        live_row ? xs[2 * e2 + 1] : 0.0f, kk::half_bits_to_float(p[e2] >> 16), a32[(2 * e2 + 1) & 3],
+                        0, 0, 0);
+                }
+            }
+            d = (a32[0] + a32[1]) + (a32[2] + a32[3]);
+        }
+        if (lane < 32) partial[(t * kF16sWaves + wid) * 32 + lane] = d;
+    };
+    auto stage_item = [&](int item, const u32x4 &v) {
+        const int i = item & 15;
+        const bool live = (static_cast<uint32_t>(c) * 1024u + 16u * lane) < row_bytes;
+        *reinterpret_cast<u32x4 *>(stage + i * kF16sRowStride + 16 * lane) = live ? v : u32x4{0u, 0u, 0u, 0u};
+        if (i == 15) tile_compute(item >> 4);
+    };
+    if (items <= kF16sDepth) {
+#pragma unroll
+        for (int dd = 0; dd < kF16sDepth; ++dd) stage_item(dd, ring[dd]);
+    } else {
+        for (int base = 0; base < items; base += kF16sDepth) {
+#pragma unroll
+            for (int dd = 0; dd < kF16sDepth; ++dd) {
+                const int item = base + dd;
+                if (item < items) stage_item(item, ring[dd]);
+                load_item(item + kF16sDepth, ring[dd]);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): the clamped refills end here
+    }
+    __syncthreads();
+    // 4. D[4g + r][n] of lane (n, g < 2): column 4g + r, weight row 16 tile + n
+    for (int idx = threadIdx.x; idx < tiles_per_group * 128; idx += kWave * kF16sWaves) {
+        const int t = idx >> 7, mm = (idx >> 4) & 7, nn = idx & 15;
+        const int row = (tile0 + t) * 16 + nn;
+        if (mm >= batch || tile0 + t >= tiles || row >= n) continue;
+        const int src_lane = (mm >> 2) * 16 + nn, r = mm & 3;
+        float sum = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < kF16sWaves; ++ww) sum += partial[(t * kF16sWaves + ww) * 32 + src_lane][r];
+        y[static_cast<size_t>(mm) * n + row] = sum;
+    }
+}
+
 } // namespace
 
 extern "C" int kk_dense_mfma_gemv(int type, const void *w, const float *x, float *y, int k, int n, int batch,
@@ -697,6 +918,30 @@ extern "C" int kk_dense_mfma_gemv(int type, const void *w, const float *x, float
     if ((type != 0 && type != 1) || !w || !x || !y || k <= 0 || (k & 31) || n <= 0 || batch < 1 ||
         batch > 16 || (reinterpret_cast<uintptr_t>(w) & 15) || (reinterpret_cast<uintptr_t>(x) & 15))
         return hipErrorInvalidValue;
+    if (type == 1 && batch <= 8 && k <= 4096 && kk::tuning_or(kk::kDenseStream, 1) != 0) {
+        constexpr int kMaxDevices = 64;
+        static bool opted[kMaxDevices] = {};
+        static int cus_of[kMaxDevices] = {};
+        int device = 0;
+        hipError_t rc = hipGetDevice(&device);
+        if (rc != hipSuccess) return rc;
+        if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+        if (!opted[device]) {
+            rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&f16_stream_gemv),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, kF16sLdsBytes);
+            if (rc != hipSuccess) return rc;
+            int cus = 256;
+            if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
+                cus = 256;
+            cus_of[device] = cus;
+            opted[device] = true;
+        }
+        const int tiles = (n + 15) / 16;
+        const int t = std::max(1, std::min(kF16sMaxTiles, (tiles + cus_of[device] - 1) / cus_of[device]));
+        hipLaunchKernelGGL(f16_stream_gemv, dim3((tiles + t - 1) / t), dim3(kWave * kF16sWaves), kF16sLdsBytes, stream,
+                           static_cast<const uint8_t *>(w), x, y, k, n, batch, t);
+        return hipGetLastError();
+    }
     const int tiles = (n + 15) / 16;
     if (type == 1)
         hipLaunchKernelGGL(dense_mfma_gemv<true>, dim3(tiles), dim3(kWave * kDenseWaves), 0, stream,

@@ -26,6 +26,7 @@ constexpr KnobName kNames[] = {
     {kI8FusedQuantLimit, "KUNLUN_I8_FUSED_QUANT_LIMIT"},
     {kQ4GemvPlanes, "KUNLUN_Q4_GEMV_PLANES"},
     {kQ4Bdiag, "KUNLUN_Q4_BDIAG"},
+    {kDenseStream, "KUNLUN_DENSE_STREAM"},
 };
 static_assert(sizeof(kNames) / sizeof(kNames[0]) == kKnobCount, "every knob has a name");
 

@@ -8,9 +8,14 @@ kernels/q4-device.h:3-12).
   subnormals) is one weight row of K = 32 with the value in column r % 32 and
   zeros elsewhere. With activations +-2^j every product and every sum is exact
   in F32, so Y must equal value * x bit for bit (+0 and -0 compare equal) on
-  each F16 route: f16_gemv (batch 1), f16_mfma_gemv (batch 2..16) and the
+  each F16 route: f16_gemv (batch 1), f16_mfma_gemv (batch 2..16: the
+  streamed fp16-MFMA kernel with activations split into hi and lo fp16 parts
+  at batch <= 8 and K <= 4096, the K-split F32-MFMA kernel beyond) and the
   fp16-MFMA GEMM (batch >= 64). Rows holding +Inf, -Inf, NaN, and +Inf with
   -Inf give +Inf, -Inf, NaN, NaN.
+* F16 small batch, split activations: a non-finite activation poisons its
+  column as in F32 arithmetic, and activations spanning 2^-60 .. 2^60 inside
+  one 512-value chunk keep the north-star bound.
 * Q4_0: rows whose block scales are F16 subnormals (all blocks, or every other
   block beside normal scales), with random nibbles and Gaussian activations,
   on every Q4_0 route: q4_gemv_dot8 (batch 1 and 2), q4_gemv_planes (batch 1
@@ -30,7 +35,10 @@ from gpu_util import check_f32_accumulate, run_matmul
 
 pytestmark = pytest.mark.gpu
 
-F16_ROUTES = [(1, "f16_gemv"), (8, "f16_mfma_gemv"), (64, "f16_gemm_mfma")]
+# batch 8 (K <= 4096): the streamed fp16-MFMA GEMV with split activations;
+# batch 16: the K-split F32-MFMA GEMV
+F16_ROUTES = [(1, "f16_gemv"), (8, "f16_mfma_gemv"), (16, "f16_mfma_gemv"), (64, "f16_gemm_mfma")]
+F16_ROUTE_IDS = ["f16_gemv", "f16_mfma_gemv_stream", "f16_mfma_gemv_ksplit", "f16_gemm_mfma"]
 
 
 def all_finite_f16():
@@ -52,7 +60,7 @@ def power_of_two_activations(batch, k=32):
     return np.repeat(col[:, None], k, axis=1).astype(np.float32)
 
 
-@pytest.mark.parametrize("batch,route", F16_ROUTES, ids=[r for _, r in F16_ROUTES])
+@pytest.mark.parametrize("batch,route", F16_ROUTES, ids=F16_ROUTE_IDS)
 def test_f16_every_finite_pattern_exact(gpu, batch, route):
     values = all_finite_f16().view(np.float16)
     w = one_hot_rows(values)
@@ -70,7 +78,7 @@ def test_f16_every_finite_pattern_exact(gpu, batch, route):
     print(f"  f16 {route}: {values.size} patterns ({int(sub.sum())} zero/subnormal) exact", flush=True)
 
 
-@pytest.mark.parametrize("batch,route", F16_ROUTES, ids=[r for _, r in F16_ROUTES])
+@pytest.mark.parametrize("batch,route", F16_ROUTES, ids=F16_ROUTE_IDS)
 def test_f16_nonfinite_rows(gpu, batch, route):
     k = 64
     inf, nan = np.float16(np.inf), np.float16(np.nan)
@@ -88,6 +96,56 @@ def test_f16_nonfinite_rows(gpu, batch, route):
     assert np.all(y[:, 0] == np.inf) and np.all(y[:, 1] == -np.inf) and np.all(y[:, 4] == np.inf)
     assert np.all(np.isnan(y[:, 2])) and np.all(np.isnan(y[:, 3]))
     assert np.all(np.isfinite(y[:, 5:]))
+
+
+@pytest.mark.parametrize("stream", [True, False], ids=["stream", "ksplit"])
+def test_f16_small_batch_nonfinite_activation(gpu, knobs, stream):
+    # one non-finite activation: its column is the F32 result (Inf / NaN),
+    # the other columns stay finite and within the bound
+    if not stream:
+        knobs("KUNLUN_DENSE_STREAM", "0")
+    k, n, batch = 1024, 48, 6
+    rng = np.random.default_rng(5)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
+    w[:, 700] = np.abs(w[:, 700]) + np.float16(0.01)       # the Inf meets positive weights only
+    x = rng.standard_normal((batch, k)).astype(np.float32)
+    x[1, 700] = np.inf
+    x[3, 9] = np.nan
+    x[4, 1000] = -np.inf
+    y, route, guard_ok = run_matmul(kl.WeightType.f16, w.view(np.uint8), x, k, n, batch)
+    assert route == "f16_mfma_gemv" and guard_ok
+    assert np.all(y[1] == np.inf) and np.all(np.isnan(y[3]))
+    want4 = np.where(w[:, 1000] > 0, -np.inf, np.where(w[:, 1000] < 0, np.inf, np.nan))
+    assert np.array_equal(np.isnan(y[4]), np.isnan(want4)) and np.all(y[4][~np.isnan(want4)] == want4[~np.isnan(want4)])
+    ok = [0, 2, 5]
+    dec = w.astype(np.float32)
+    gold = (x[ok].astype(np.float64) @ dec.astype(np.float64).T)
+    res = check_f32_accumulate(y[ok], gold, dec, x[ok])
+    assert res["finite"] and res["north_star"] and res["reference"], res
+
+
+@pytest.mark.parametrize("stream", [True, False], ids=["stream", "ksplit"])
+def test_f16_small_batch_wide_activation_range(gpu, knobs, stream):
+    # activations from 2^-60 to 2^60 inside one chunk, largest finite F16
+    # weights and subnormal ones: the hi/lo split keeps the F32-accumulate bound
+    if not stream:
+        knobs("KUNLUN_DENSE_STREAM", "0")
+    k, n, batch = 4096, 96, 8
+    rng = np.random.default_rng(6)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
+    w[:, ::97] = np.float16(65504.0)
+    w[:, 5::97] = np.float16(2.0 ** -24)
+    mag = np.exp2(rng.integers(-60, 61, size=(batch, k))).astype(np.float32)
+    x = (rng.standard_normal((batch, k)) * mag).astype(np.float32)
+    x[7] = rng.standard_normal(k).astype(np.float32) * np.float32(3e38 / 65504 / 64)   # near the F32 range
+    y, route, guard_ok = run_matmul(kl.WeightType.f16, w.view(np.uint8), x, k, n, batch)
+    assert route == "f16_mfma_gemv" and guard_ok
+    dec = w.astype(np.float32)
+    gold = x.astype(np.float64) @ dec.astype(np.float64).T
+    res = check_f32_accumulate(y, gold, dec, x)
+    # terms of 2^60 and more cancel in places, so only the norm bound holds
+    # for every F32-accumulate order; the relative bound is not asserted
+    assert res["finite"] and res["north_star"], res
 
 
 # --- Q4_0 with F16-subnormal block scales ----------------------------------------
