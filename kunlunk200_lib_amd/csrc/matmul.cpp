@@ -65,6 +65,13 @@ bool q4_bdiag_batch(int batch) {
     return kk::tuning_or(kk::kQ4Bdiag, 1) != 0 && q4_mfma_batch(batch, true);
 }
 
+// Batch range of the streamed Q4_0 GEMV at K = 4096: KUNLUN_Q4_STREAM_MIN
+// (default 5) to 8; a minimum above 8 turns it off.
+bool q4_stream_batch(int batch) {
+    const int min_b = kk::tuning_or(kk::kQ4StreamMin, 5);
+    return batch >= std::max(1, min_b) && batch <= 8;
+}
+
 // Batch range of the single-pass F32/F16 MFMA GEMV (within 1..16).
 bool dense_mfma_batch(int batch) {
     const int min_b = std::max(1, kk::tuning_or(kk::kDenseMfmaMin, 2));
@@ -172,6 +179,12 @@ void matmul(Kernel & kernel, int id, void * y, const void * w, const void * x, i
                                                          static_cast<float *>(y), k, n, batch, ctx.stream),
                           "kk_dense_mfma_gemv");
         impl.route = type == WeightType::f16 ? "f16_mfma_gemv" : "f32_mfma_gemv";
+    } else if (type == WeightType::q4_0 && kk::q4_stream_batch(batch) &&
+               kk_q4_stream_gemv_supported(w, static_cast<const float *>(x), k, n, batch)) {
+        detail::check_hip((hipError_t)kk_q4_stream_gemv(w, static_cast<const float *>(x), static_cast<float *>(y), k, n,
+                                                        batch, ctx.cus, ctx.stream),
+                          "kk_q4_stream_gemv");
+        impl.route = "q4_stream_gemv";
     } else if (type == WeightType::q4_0 && kk::q4_bdiag_batch(batch) &&
                kk_q4_bdiag_gemv_supported(w, static_cast<const float *>(x), k, n, batch)) {
         detail::check_hip((hipError_t)kk_q4_bdiag_gemv(w, static_cast<const float *>(x), static_cast<float *>(y), k, n,

@@ -100,6 +100,9 @@ extern "C" int kunlun_matmul_noalloc(int device, void *y, const void *w, const v
     } else if ((type == 0 || type == 1) && kk::dense_mfma_batch(batch) && (wa & 15) == 0 && (xa & 15) == 0) {
         rc = static_cast<hipError_t>(kk_dense_mfma_gemv(type, w, xf, yf, k, n, batch, s));
         taken = type == 1 ? "f16_mfma_gemv" : "f32_mfma_gemv";
+    } else if (type == 2 && kk::q4_stream_batch(batch) && kk_q4_stream_gemv_supported(w, xf, k, n, batch)) {
+        rc = static_cast<hipError_t>(kk_q4_stream_gemv(w, xf, yf, k, n, batch, d.cus, s));
+        taken = "q4_stream_gemv";
     } else if (type == 2 && kk::q4_bdiag_batch(batch) && kk_q4_bdiag_gemv_supported(w, xf, k, n, batch)) {
         rc = static_cast<hipError_t>(kk_q4_bdiag_gemv(w, xf, yf, k, n, batch, d.cus, s));
         taken = "q4_bdiag_gemv";

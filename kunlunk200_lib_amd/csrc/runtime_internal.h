@@ -45,6 +45,7 @@ namespace kk {
 int gemm_min_batch();
 bool q4_mfma_batch(int batch, bool streamed);
 bool q4_bdiag_batch(int batch);
+bool q4_stream_batch(int batch);
 bool dense_mfma_batch(int batch);
 } // namespace kk
 

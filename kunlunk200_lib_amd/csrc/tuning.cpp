@@ -27,6 +27,7 @@ constexpr KnobName kNames[] = {
     {kQ4GemvPlanes, "KUNLUN_Q4_GEMV_PLANES"},
     {kQ4Bdiag, "KUNLUN_Q4_BDIAG"},
     {kDenseStream, "KUNLUN_DENSE_STREAM"},
+    {kQ4StreamMin, "KUNLUN_Q4_STREAM_MIN"},
 };
 static_assert(sizeof(kNames) / sizeof(kNames[0]) == kKnobCount, "every knob has a name");
 

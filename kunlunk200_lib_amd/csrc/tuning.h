@@ -19,6 +19,7 @@ enum Knob {
     kQ4GemvPlanes,        // KUNLUN_Q4_GEMV_PLANES=1: batch-1 Q4_0 GEMV on the LDS-staged digit-plane kernel
     kQ4Bdiag,             // KUNLUN_Q4_BDIAG=0: the Q4_0 MFMA GEMV batch range on the LDS-staged kernels instead
     kDenseStream,         // KUNLUN_DENSE_STREAM=0: F16 batch 2..8 at K <= 4096 on the K-split kernel, not the streamed one
+    kQ4StreamMin,         // KUNLUN_Q4_STREAM_MIN: smallest batch (default 5, up to 8) on the streamed Q4_0 GEMV at K = 4096
     kKnobCount
 };
 

@@ -19,7 +19,8 @@ kernels/q4-device.h:3-12).
 * Q4_0: rows whose block scales are F16 subnormals (all blocks, or every other
   block beside normal scales), with random nibbles and Gaussian activations,
   on every Q4_0 route: q4_gemv_dot8 (batch 1 and 2), q4_gemv_planes (batch 1
-  under KUNLUN_Q4_GEMV_PLANES=1), the block-diagonal q4_bdiag_gemv, the
+  under KUNLUN_Q4_GEMV_PLANES=1), the streamed q4_stream_gemv (K = 4096,
+  batch 5..8), the block-diagonal q4_bdiag_gemv, the
   streamed and the register-staged q4_mfma_gemv (under KUNLUN_Q4_BDIAG=0),
   the LDS GEMM and the register-staged GEMM, native_q4_matmul and common_q4_matmul (M = 1 and M > 1). Each route meets
   its own bound against FP64 gold of the exactly decoded weights: the
@@ -191,7 +192,9 @@ Q4_ROUTES = [
     (4096, 1, 0, "q4_gemv_planes", 1e-4),      # opt-in batch-1 route (KUNLUN_Q4_GEMV_PLANES=1)
     (1088, 1, 0, "q4_gemv_dot8", 1e-4),        # K % 128 != 0
     (4096, 2, 0, "q4_gemv_dot8", 1e-4),
-    (4096, 8, 0, "q4_bdiag_gemv", 1e-4),       # block-diagonal MFMA GEMV
+    (4096, 8, 0, "q4_stream_gemv", 1e-4),      # streamed MFMA GEMV (K = 4096, batch 5..8)
+    (4096, 6, 0, "q4_stream_gemv", 1e-4),
+    (4096, 8, 0, "q4_bdiag_gemv", 1e-4),       # block-diagonal MFMA GEMV (KUNLUN_Q4_STREAM_MIN=9)
     (1088, 8, 0, "q4_bdiag_gemv", 1e-4),
     (4096, 8, 0, "q4_mfma_gemv", 1e-4),        # streamed (KUNLUN_Q4_BDIAG=0; K % 256 == 0, 16-byte aligned)
     (1088, 8, 0, "q4_mfma_gemv", 1e-4),        # register-staged (KUNLUN_Q4_BDIAG=0; K % 256 != 0)
@@ -209,6 +212,8 @@ def test_q4_subnormal_scales(gpu, oracle, knobs, k, batch, w_offset, route, tol,
         knobs("KUNLUN_Q4_GEMV_PLANES", "1")
     if route == "q4_mfma_gemv":
         knobs("KUNLUN_Q4_BDIAG", "0")
+    if route != "q4_stream_gemv":
+        knobs("KUNLUN_Q4_STREAM_MIN", "9")
     n = 160
     mixed = scales.endswith("mixed")
     tiny = scales.startswith("tiny") or scales == "low_normal"

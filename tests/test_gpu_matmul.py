@@ -269,7 +269,7 @@ def test_rowwise_i8_nonfinite_activation_aborts_at_wait(gpu, k, batch):
     (4096, 32000, 1, "q4_gemv_dot8"),      # configs[1]: LM head
     (4096, 14336, 2, "q4_gemv_dot8"),      # configs[2]: batch 2 (two columns per pass)
     (4096, 14336, 4, "q4_bdiag_gemv"),     # activation fragments of all of K fit in LDS
-    (4096, 14336, 8, "q4_bdiag_gemv"),
+    (4096, 14336, 8, "q4_stream_gemv"),    # batch 5..8 at K = 4096: rows streamed through per-wave LDS
     (4096, 14336, 16, "q4_mfma_gemv"),     # they do not: the LDS-staged kernel
 ])
 def test_q4_baseline_configs_default_route(gpu, oracle, k, n, batch, route):

@@ -1,7 +1,9 @@
 """GPU parity of the single-pass small-batch Q4_0 GEMVs (batch 2..16, fp16
-MFMA with hi/lo activations): the block-diagonal kernel (q4_bdiag_gemv,
-where the activation fragments of all of K fit in LDS) and the LDS-staged
-kernels (q4_mfma_gemv, everywhere else and under KUNLUN_Q4_BDIAG=0), on
+MFMA with hi/lo activations): the streamed kernel (q4_stream_gemv, K = 4096
+and batch <= 8, from batch 5 by default, from 2 under KUNLUN_Q4_STREAM_MIN=2),
+the block-diagonal kernel (q4_bdiag_gemv, where the activation fragments of
+all of K fit in LDS) and the LDS-staged kernels (q4_mfma_gemv, everywhere else
+and under KUNLUN_Q4_BDIAG=0), on
 BASELINE configs[2] shapes, K chunk tails, N tails, extreme and zero
 activation rows, against the FP64 gold of the exactly decoded weights
 (reference bench/library-bench.cpp:121-122) with the f32-accumulate bound
@@ -18,7 +20,7 @@ from gpu_util import check_f32_accumulate, run_matmul
 
 pytestmark = pytest.mark.gpu
 
-KERNELS = ["bdiag", "lds"]
+KERNELS = ["bdiag", "lds", "stream"]
 
 
 def gaussian(shape, sigma, seed):
@@ -44,8 +46,10 @@ def bdiag_fits(k, batch):
     return False
 
 
-def expected_route(kernel, k, batch):
-    return "q4_bdiag_gemv" if kernel == "bdiag" and bdiag_fits(k, batch) else "q4_mfma_gemv"
+def expected_route(kernel, k, batch, w_offset=0):
+    if kernel == "stream" and k == 4096 and batch <= 8 and w_offset % 16 == 0:
+        return "q4_stream_gemv"
+    return "q4_bdiag_gemv" if kernel != "lds" and bdiag_fits(k, batch) else "q4_mfma_gemv"
 
 
 @pytest.fixture(autouse=True)
@@ -55,7 +59,8 @@ def mfma_from_batch_two(gpu, knobs):
 
 @pytest.fixture(params=KERNELS)
 def kernel(request, knobs):
-    knobs("KUNLUN_Q4_BDIAG", "1" if request.param == "bdiag" else "0")
+    knobs("KUNLUN_Q4_BDIAG", "0" if request.param == "lds" else "1")
+    knobs("KUNLUN_Q4_STREAM_MIN", "2" if request.param == "stream" else "9")
     return request.param
 
 
@@ -105,7 +110,7 @@ def test_weights_off_16_bytes(gpu, oracle, kernel):
     for w_offset in (0, 4):
         y, route, guard_ok = run_matmul(kl.WeightType.q4_0, q4, x, k, n, batch, w_offset=w_offset)
         res = check_f32_accumulate(y, gold, dec, x)
-        assert route == expected_route(kernel, k, batch)
+        assert route == expected_route(kernel, k, batch, w_offset)
         assert guard_ok and res["finite"] and res["north_star"] and res["reference"]
 
 
@@ -115,7 +120,12 @@ def test_default_batch_routing(gpu, oracle, kernel):
     # 0, 16-byte aligned weights) from batch 3, the register-staged one from
     # batch 5, batch-1 passes below
     kl.set_tuning("KUNLUN_Q4_MFMA_MIN", None)
-    if kernel == "bdiag":
+    if kernel == "stream":
+        # streamed from batch 5 at K = 4096 (16-byte aligned weights), else as before
+        kl.set_tuning("KUNLUN_Q4_STREAM_MIN", None)
+        cases = [(4096, 5, 0, "q4_stream_gemv"), (4096, 8, 0, "q4_stream_gemv"), (4096, 4, 0, "q4_bdiag_gemv"),
+                 (4096, 8, 4, "q4_bdiag_gemv"), (512, 8, 0, "q4_bdiag_gemv"), (4096, 9, 0, "q4_mfma_gemv")]
+    elif kernel == "bdiag":
         cases = [(512, 3, 0, "q4_bdiag_gemv"), (512, 2, 0, "q4_gemv_dot8"), (576, 3, 0, "q4_bdiag_gemv"),
                  (576, 5, 0, "q4_bdiag_gemv"), (512, 4, 4, "q4_bdiag_gemv"), (4096, 16, 0, "q4_mfma_gemv")]
     else:
@@ -146,6 +156,26 @@ def test_extreme_rows(gpu, oracle, kernel):
     assert np.all(y[3] == 0.0)
 
 
+def test_stream_nonfinite_activation_poisons_column(gpu, oracle, knobs):
+    # an Inf or NaN in a batch column makes that column NaN in every row (the
+    # batch-1 GEMV's rule); the other columns keep the bound
+    knobs("KUNLUN_Q4_STREAM_MIN", "2")
+    k, n, batch = 4096, 100, 6
+    x = gaussian((batch, k), 1.0, 31)
+    x[2, 5] = np.inf
+    x[4, 3000] = np.nan
+    x[5, 4095] = -np.inf
+    w = gaussian((n, k), 0.02, 32)
+    q4 = kl.quantize_q4_0(w)
+    dec = oracle.q4_decode(q4, k, n)
+    y, route, guard_ok = run_matmul(kl.WeightType.q4_0, q4, x, k, n, batch)
+    assert route == "q4_stream_gemv" and guard_ok
+    assert np.all(np.isnan(y[[2, 4, 5]]))
+    ok = [0, 1, 3]
+    res = check_f32_accumulate(y[ok], oracle.gold(dec, x[ok]), dec, x[ok])
+    assert res["finite"] and res["north_star"] and res["reference"], res
+
+
 def test_matches_batch_one_kernel(gpu, oracle, knobs, kernel):
     # the same call with the MFMA GEMV disabled (pairs of dot8 columns)
     k, n, batch = 4096, 1000, 8
@@ -154,6 +184,7 @@ def test_matches_batch_one_kernel(gpu, oracle, knobs, kernel):
     q4 = kl.quantize_q4_0(w)
     y_mfma, r1, _ = run_matmul(kl.WeightType.q4_0, q4, x, k, n, batch)
     knobs("KUNLUN_Q4_MFMA_MIN", "17")
+    knobs("KUNLUN_Q4_STREAM_MIN", "9")
     y_dot8, r2, _ = run_matmul(kl.WeightType.q4_0, q4, x, k, n, batch)
     assert r1 == expected_route(kernel, k, batch) and r2 == "q4_gemv_dot8"
     dec = oracle.q4_decode(q4, k, n)

@@ -20,7 +20,8 @@ CASES = [
     (Q4, "q4_gemm_mfma", (4096, 1024, 128), (2048, 520, 64)),     # LDS GEMM, scratch: fp16 X + row scales
     (Q4, "q4_gemm_mfma", (1088, 384, 96), (544, 130, 64)),        # register-staged GEMM (K % 256 != 0)
     (F16, "f16_gemm_mfma", (1024, 256, 96), (512, 130, 64)),      # F16 GEMM
-    (Q4, "q4_bdiag_gemv", (4096, 2048, 8), (1024, 300, 4)),       # block-diagonal MFMA GEMV, no scratch
+    (Q4, "q4_stream_gemv", (4096, 2048, 8), (4096, 300, 5)),      # streamed MFMA GEMV (K = 4096), no scratch
+    (Q4, "q4_bdiag_gemv", (1024, 2048, 8), (1024, 300, 4)),       # block-diagonal MFMA GEMV, no scratch
     (Q4, "q4_mfma_gemv", (4096, 2048, 16), (4096, 300, 12)),      # LDS-staged MFMA GEMV, scratch: X fragments
     (Q4, "q4_gemv_dot8", (4096, 1024, 1), (1024, 129, 1)),        # no scratch
     (F32, "f32_mfma_gemv", (1024, 256, 8), (512, 65, 2)),         # no scratch
