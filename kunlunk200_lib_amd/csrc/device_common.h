@@ -115,6 +115,13 @@ __device__ __forceinline__ u32x4_a4 load_u32x4(const uint32_t *p) {
     return *reinterpret_cast<const u32x4_a4 *>(p);
 }
 
+// The same with the non-temporal hint, for weight bytes read once per call
+// (streamed past the caches instead of displacing reused data such as X).
+__device__ __forceinline__ u32x4_a4 load_u32x4_stream(const uint32_t *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4 *>(p));
+}
+__device__ __forceinline__ uint32_t load_u32_stream(const uint32_t *p) { return __builtin_nontemporal_load(p); }
+
 // Eight activations as signed fixed point X_t = rint(v[t] * to_fixed) (round
 // to nearest even via the 1.5 * 2^23 magic constant, one FMA), written as
 // DIGITS balanced base-16 digits in [-8, 7]. With FRAC = 4 * DIGITS - 2,

@@ -441,7 +441,9 @@ __global__ __launch_bounds__(64 * WAVES) void dense_stream(const uint8_t *__rest
         const int ord = it / chunks, c = it - ord * chunks;
         const int r = min(wave + ord * nwaves, n - 1);
         const uint32_t off = min(static_cast<uint32_t>(c) * 1024u + 16u * lane, row_bytes - 16u);
-        v = *reinterpret_cast<const uint4 *>(w + static_cast<size_t>(r) * row_bytes + off);
+        typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+        const u32x4v t = __builtin_nontemporal_load(reinterpret_cast<const u32x4v *>(w + static_cast<size_t>(r) * row_bytes + off));
+        v = make_uint4(t[0], t[1], t[2], t[3]);
     };
     uint4 ring[DEPTH];
 #pragma unroll

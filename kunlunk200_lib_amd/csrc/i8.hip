@@ -622,7 +622,7 @@ __global__ __launch_bounds__(kRowsThreads) void i8_gemv_rows(const float *__rest
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
             const int off = min(1024 * i + 16 * lane, k - 16);
-            wv[j][i] = kk::load_u32x4(reinterpret_cast<const uint32_t *>(w + static_cast<size_t>(r) * k + off));
+            wv[j][i] = kk::load_u32x4_stream(reinterpret_cast<const uint32_t *>(w + static_cast<size_t>(r) * k + off));
         }
     }
     __builtin_amdgcn_sched_barrier(0);

@@ -395,7 +395,7 @@ __device__ __forceinline__ void lg_copy_stage(const uint8_t *frag, int frag_byte
     for (int t = 0; t < L::BCopiesPerWave; ++t)
         if (wid + 8 * t < L::BCopies)                           // wave-uniform
             __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, buf + L::AStageBytes + (wid + 8 * t) * 1024, 16,
-                                                     b_off[t], s * L::RowStage, 0, 0);
+                                                     b_off[t], s * L::RowStage, 0, 2);   // non-temporal: read once
 }
 
 template <int SB, bool PACKED>
@@ -773,7 +773,7 @@ __global__ __launch_bounds__(kWave * kF16sWaves) void f16_stream_gemv(const uint
         const int tile = min(tile0 + t, tiles - 1);
         const int r = min(tile * 16 + i, n - 1);
         const uint32_t off = min(static_cast<uint32_t>(c) * 1024u + 16u * lane, row_bytes - 16u);
-        v = *reinterpret_cast<const u32x4 *>(w + static_cast<size_t>(r) * row_bytes + off);
+        v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(w + static_cast<size_t>(r) * row_bytes + off));
     };
     u32x4 ring[kF16sDepth];
 #pragma unroll

@@ -117,7 +117,7 @@ __global__ __launch_bounds__(kWave * kWaves) void q4_stream_gemv(const uint8_t *
     }
     auto load = [&](int t, int i) {
         return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(tile_buffer(t),
-                                                                              static_cast<int>(goff[i]), 0, 0));
+                                                                              static_cast<int>(goff[i]), 0, 2));
     };
     u32x4 ring_a[kPiecesPerLane], ring_b[kPiecesPerLane];
 #pragma unroll
