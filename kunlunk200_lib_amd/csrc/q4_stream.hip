@@ -184,14 +184,22 @@ __global__ __launch_bounds__(kWave * kWaves) void q4_stream_gemv(const uint8_t *
     };
 
     // 4. per 16-row group: one MFMA per block, then the block scales
-    uint32_t nibble_mask = 0x000f000fu, magic = 0x64006400u;   // (0x6400 | q) is 1024 + q
-    asm volatile("" : "+v"(nibble_mask), "+v"(magic));         // held in VGPRs for v_bfi
+    // (0x6400 | q) is 1024 + q: minus 1032 gives q - 8; a high nibble left in
+    // place, (0x6400 | 16 q) = 1024 + 16 q, times 1/16 minus 72 gives q - 8
+    // (both exact in fp16, one shift per dword)
+    uint32_t low_mask = 0x000f000fu, high_mask = 0x00f000f0u, magic = 0x64006400u;
+    asm volatile("" : "+v"(low_mask), "+v"(high_mask), "+v"(magic));   // held in VGPRs for v_bfi
     auto decode = [&](uint32_t qs) {
         const half2v off = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
-        const half2v a = __builtin_bit_cast(half2v, bit_insert(nibble_mask, qs, magic)) + off;
-        const half2v b = __builtin_bit_cast(half2v, bit_insert(nibble_mask, qs >> 8, magic)) + off;
-        const half2v cc = __builtin_bit_cast(half2v, bit_insert(nibble_mask, qs >> 4, magic)) + off;
-        const half2v d = __builtin_bit_cast(half2v, bit_insert(nibble_mask, qs >> 12, magic)) + off;
+        const half2v sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+        const half2v off16 = {static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
+        const uint32_t s8 = qs >> 8;
+        const half2v a = __builtin_bit_cast(half2v, bit_insert(low_mask, qs, magic)) + off;
+        const half2v b = __builtin_bit_cast(half2v, bit_insert(low_mask, s8, magic)) + off;
+        const half2v cc =
+            __builtin_elementwise_fma(__builtin_bit_cast(half2v, bit_insert(high_mask, qs, magic)), sixteenth, off16);
+        const half2v d =
+            __builtin_elementwise_fma(__builtin_bit_cast(half2v, bit_insert(high_mask, s8, magic)), sixteenth, off16);
         return __builtin_bit_cast(half8, u32x4{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
                                                __builtin_bit_cast(uint32_t, cc), __builtin_bit_cast(uint32_t, d)});
     };
