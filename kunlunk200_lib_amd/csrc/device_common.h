@@ -91,18 +91,26 @@ __device__ __forceinline__ int round_clamp(float value, int limit) {
 
 // Eight Q4_0 values of nibble dword `qs` (its bytes j = 0..3 hold values j in
 // the low nibble and 16 + j in the high nibble) as exact fp16 q - 8, in the
-// order (0, 2, 1, 3, 16, 18, 17, 19): (0x6400 | q) is 1024 + q, and one packed
-// add of -1032 per pair.
+// order (0, 2, 1, 3, 16, 18, 17, 19): (0x6400 | q) is 1024 + q, minus 1032 in
+// one packed add per pair; a high nibble left in place gives (0x6400 | 16 q) =
+// 1024 + 16 q, times 1/16 minus 72 in one packed fma. One shift per dword; the
+// bit inserts (v_bfi_b32) take their masks from VGPRs.
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ uint32_t nibble_insert(uint32_t mask, uint32_t a) {
+    uint32_t r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(mask), "v"(a), "v"(0x64006400u));   // (a & mask) | 0x6400 pair
+    return r;
+}
 __device__ __forceinline__ half8 q4_dword_halves(uint32_t qs) {
     typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-    union { uint32_t u; half2v h; } p0, p1, p2, p3;
-    p0.u = (qs & 0x000f000fu) | 0x64006400u;
-    p1.u = ((qs >> 8) & 0x000f000fu) | 0x64006400u;
-    p2.u = ((qs >> 4) & 0x000f000fu) | 0x64006400u;
-    p3.u = ((qs >> 12) & 0x000f000fu) | 0x64006400u;
+    const uint32_t s8 = qs >> 8;
     const half2v off = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
-    const half2v a = p0.h + off, b = p1.h + off, c = p2.h + off, d = p3.h + off;
+    const half2v sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+    const half2v off16 = {static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
+    const half2v a = __builtin_bit_cast(half2v, nibble_insert(0x000f000fu, qs)) + off;
+    const half2v b = __builtin_bit_cast(half2v, nibble_insert(0x000f000fu, s8)) + off;
+    const half2v c = __builtin_elementwise_fma(__builtin_bit_cast(half2v, nibble_insert(0x00f000f0u, qs)), sixteenth, off16);
+    const half2v d = __builtin_elementwise_fma(__builtin_bit_cast(half2v, nibble_insert(0x00f000f0u, s8)), sixteenth, off16);
     half8 out;
     out[0] = a[0]; out[1] = a[1]; out[2] = b[0]; out[3] = b[1];
     out[4] = c[0]; out[5] = c[1]; out[6] = d[0]; out[7] = d[1];
