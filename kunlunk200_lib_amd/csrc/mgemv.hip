@@ -606,12 +606,16 @@ extern "C" int kk_q4_mfma_gemv(const void *w, const float *x, float *y, int k, i
 // pass over the weights for the whole batch.
 //
 // Workgroup = one 16-row weight tile; its 8 waves take K eighths (32-value
-// steps, 4 in flight per wave) and meet in LDS at the end in wave order. Per step a lane
-// (n = lane % 16, g = lane / 16) loads 8 consecutive weights of row n and the
-// 8 activations of batch row n at k0 + 8g .. k0 + 8g + 7 with 16-byte loads;
-// MFMA t (0..7) of the step takes k0 + 8g + t from lane group g, so both
-// operands come straight from global memory in the MFMA layout (A[m][k] in
-// lane m + 16 k, B[k][n] in lane n + 16 k, D[4g + i][n] in lane n + 16 g).
+// steps, 4 in flight per wave) and meet in LDS at the end in wave order.
+// MFMA t (0..7) of a step takes k0 + 8g + t from lane group g (A[m][k] in
+// lane m + 16 k, B[k][n] in lane n + 16 k, D[4g + i][n] in lane n + 16 g), so
+// lane (n, g) needs weights and activations k0 + 8g .. k0 + 8g + 7 of row n.
+// The loads are laid out for the cache instead: lane l reads row l / 4 (and
+// batch row l / 4), 16-byte piece 2 (l % 4) of the step in one load and piece
+// 2 (l % 4) + 1 in the other (F16: piece l % 4), so each group of 4 lanes
+// stays in one cache line (a load whose lanes read 16 different rows costs
+// several times more), and ds_bpermute moves lane 4n + g's values to lane
+// (n, g): the same values in the same MFMA order.
 namespace {
 
 constexpr int kDenseWaves = 8;     // K split over the workgroup's waves (two per SIMD)
@@ -627,15 +631,18 @@ __global__ __launch_bounds__(kWave * kDenseWaves) void dense_mfma_gemv(const uin
     const int lane = tid & (kWave - 1);
     const int q = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nl = lane & 15, g = lane >> 4;
-    const int r = min(static_cast<int>(blockIdx.x) * 16 + nl, n - 1);
-    const bool live_m = nl < batch;
-    const float *xrow = x + static_cast<size_t>(min(nl, batch - 1)) * k + 8 * g;
-    const uint8_t *wrow = w + static_cast<size_t>(r) * k * (F16W ? 2 : 4) + 8 * g * (F16W ? 2 : 4);
+    const int lr = lane >> 2, lp = lane & 3;                   // loader row and piece pair
+    const int r = min(static_cast<int>(blockIdx.x) * 16 + lr, n - 1);
+    const bool live_m = lr < batch;
+    const float *xrow = x + static_cast<size_t>(min(lr, batch - 1)) * k + 8 * lp;
+    const uint8_t *wrow = w + static_cast<size_t>(r) * k * (F16W ? 2 : 4) + (F16W ? 16 : 32) * lp;
+    const int src = (4 * nl + g) * 4;                          // lane (n, g) takes loader lane 4n + g
     const int steps = k >> 5;
     const int s0 = steps * q / kDenseWaves, s1 = steps * (q + 1) / kDenseWaves;
 
     // one step: 8 activations and 8 weights of this lane (a past-the-end step
     // reloads the wave's last step; its MFMAs are skipped)
+    // b holds 8 F32 weights, or (F16) 4 dwords of raw halves widened after the move
     auto load = [&](int s, float (&a)[8], float (&b)[8]) {
         s = min(s, max(s1 - 1, s0));
         const float4 *xs = reinterpret_cast<const float4 *>(xrow + static_cast<size_t>(s) * 32);
@@ -644,13 +651,30 @@ __global__ __launch_bounds__(kWave * kDenseWaves) void dense_mfma_gemv(const uin
 #pragma unroll
         for (int t = 0; t < 8; ++t) a[t] = live_m ? a[t] : 0.0f;
         if constexpr (F16W) {
-            const half8 h = *reinterpret_cast<const half8 *>(wrow + static_cast<size_t>(s) * 64);
-#pragma unroll
-            for (int t = 0; t < 8; ++t) b[t] = static_cast<float>(h[t]);
+            const uint4 h = *reinterpret_cast<const uint4 *>(wrow + static_cast<size_t>(s) * 64);
+            b[0] = __uint_as_float(h.x); b[1] = __uint_as_float(h.y); b[2] = __uint_as_float(h.z); b[3] = __uint_as_float(h.w);
         } else {
-            const float4 *ws = reinterpret_cast<const float4 *>(wrow + static_cast<size_t>(s) * 128);
-            const float4 w0 = ws[0], w1 = ws[1];
+            const uint8_t *ws = wrow + static_cast<size_t>(s) * 128;
+            const float4 w0 = *reinterpret_cast<const float4 *>(ws), w1 = *reinterpret_cast<const float4 *>(ws + 16);
             b[0] = w0.x; b[1] = w0.y; b[2] = w0.z; b[3] = w0.w; b[4] = w1.x; b[5] = w1.y; b[6] = w1.z; b[7] = w1.w;
+        }
+    };
+    auto to_mfma_layout = [&](float (&a)[8], float (&b)[8]) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) a[t] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(a[t])));
+        if constexpr (F16W) {
+            float wide[8];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t u = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, __float_as_int(b[t])));
+                wide[2 * t] = kk::half_bits_to_float(u & 0xffffu);
+                wide[2 * t + 1] = kk::half_bits_to_float(u >> 16);
+            }
+#pragma unroll
+            for (int t = 0; t < 8; ++t) b[t] = wide[t];
+        } else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) b[t] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(b[t])));
         }
     };
 
@@ -666,6 +690,7 @@ __global__ __launch_bounds__(kWave * kDenseWaves) void dense_mfma_gemv(const uin
 #pragma unroll
                 for (int t = 0; t < 8; ++t) { ca[t] = a[d][t]; cb[t] = b[d][t]; }
                 load(s + d + kDenseDepth, a[d], b[d]);
+                to_mfma_layout(ca, cb);
 #pragma unroll
                 for (int t = 0; t < 8; t += 2) {
                     acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(ca[t], cb[t], acc0, 0, 0, 0);
