@@ -360,9 +360,12 @@ __global__ __launch_bounds__(256) void i8_mfma_matmul(const int8_t *__restrict__
 
 // Batch 1..64 (2*batch <= 16 MT code rows: MT MFMA row tiles): one
 // workgroup per 16 weight rows, its 8 waves splitting K into contiguous ranges
-// of 64-value steps; a chunk of steps is loaded before its MFMAs (16 B per
-// lane and operand row tile per step: row l % 16 at k0 + 16 (l / 16)). The
-// waves' int32 sums meet in LDS (exact in any order), then the combine.
+// of 64-value steps; a chunk of steps is loaded before its MFMAs. The MFMA
+// wants row l % 16 at k0 + 16 (l / 16) in lane l; the loads read row l / 4
+// at k0 + 16 (l % 4) instead (a group of 4 lanes in one row: a load whose
+// lanes read 16 rows costs several times more), and ds_bpermute moves lane
+// 4 (l % 16) + l / 16's 16 bytes to lane l. The waves' int32 sums meet in LDS
+// (exact in any order), then the combine.
 constexpr int kGemvWaves = 8;
 template <int MT>
 __global__ __launch_bounds__(kGemvWaves * kWave) void i8_gemv_ksplit(const int8_t *__restrict__ codes,
@@ -381,10 +384,16 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void i8_gemv_ksplit(const int8_
     const int steps = (k + 63) / 64;
     const int per = (steps + kGemvWaves - 1) / kGemvWaves;
     const int s0 = wid * per, s1 = min(steps, s0 + per);
+    const int lr = lane >> 2, lp = lane & 3;                   // loader row and 16-byte piece
+    const int src = (4 * c + g) * 4;                           // lane (c, g) takes loader lane 4c + g
     const int8_t *arow[MT];
 #pragma unroll
-    for (int i = 0; i < MT; ++i) arow[i] = codes + static_cast<size_t>(16 * i + c < rows ? 16 * i + c : 0) * k;
-    const int8_t *brow = w + static_cast<size_t>(min(n0 + c, n - 1)) * k;
+    for (int i = 0; i < MT; ++i) arow[i] = codes + static_cast<size_t>(16 * i + lr < rows ? 16 * i + lr : 0) * k;
+    const int8_t *brow = w + static_cast<size_t>(min(n0 + lr, n - 1)) * k;
+    auto to_mfma_lane = [&](const int32x4 &v) {
+        return int32x4{__builtin_amdgcn_ds_bpermute(src, v[0]), __builtin_amdgcn_ds_bpermute(src, v[1]),
+                       __builtin_amdgcn_ds_bpermute(src, v[2]), __builtin_amdgcn_ds_bpermute(src, v[3])};
+    };
 
     int32x4 acc[MT];
 #pragma unroll
@@ -393,7 +402,7 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void i8_gemv_ksplit(const int8_
         int32x4 af[kChunk][MT], bf[kChunk];
 #pragma unroll
         for (int t = 0; t < kChunk; ++t) {
-            const int kk0 = (sc + t) * 64 + 16 * g;
+            const int kk0 = (sc + t) * 64 + 16 * lp;
             const bool ok = sc + t < s1 && kk0 < k;             // K % 32 == 0: a 16-byte chunk is all in or out
             if (ok) {
                 const kk::u32x4_a4 b = kk::load_u32x4(reinterpret_cast<const uint32_t *>(brow + kk0));
@@ -403,7 +412,7 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void i8_gemv_ksplit(const int8_
             }
 #pragma unroll
             for (int i = 0; i < MT; ++i) {
-                if (ok && 16 * i + c < rows) {
+                if (ok && 16 * i + lr < rows) {
                     const kk::u32x4_a4 a = kk::load_u32x4(reinterpret_cast<const uint32_t *>(arow[i] + kk0));
                     af[t][i] = int32x4{static_cast<int>(a.x), static_cast<int>(a.y), static_cast<int>(a.z), static_cast<int>(a.w)};
                 } else {
@@ -412,9 +421,12 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void i8_gemv_ksplit(const int8_
             }
         }
 #pragma unroll
-        for (int t = 0; t < kChunk; ++t)
+        for (int t = 0; t < kChunk; ++t) {
+            const int32x4 b = to_mfma_lane(bf[t]);
 #pragma unroll
-            for (int i = 0; i < MT; ++i) acc[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[t][i], bf[t], acc[i], 0, 0, 0);
+            for (int i = 0; i < MT; ++i)
+                acc[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(to_mfma_lane(af[t][i]), b, acc[i], 0, 0, 0);
+        }
     }
     if (wid > 0) {
 #pragma unroll
