@@ -90,7 +90,8 @@ def test_config2_shapes(gpu, oracle, kernel, batch):
 # K-part splits of 1, 2 and 4 tiles per workgroup
 @pytest.mark.parametrize("k,n,batch", [(64, 1, 2), (64, 17, 16), (4160, 33, 3), (11008, 4096, 4), (16384, 70, 16),
                                        (1024, 16, 5), (2048, 1000, 9), (4096, 4096, 15), (576, 130, 12),
-                                       (8192, 300, 4), (2048, 5000, 16), (4096, 4200, 7)])
+                                       (8192, 300, 4), (2048, 5000, 16), (4096, 4200, 7),
+                                       (4096, 1, 6), (4096, 33, 8)])   # streamed kernel: one row, one partial tile
 def test_tails(gpu, oracle, kernel, k, n, batch):
     y, route, guard_ok, res = q4_case(oracle, k, n, batch, k + n + batch)
     assert route == expected_route(kernel, k, batch)
@@ -210,7 +211,9 @@ def dense_case(oracle, type_, k, n, batch, seed):
 
 @pytest.mark.parametrize("type_", [kl.WeightType.f16, kl.WeightType.f32], ids=["f16", "f32"])
 @pytest.mark.parametrize("k,n,batch", [(4096, 4096, 8), (4096, 4096, 2), (4096, 1000, 16), (32, 17, 3),
-                                       (16384, 40, 5), (11008, 300, 12), (96, 1, 16)])
+                                       (16384, 40, 5), (11008, 300, 12), (96, 1, 16),
+                                       (4096, 1, 8), (4064, 17, 5), (544, 4100, 7)])   # F16 streamed: one row,
+                                                                                    # a partial last chunk, N tail
 def test_dense_mfma(gpu, oracle, type_, k, n, batch):
     _, route, guard_ok, res, _, _ = dense_case(oracle, type_, k, n, batch, k + 5 * n + batch)
     assert route == ("f16_mfma_gemv" if type_ == kl.WeightType.f16 else "f32_mfma_gemv")
