@@ -279,7 +279,9 @@ __global__ __launch_bounds__(kCqThreads) void common_gemv(GemvMatrix m0, GemvMat
     auto load_item = [&](int s, uint32_t (&buf)[5]) {
         const int it = min(wid + kCqWaves * s, pairs - 1);
         const int blk = 2 * it + (lane >> 5);
-        const uint4 v = *reinterpret_cast<const uint4 *>(mat.w + (tile_block0 + blk) * 512 + chunk * 16);
+        // 1 KB contiguous per wave, read once per call: non-temporal
+        const kk::u32x4_a4 v = kk::load_u32x4_stream(
+            reinterpret_cast<const uint32_t *>(mat.w + (tile_block0 + blk) * 512 + chunk * 16));
         buf[0] = v.x;
         buf[1] = v.y;
         buf[2] = v.z;
