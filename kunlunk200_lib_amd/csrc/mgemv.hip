@@ -606,7 +606,10 @@ extern "C" int kk_q4_mfma_gemv(const void *w, const float *x, float *y, int k, i
 // pass over the weights for the whole batch.
 //
 // Workgroup = one 16-row weight tile; its 8 waves take K eighths (32-value
-// steps, 4 in flight per wave) and meet in LDS at the end in wave order.
+// steps, 2 in flight per wave) and meet in LDS at the end in wave order.
+// Two steps keep the kernel at 66 VGPRs, so 7 waves fit per SIMD and more
+// tiles' loads are in flight per CU than deeper per-wave rings give (at
+// 4096 x 4096, F32 batch 8: 15.7 us at 2 steps, 18.4 at 4, 21.7 at 1).
 // MFMA t (0..7) of a step takes k0 + 8g + t from lane group g (A[m][k] in
 // lane m + 16 k, B[k][n] in lane n + 16 k, D[4g + i][n] in lane n + 16 g), so
 // lane (n, g) needs weights and activations k0 + 8g .. k0 + 8g + 7 of row n.
@@ -619,7 +622,7 @@ extern "C" int kk_q4_mfma_gemv(const void *w, const float *x, float *y, int k, i
 namespace {
 
 constexpr int kDenseWaves = 8;     // K split over the workgroup's waves (two per SIMD)
-constexpr int kDenseDepth = 4;     // 32-value steps of loads in flight per wave
+constexpr int kDenseDepth = 2;     // 32-value steps of loads in flight per wave
 
 template <bool F16W>
 __global__ __launch_bounds__(kWave * kDenseWaves) void dense_mfma_gemv(const uint8_t *__restrict__ w,
