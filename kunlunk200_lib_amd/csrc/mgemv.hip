@@ -607,9 +607,9 @@ extern "C" int kk_q4_mfma_gemv(const void *w, const float *x, float *y, int k, i
 //
 // Workgroup = one 16-row weight tile; its 8 waves take K eighths (32-value
 // steps, 2 in flight per wave) and meet in LDS at the end in wave order.
-// Two steps keep the kernel at 66 VGPRs, so 7 waves fit per SIMD and more
-// tiles' loads are in flight per CU than deeper per-wave rings give (at
-// 4096 x 4096, F32 batch 8: 15.7 us at 2 steps, 18.4 at 4, 21.7 at 1).
+// Two steps in flight measured fastest (4096 x 4096, F32 batch 8: 15.7 us
+// at 2 steps, 17.1 at 3, 18.4 at 4, 21.7 at 1); there a launch is one
+// workgroup per CU, each wave with 64 KiB of loads to issue.
 // MFMA t (0..7) of a step takes k0 + 8g + t from lane group g (A[m][k] in
 // lane m + 16 k, B[k][n] in lane n + 16 k, D[4g + i][n] in lane n + 16 g), so
 // lane (n, g) needs weights and activations k0 + 8g .. k0 + 8g + 7 of row n.
