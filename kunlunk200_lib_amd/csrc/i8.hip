@@ -95,6 +95,12 @@ __device__ __forceinline__ size_t group_code_offset(size_t flat4, int k, int com
     const size_t b = flat4 / static_cast<size_t>(k), j = flat4 - b * static_cast<size_t>(k);
     return (2 * b + component) * static_cast<size_t>(k) + j;
 }
+// The same offset in 32-bit arithmetic, for 2 * batch * k < 2^32 (a 64-bit
+// division is a long instruction sequence; a 32-bit one a few).
+__device__ __forceinline__ uint32_t group_code_offset32(uint32_t flat4, uint32_t k, int component) {
+    const uint32_t b = flat4 / k, j = flat4 - b * k;
+    return (2 * b + static_cast<uint32_t>(component)) * k + j;
+}
 __device__ __forceinline__ uint32_t pack_codes(int a, int b, int c, int d) {
     return (static_cast<uint32_t>(a) & 0xffu) | ((static_cast<uint32_t>(b) & 0xffu) << 8) |
            ((static_cast<uint32_t>(c) & 0xffu) << 16) | (static_cast<uint32_t>(d) << 24);
@@ -185,8 +191,13 @@ __global__ __launch_bounds__(kQuantThreads) void i8_pass_residual(const float *_
 }
 
 // All three passes in one workgroup, for small X (count <= 4 * kFusedThreads *
-// kFusedGroups): each thread loads its groups once and keeps them in registers.
+// kFusedGroups = 65536, so code offsets fit 32 bits): each thread loads its
+// groups once and keeps them in registers. The arithmetic runs on one CU (about
+// 0.2 us per 1024 values), so by default it takes X only up to 16384 values,
+// where it costs as much as the three grid passes (K4096: 8.8 us at 16384
+// values, 12.5 at 32768, 18.9 at 65536; the passes about 9.7 together).
 constexpr int kFusedGroups = 16;
+constexpr int kFusedQuantDefault = 16384;
 __global__ __launch_bounds__(kFusedThreads) void i8_quantize_fused(const float *__restrict__ x, size_t count, int k,
                                                                   int8_t *__restrict__ codes,
                                                                   float *__restrict__ final_max, int *status) {
@@ -212,7 +223,7 @@ __global__ __launch_bounds__(kFusedThreads) void i8_quantize_fused(const float *
         if (q >= groups4) break;
         const int a = quant_primary(v[t].x, max0), b = quant_primary(v[t].y, max0);
         const int c = quant_primary(v[t].z, max0), d = quant_primary(v[t].w, max0);
-        *reinterpret_cast<uint32_t *>(codes + group_code_offset(4 * static_cast<size_t>(q), k, 0)) = pack_codes(a, b, c, d);
+        *reinterpret_cast<uint32_t *>(codes + group_code_offset32(4u * q, k, 0)) = pack_codes(a, b, c, d);
         m1 = fmaxf(m1, fmaxf(fmaxf(fabsf(residual_of(v[t].x, a, max0)), fabsf(residual_of(v[t].y, b, max0))),
                              fmaxf(fabsf(residual_of(v[t].z, c, max0)), fabsf(residual_of(v[t].w, d, max0)))));
     }
@@ -223,7 +234,7 @@ __global__ __launch_bounds__(kFusedThreads) void i8_quantize_fused(const float *
         const int q = static_cast<int>(threadIdx.x) + kFusedThreads * t;
         if (q >= groups4) break;
         auto q1 = [&](float value) { return quant_residual(residual_of(value, quant_primary(value, max0), max0), max1); };
-        *reinterpret_cast<uint32_t *>(codes + group_code_offset(4 * static_cast<size_t>(q), k, 1)) =
+        *reinterpret_cast<uint32_t *>(codes + group_code_offset32(4u * q, k, 1)) =
             pack_codes(q1(v[t].x), q1(v[t].y), q1(v[t].z), q1(v[t].w));
     }
     if (threadIdx.x == 0) {
@@ -883,7 +894,7 @@ extern "C" int kk_i8_quantize(const float *x, int k, int batch, void *workspace,
     if (!x || !workspace || !status || k <= 0 || batch <= 0) return hipErrorInvalidValue;
     const Workspace ws = layout(workspace, k, batch);
     const size_t count = static_cast<size_t>(k) * batch;
-    const size_t fused_limit = std::min<size_t>(static_cast<size_t>(kk::tuning_or(kk::kI8FusedQuantLimit, 65536)),
+    const size_t fused_limit = std::min<size_t>(static_cast<size_t>(kk::tuning_or(kk::kI8FusedQuantLimit, kFusedQuantDefault)),
                                                 4 * kFusedThreads * kFusedGroups);
     if (count <= fused_limit) {
         hipLaunchKernelGGL(i8_quantize_fused, dim3(1), dim3(kFusedThreads), 0, stream, x, count, k, ws.codes,

@@ -203,7 +203,7 @@ def test_rowwise_i8_bit_exact(gpu, oracle, k, n, batch):
 @pytest.mark.parametrize("k,n,batch", [(1024, 96, 3), (2048, 64, 40), (4096, 32, 20)])
 def test_rowwise_i8_activation_4_byte_aligned(gpu, oracle, k, n, batch):
     # X only float-aligned: the quantizer's 16-byte loads run at 4-byte alignment
-    # (single-workgroup quantizer up to 65536 values, three passes above)
+    # (single-workgroup quantizer up to 16384 values by default, three passes above)
     w = gaussian((n, k), 0.02, k + n)
     x = gaussian((batch, k), 1.0, k + n + 1)
     y, route, guard_ok = run_matmul(kl.WeightType.rowwise_i8, None, x, k, n, batch, w_f32=w, x_offset=4)
@@ -229,6 +229,21 @@ def test_rowwise_i8_fixture_patterns(gpu, oracle, pattern):
     y, _, _ = run_matmul(kl.WeightType.rowwise_i8, None, x, k, n, batch, w_f32=dec)
     expect = oracle.rowwise_i8_matmul(dec, x)
     assert np.array_equal(y.view(np.uint32), expect.view(np.uint32))
+
+
+@pytest.mark.parametrize("limit,k,n,batch", [(None, 1024, 64, 16), (None, 1024, 64, 17), ("65536", 4096, 48, 16),
+                                              ("65536", 2048, 96, 17), ("65536", 16384, 64, 2)])
+def test_rowwise_i8_single_workgroup_quantizer_limit(gpu, oracle, knobs, limit, k, n, batch):
+    # batch*k = 16384 (the default limit) and 17408 either side of it; with the
+    # limit raised to its maximum, the single-workgroup quantizer up to 65536 values
+    if limit is not None:
+        knobs("KUNLUN_I8_FUSED_QUANT_LIMIT", limit)
+    w = gaussian((n, k), 0.02, k + batch)
+    x = gaussian((batch, k), 1.0, k + batch + 1)
+    x[batch - 1, k - 1] = -11.0
+    y, _, guard_ok = run_matmul(kl.WeightType.rowwise_i8, None, x, k, n, batch, w_f32=w)
+    assert guard_ok
+    assert np.array_equal(y.view(np.uint32), oracle.rowwise_i8_matmul(w, x).view(np.uint32))
 
 
 def test_rowwise_i8_large_activation_path(gpu, oracle):
