@@ -660,6 +660,12 @@ hipError_t launch_q4_dot8_slices(const uint8_t *w, const uint8_t *w2, const floa
             return launch_q4_dot8_cfg<1, SLICES, 2, false, 6, 8>(w, w2, x, y, k, n, y_stride, stream, info, 8);
         return launch_q4_dot8_cfg<1, SLICES, 3, false, 6, 8, true>(w, w2, x, y, k, n, y_stride, stream, info, 8);
     }
+    if constexpr (B == 1 && PAIR && SLICES == 1) {
+        // gate/up pair, K <= 4096: 4 waves per CU over strided rows, 2 row
+        // pairs in flight (K4096 x 2 x N11008: 12.0 against 12.7 us with 8
+        // waves per CU and contiguous rows; 12.4 us with 3 in flight)
+        return launch_q4_dot8_cfg<1, 1, 2, true, 6, 4, true>(w, w2, x, y, k, n, y_stride, stream, info, 4);
+    }
     // items in flight per wave: 3 single-column items, 2 when an item is twice
     // the work (two batch columns, or a gate/up row pair) or when a wave owns
     // at most 2 items (then all of them are in flight and a third would be a
