@@ -143,9 +143,13 @@ def cpu_baseline(seconds: float) -> dict | None:
 
     runs = [(1, "port", "oracle orc_gold: FP64 restatement of bench/library-bench.cpp:121-122, 1 thread",
              lambda: orc.gold(dec, x, threads=1))]
+    prepared = None
     if ref is not None:
-        runs.append((6, "reference", "kref_reference: the reference's bench/native-q4-reference.h:98-108 "
-                     "compiled as is (FP64, 6 OpenMP threads)", lambda: ref.reference(dec, x)))
+        # the vectors are built once, and each timed call is reference() alone, as
+        # the reference's bench/native-q4-bench.cpp:22-25 times it
+        prepared = ref.prepared(dec, x)
+        runs.append((6, "reference", "kref_run: the reference's bench/native-q4-reference.h:98-108 "
+                     "compiled as is (FP64, 6 OpenMP threads) on vectors built once", prepared.run))
     else:
         runs.append((6, "port", "oracle orc_gold, 6 threads (oracle/_ref not built)",
                      lambda: orc.gold(dec, x, threads=6)))
@@ -160,6 +164,8 @@ def cpu_baseline(seconds: float) -> dict | None:
                            "ms_per_call": round(per_call * 1e3, 3), "calls": reps,
                            "seconds": round(elapsed, 2)})
         log(f"cpu baseline {threads} thread(s): {per_call * 1e3:.3f} ms/call")
+    if prepared is not None:
+        prepared.close()
     head = by_threads[1]
     return {"value": head["gbps"], "unit": "GB/s", "cores": head["threads"], "kind": head["kind"],
             "sample": f"{head['what']}; K{k}xN{n} batch 1, decoded Q4_0 weights, {head['calls']} calls in "
@@ -190,16 +196,23 @@ def copy_leg(events, stream, device: int, reps: int = 10) -> dict:
     return {"bytes": COPY_BYTES, "reps": reps, "us": round(ms * 1e3, 2)}
 
 
-READ_SIZES = (("gate_gemv", q4_bytes(4096, 11008)), ("lm_head_gemv", q4_bytes(4096, 32000)),
-              ("256mib", 256 << 20))
+# the read leg at the size of every per-shape GEMV (down K11008 x N4096 has the
+# gate's bytes), of the small-batch Q4_0 weights (configs[2], K4096 x N14336
+# at batch 8) and of 256 MiB
+READ_SIZES = (("gate_gemv", q4_bytes(4096, 11008)), ("qkv_gemv", q4_bytes(4096, 12288)),
+              ("lm_head_gemv", q4_bytes(4096, 32000)), ("cfg0_gemv", q4_bytes(4096, 4096)),
+              ("small_batch_q4", q4_bytes(4096, 14336, 8)), ("256mib", 256 << 20))
+READ_OF_SHAPE = {"qkv": "qkv_gemv", "gate": "gate_gemv", "up": "gate_gemv", "down": "gate_gemv",
+                 "lm_head": "lm_head_gemv", "cfg0": "cfg0_gemv"}
 READ_WAVES = (2048, 4096, 8192)          # 8, 16 and 32 waves per CU
 READ_VARIANTS = ((0, "grid_stride"), (1, "all_issued"), (2, "all_issued_nt"))
 
 
-def read_ceiling_leg(events, stream, device: int, reps: int) -> dict:
+def read_ceiling_leg(events, stream, device: int, reps: int, sizes=None, variants=None, waves_list=None) -> dict:
     """Measured HBM read ceiling: kk_stream_read (kunlunk200_lib_amd/csrc/stream_read.hip) reads
     each size once per launch from a buffer slot that rotates over >= ROTATE_BYTES, for every
-    variant and grid size that fits (at most 64 KiB per wave); `best` is the fastest."""
+    variant and grid size that fits (at most 64 KiB per wave); `best` is the fastest. `sizes`,
+    `variants` and `waves_list` restrict the runs (names, variant numbers, wave counts)."""
     lib = ctypes.CDLL(os.path.join(ROOT, "kunlunk200_lib_amd", "lib", "libkunlunk200_stream.so"))
     lib.kk_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int,
                                    ctypes.c_void_p, ctypes.c_void_p]
@@ -207,6 +220,8 @@ def read_ceiling_leg(events, stream, device: int, reps: int) -> dict:
     out_word = kl.Buffer(device, 256)
     out = {}
     for name, size in READ_SIZES:
+        if sizes and name not in sizes:
+            continue
         size = size // 16 * 16
         slot = (size + 255) & ~255
         slots = max(2, -(-ROTATE_BYTES // slot))
@@ -216,6 +231,8 @@ def read_ceiling_leg(events, stream, device: int, reps: int) -> dict:
         for variant, vname in READ_VARIANTS:
             for waves in READ_WAVES:
                 if variant > 0 and -(-size // waves) > 64 * 1024:
+                    continue
+                if (variants and variant not in variants) or (waves_list and waves not in waves_list):
                     continue
 
                 def one(i, variant=variant, waves=waves):
@@ -263,57 +280,75 @@ PAIR_N = 11008
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
 
+def rotating_copies(device: int, first: kl.Buffer, nbytes: int, total: int = ROTATE_BYTES) -> list:
+    """`first` and device copies of it, at least `total` bytes in all (at least 2 buffers), so a
+    loop over them reads its weights from HBM rather than from the 256 MB Infinity Cache."""
+    bufs = [first]
+    for _ in range(max(2, -(-total // nbytes)) - 1):
+        b = kl.Buffer(device, nbytes)
+        with kl.runtime_mutex():
+            kl.select(device)
+            kl.check(kl.copy(b.data, first.data, nbytes, kl.CopyKind.device_to_device))
+            kl.check(kl.wait())
+        bufs.append(b)
+    return bufs
+
+
 def gemm_leg(kernel, events, stream, device: int, reps: int) -> dict:
     """Q4_0 prefill GEMM at batch 512: TFLOP/s = 2*b*k*n / time; the
-    gate/up pair with SiLU * up counts 2 * 2*b*k*n per call."""
+    gate/up pair with SiLU * up counts 2 * 2*b*k*n per call. Weights rotate over >= 640 MB of
+    device copies (the gate/up pair: pairs of copies), so each call reads them from HBM."""
     batch = 512
     out = {}
     rng = np.random.Generator(np.random.PCG64(11))
-    for tag, k, n in GEMM_SHAPES:
-        wbuf = kl.Buffer(device, n * (k // 32) * 18)
-        upload_q4_matrix(wbuf, k, n, seed=2000 + n)
-        xbuf = kl.Buffer(device, 4 * batch * k)
-        xbuf.upload(rng.standard_normal((batch, k), dtype=np.float32))
-        ybuf = kl.Buffer(device, 4 * batch * n)
+
+    def timed_calls(call) -> float:
         with kl.runtime_mutex():
-            for _ in range(3):
-                kl.matmul(kernel, device, ybuf.data, wbuf.data, xbuf.data, k, n, batch, kl.WeightType.q4_0)
+            for i in range(3):
+                call(i)
             kl.select(device)
             kl.check(kl.wait())
             start, stop = events.create(), events.create()
             events.record(start, stream)
-            for _ in range(reps):
-                kl.matmul(kernel, device, ybuf.data, wbuf.data, xbuf.data, k, n, batch, kl.WeightType.q4_0)
+            for i in range(reps):
+                call(i)
             events.record(stop, stream)
             ms = events.elapsed_ms(start, stop) / reps
             kl.check(kl.wait())
+        return ms
+
+    for tag, k, n in GEMM_SHAPES:
+        nbytes = n * (k // 32) * 18
+        first = kl.Buffer(device, nbytes)
+        upload_q4_matrix(first, k, n, seed=2000 + n)
+        wbufs = rotating_copies(device, first, nbytes)
+        xbuf = kl.Buffer(device, 4 * batch * k)
+        xbuf.upload(rng.standard_normal((batch, k), dtype=np.float32))
+        ybuf = kl.Buffer(device, 4 * batch * n)
+        ms = timed_calls(lambda i: kl.matmul(kernel, device, ybuf.data, wbufs[i % len(wbufs)].data, xbuf.data,
+                                             k, n, batch, kl.WeightType.q4_0))
         tflops = 2.0 * batch * k * n / (ms * 1e-3) / 1e12
         out[tag] = {"us": round(ms * 1e3, 2), "tflops": round(tflops, 1),
-                    "mfma_f16_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "route": kernel.route}
+                    "mfma_f16_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "route": kernel.route,
+                    "rotating_copies": len(wbufs)}
         if n == PAIR_N:
             # BASELINE configs[4]: gate/up pair sharing X, then SiLU(gate) * up, one call
-            ubuf = kl.Buffer(device, n * (k // 32) * 18)
-            upload_q4_matrix(ubuf, k, n, seed=3000 + n)
-            with kl.runtime_mutex():
-                for _ in range(3):
-                    kl.matmul_swiglu(kernel, device, ybuf.data, wbuf.data, ubuf.data, xbuf.data, k, n, batch,
-                                     kl.WeightType.q4_0)
-                kl.select(device)
-                kl.check(kl.wait())
-                start, stop = events.create(), events.create()
-                events.record(start, stream)
-                for _ in range(reps):
-                    kl.matmul_swiglu(kernel, device, ybuf.data, wbuf.data, ubuf.data, xbuf.data, k, n, batch,
-                                     kl.WeightType.q4_0)
-                events.record(stop, stream)
-                ms = events.elapsed_ms(start, stop) / reps
-                kl.check(kl.wait())
+            ufirst = kl.Buffer(device, nbytes)
+            upload_q4_matrix(ufirst, k, n, seed=3000 + n)
+            half = ROTATE_BYTES // 2
+            gates = wbufs[:max(2, -(-half // nbytes))]
+            ups = rotating_copies(device, ufirst, nbytes, half)
+            pairs = list(zip(gates, ups))
+            ms = timed_calls(lambda i: kl.matmul_swiglu(kernel, device, ybuf.data, pairs[i % len(pairs)][0].data,
+                                                        pairs[i % len(pairs)][1].data, xbuf.data, k, n, batch,
+                                                        kl.WeightType.q4_0))
             tflops = 4.0 * batch * k * n / (ms * 1e-3) / 1e12
             out[f"pair_swiglu_{tag}"] = {"us": round(ms * 1e3, 2), "tflops": round(tflops, 1),
                                          "mfma_f16_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
-                                         "route": kernel.route}
-            ubuf.close()
-        for b in (wbuf, xbuf, ybuf):
+                                         "route": kernel.route, "rotating_copies": len(pairs)}
+            for b in ups:
+                b.close()
+        for b in wbufs + [xbuf, ybuf]:
             b.close()
     return out
 
@@ -584,6 +619,12 @@ def main() -> int:
     ap.add_argument("--common-reps", type=int, default=50, help="timed common_q4_matmul calls per shape (0: skip)")
     ap.add_argument("--i8-reps", type=int, default=50, help="timed rowwise_i8 matmul calls per case (0: skip)")
     ap.add_argument("--read-reps", type=int, default=200, help="timed launches per read-ceiling run (0: skip)")
+    ap.add_argument("--tune", action="append", default=[], metavar="NAME=V1,V2",
+                    help="profiling aid with --only SHAPE: time the GEMV once per value of this tuning knob "
+                         "(repeatable: every combination)")
+    ap.add_argument("--read-sizes", default="", help="profiling aid: comma list of read-leg size names to run")
+    ap.add_argument("--read-variants", default="", help="profiling aid: comma list of read-leg variants (0, 1, 2)")
+    ap.add_argument("--read-waves", default="", help="profiling aid: comma list of read-leg wave counts")
     ap.add_argument("--only", choices=[name for name, _, _ in SHAPES] + ["gemm", "copy", "small", "native", "common",
                                                                           "i8", "read"],
                     help="profiling aid: time only this GEMV's launch loop, one leg, or (copy) a "
@@ -616,8 +657,12 @@ def main() -> int:
     if args.only == "native":
         print(json.dumps({"native_q4": native_leg(events, stream, device, args.native_reps)}), flush=True)
         return 0
+    read_filter = {"sizes": [v for v in args.read_sizes.split(",") if v] or None,
+                   "variants": [int(v) for v in args.read_variants.split(",") if v] or None,
+                   "waves_list": [int(v) for v in args.read_waves.split(",") if v] or None}
     if args.only == "read":
-        print(json.dumps({"read_ceiling": read_ceiling_leg(events, stream, device, args.read_reps)}), flush=True)
+        print(json.dumps({"read_ceiling": read_ceiling_leg(events, stream, device, args.read_reps, **read_filter)}),
+              flush=True)
         return 0
     if args.only == "copy":
         print(json.dumps({"copy": copy_leg(events, stream, device)}), flush=True)
@@ -682,10 +727,19 @@ def main() -> int:
 
         def only(i):
             kl.matmul(kernel, device, ys[name].data, weights(name, i), xs[name].data, k, n, 1, kl.WeightType.q4_0)
-        ms = timed(only, args.kernel_reps, args.warmup, "only") / args.kernel_reps
-        print(json.dumps({"only": name, "k": k, "n": n, "us_per_launch": round(ms * 1e3, 3),
-                          "host_us_per_call": round(host_us["only"], 3),
-                          "gbps": round(q4_bytes(k, n) / (ms * 1e-3) / 1e9, 1), "route": kernel.route}), flush=True)
+        # --tune NAME=V1,V2 (repeatable): one timed loop per combination of knob values
+        knobs = [(t.split("=", 1)[0], t.split("=", 1)[1].split(",")) for t in args.tune]
+        combos = [[]]
+        for knob, values in knobs:
+            combos = [c + [(knob, v)] for c in combos for v in values]
+        for combo in combos:
+            for knob, value in combo:
+                kl.set_tuning(knob, value)
+            ms = timed(only, args.kernel_reps, args.warmup, "only") / args.kernel_reps
+            print(json.dumps({"only": name, "k": k, "n": n, "tuning": dict(combo), "us_per_launch": round(ms * 1e3, 3),
+                              "host_us_per_call": round(host_us["only"], 3),
+                              "gbps": round(q4_bytes(k, n) / (ms * 1e-3) / 1e9, 1), "route": kernel.route}),
+                  flush=True)
         return 0
 
     dname, dk, dn = DOMINANT
@@ -746,8 +800,22 @@ def main() -> int:
     native = native_leg(events, stream, device, args.native_reps) if args.native_reps > 0 else None
     common = common_leg(events, stream, device, args.common_reps) if args.common_reps > 0 else None
     i8 = i8_leg(kernel, events, stream, device, args.i8_reps) if args.i8_reps > 0 else None
-    read = read_ceiling_leg(events, stream, device, args.read_reps) if args.read_reps > 0 else None
-    read_gbps = read["gate_gemv"]["best"]["gbps"] if read else None
+    read = read_ceiling_leg(events, stream, device, args.read_reps, **read_filter) if args.read_reps > 0 else None
+    read_gbps = read["gate_gemv"]["best"]["gbps"] if read and "gate_gemv" in read else None
+    if read:
+        # each GEMV against the read leg at its own size: read time / GEMV time
+        for name, k, n in SHAPES:
+            leg = read.get(READ_OF_SHAPE[name])
+            if leg:
+                entry = per_shape[f"{name}_k{k}_n{n}"]
+                entry["read_leg_us"] = leg["best"]["us"]
+                entry["frac_of_read_leg"] = round(leg["best"]["us"] / entry["us"], 4)
+        if small:
+            leg = read.get("small_batch_q4")
+            for tag, entry in small.items():
+                if leg and tag.startswith("q4_k4096_n14336_"):
+                    entry["read_leg_us"] = leg["best"]["us"]
+                    entry["frac_of_read_leg"] = round(leg["best"]["us"] / entry["us"], 4)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     result = {
         "metric": METRIC,

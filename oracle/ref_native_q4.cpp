@@ -39,6 +39,28 @@ int kref_reference(const float *w, const float *x, int k, int n, int batch, doub
     return 0;
 }
 
+// The same call split as the reference's own bench times it
+// (reference bench/native-q4-bench.cpp:22-25): the weight and input vectors
+// are built once (kref_prepare), and kref_run times reference() alone on them.
+struct Prepared {
+    std::vector<float> w, x;
+    int k, n, batch;
+};
+
+void *kref_prepare(const float *w, const float *x, int k, int n, int batch) {
+    return new Prepared{std::vector<float>(w, w + (size_t)n * k), std::vector<float>(x, x + (size_t)batch * k), k, n,
+                        batch};
+}
+
+int kref_run(void *handle, double *y) {
+    const Prepared *p = static_cast<const Prepared *>(handle);
+    auto result = reference(p->w, p->x, p->k, p->n, p->batch);
+    if (y) std::memcpy(y, result.data(), result.size() * sizeof(double));
+    return 0;
+}
+
+void kref_release(void *handle) { delete static_cast<Prepared *>(handle); }
+
 // Multi-component per-tensor activation quantization: codes [components][batch*k]
 // and component scales max/limit (reference bench/native-q4-reference.h:70-97).
 int kref_activation(const float *x, int k, int batch, int bits, int components,

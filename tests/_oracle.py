@@ -302,6 +302,12 @@ class ReferenceOracle:
         lib.kref_activation.argtypes = [P, I, I, I, I, P, P]
         for fn in (lib.kref_weights, lib.kref_input, lib.kref_reference, lib.kref_activation):
             fn.restype = I
+        lib.kref_prepare.argtypes = [P, P, I, I, I]
+        lib.kref_prepare.restype = ctypes.c_void_p
+        lib.kref_run.argtypes = [ctypes.c_void_p, P]
+        lib.kref_run.restype = I
+        lib.kref_release.argtypes = [ctypes.c_void_p]
+        lib.kref_release.restype = None
         self.lib = lib
 
     def weights(self, k: int, n: int):
@@ -325,6 +331,11 @@ class ReferenceOracle:
         self.lib.kref_reference(_p(w), _p(x), k, n, batch, _p(y))
         return y
 
+    def prepared(self, w: np.ndarray, x: np.ndarray) -> "PreparedReference":
+        """reference() on vectors built once, timed alone per call as the reference's
+        bench/native-q4-bench.cpp:22-25 times it."""
+        return PreparedReference(self.lib, w, x)
+
     def activation(self, x: np.ndarray, bits: int = 8, components: int = 2):
         x = np.ascontiguousarray(x, dtype=np.float32)
         batch, k = x.shape
@@ -332,3 +343,25 @@ class ReferenceOracle:
         scales = np.empty(components, np.float32)
         self.lib.kref_activation(_p(x), k, batch, bits, components, _p(linear), _p(scales))
         return linear, scales
+
+
+class PreparedReference:
+    """A kref_prepare handle: run() calls the reference's reference() on the stored vectors."""
+
+    def __init__(self, lib, w: np.ndarray, x: np.ndarray):
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        self.lib = lib
+        self.n, self.k = w.shape
+        self.batch = x.shape[0]
+        self.handle = lib.kref_prepare(_p(w), _p(x), self.k, self.n, self.batch)
+        self.y = np.empty((self.batch, self.n), np.float64)
+
+    def run(self) -> np.ndarray:
+        self.lib.kref_run(self.handle, _p(self.y))
+        return self.y
+
+    def close(self) -> None:
+        if self.handle:
+            self.lib.kref_release(self.handle)
+            self.handle = None
