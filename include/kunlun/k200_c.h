@@ -209,7 +209,7 @@ void kunlun_matmul_swiglu(kunlun_kernel *kernel, int device, void *y, const void
  * variable (KUNLUN_GEMM_MIN_BATCH, KUNLUN_Q4_MFMA_MIN, KUNLUN_Q4_MFMA_MAX,
  * KUNLUN_DENSE_MFMA_MIN, KUNLUN_DENSE_MFMA_MAX, KUNLUN_GEMM_TILE (BMxWN),
  * KUNLUN_GEMM_BN, KUNLUN_GEMV_GENERAL, KUNLUN_I8_FUSED_QUANT_LIMIT,
- * KUNLUN_Q4_GEMV_PLANES, KUNLUN_Q4_BDIAG, KUNLUN_DENSE_STREAM,
+ * KUNLUN_Q4_BDIAG, KUNLUN_DENSE_STREAM,
  * KUNLUN_Q4_STREAM_MIN), which
  * the library reads once, at the first matmul. kunlun_set_tuning sets a knob
  * from text in the variable's syntax; a NULL value restores the value read

@@ -45,6 +45,7 @@
 // contribute zero (weight scale 0, zero activations, activation scale 0).
 #include "device_common.h"
 #include "launch.h"
+#include "lds_opt_in.h"
 
 #include <algorithm>
 
@@ -308,21 +309,10 @@ const void *bdiag_kernel_for(int q, const BdPlan &p) {
 }
 
 // Workgroups of `kernel` one CU holds at once with `lds` bytes each (dynamic
-// LDS above 64 KiB opted into once per device and kernel; callers hold the
-// runtime lock). 0 when the query fails.
-int bdiag_per_cu(const void *kernel, size_t lds, int device) {
-    constexpr int kMaxDevices = 64;
-    constexpr int kKernels = 32;
-    static const void *opted[kMaxDevices][kKernels] = {};
-    if (device < 0 || device >= kMaxDevices) return 0;
-    int slot = 0;
-    while (slot < kKernels && opted[device][slot] && opted[device][slot] != kernel) ++slot;
-    if (slot == kKernels) return 0;
-    if (!opted[device][slot]) {
-        if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLdsBytes) != hipSuccess)
-            return 0;
-        opted[device][slot] = kernel;
-    }
+// LDS above 64 KiB opted into once per device and kernel). 0 when the query
+// fails.
+int bdiag_per_cu(const void *kernel, size_t lds) {
+    if (kk::opt_in_lds(kernel, lds) != hipSuccess) return 0;
     int blocks = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, kThreads, lds) != hipSuccess) return 0;
     return blocks;
@@ -355,7 +345,7 @@ extern "C" int kk_q4_bdiag_gemv(const void *w, const float *x, float *y, int k, 
         const BdPlan p = bdiag_candidate(k, batch, t);
         if (p.parts == 0) continue;
         const void *kp = bdiag_kernel_for(q, p);
-        const int per_cu = bdiag_per_cu(kp, p.lds_bytes, device);
+        const int per_cu = bdiag_per_cu(kp, p.lds_bytes);
         if (per_cu == 0) continue;
         plan = p;
         kernel = kp;

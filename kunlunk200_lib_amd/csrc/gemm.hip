@@ -18,6 +18,7 @@
 // product (the fp16-MFMA tolerance of the path is 2e-3 relative).
 #include "device_common.h"
 #include "launch.h"
+#include "lds_opt_in.h"
 #include "tuning.h"
 
 #include <algorithm>
@@ -1014,19 +1015,9 @@ GemmPlan plan(int k, int n, int batch) {
 template <bool F16W, int BN, bool PAIR = false>
 hipError_t launch_gemm(const void *w, const void *w2, const _Float16 *x16, const float *row_inv, float *y, int batch,
                        int n, int k, const GemmPlan &p, size_t w_bytes, hipStream_t stream) {
-    // dynamic LDS above 64 KiB is opted into once per device (callers hold the runtime lock)
-    constexpr int kMaxDevices = 64;
-    static bool configured[kMaxDevices] = {};
-    int device = 0;
-    hipError_t rc = hipGetDevice(&device);
+    const hipError_t rc =
+        kk::opt_in_lds(reinterpret_cast<const void *>(&mfma_gemm<F16W, BN, PAIR>), gemm_lds_bytes<BN>());
     if (rc != hipSuccess) return rc;
-    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
-    if (!configured[device]) {
-        rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&mfma_gemm<F16W, BN, PAIR>),
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(gemm_lds_bytes<BN>()));
-        if (rc != hipSuccess) return rc;
-        configured[device] = true;
-    }
     const int tiles = p.m_tiles * p.n_tiles;
     const int tiles_per_xcd = (tiles + kXcds - 1) / kXcds;
     hipLaunchKernelGGL((mfma_gemm<F16W, BN, PAIR>), dim3(tiles_per_xcd * kXcds), dim3(kGemmThreads),
@@ -1035,18 +1026,10 @@ hipError_t launch_gemm(const void *w, const void *w2, const _Float16 *x16, const
     return hipGetLastError();
 }
 
-constexpr int kMaxDevices = 64;
-
 int device_cus() {
-    static int cus[kMaxDevices] = {};
     int device = 0;
-    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) return 256;
-    if (cus[device] == 0) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || v <= 0) v = 256;
-        cus[device] = v;
-    }
-    return cus[device];
+    if (hipGetDevice(&device) != hipSuccess) return 256;
+    return kk::cu_count(device);
 }
 
 struct QlTile {
@@ -1085,17 +1068,8 @@ template <int BM, int WN, bool PAIR>
 hipError_t launch_ql_gemm(const void *w, const void *w2, const _Float16 *x16, const float *row_inv, float *y, int batch,
                           int n, int k, int k_pad, hipStream_t stream) {
     using S = QlShape<BM, WN, PAIR>;
-    static bool configured[kMaxDevices] = {};     // LDS above 64 KiB: opted into once per device
-    int device = 0;
-    hipError_t rc = hipGetDevice(&device);
+    hipError_t rc = kk::opt_in_lds(reinterpret_cast<const void *>(&q4_lds_gemm<BM, WN, PAIR>), S::LdsBytes);
     if (rc != hipSuccess) return rc;
-    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
-    if (!configured[device]) {
-        rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&q4_lds_gemm<BM, WN, PAIR>),
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, S::LdsBytes);
-        if (rc != hipSuccess) return rc;
-        configured[device] = true;
-    }
     const int out = PAIR ? S::BN / 2 : S::BN;
     const int m_tiles = (batch + BM - 1) / BM;
     const int tiles = m_tiles * ((n + out - 1) / out);

@@ -19,6 +19,7 @@
 //                 row. Correct for every input the API accepts; slow.
 #include "device_common.h"
 #include "launch.h"
+#include "lds_opt_in.h"
 #include "tuning.h"
 
 #include <algorithm>
@@ -699,9 +700,8 @@ hipError_t launch_dense(const uint8_t *w, const float *x, float *y, int k, int n
     const size_t lds = static_cast<size_t>(B) * k * 4;
     const int rowblocks = (n + U - 1) / U;
     const int groups = groups_for(rowblocks, info.cus, 8);
-    hipError_t rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&dense_gemv<B, U, F16>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    (void)rc;
+    const hipError_t rc = kk::opt_in_lds(reinterpret_cast<const void *>(&dense_gemv<B, U, F16>), lds);
+    if (rc != hipSuccess) return rc;
     hipLaunchKernelGGL((dense_gemv<B, U, F16>), dim3(groups), dim3(kThreads), lds, stream, w, x, y, k, n, y_stride);
     return hipGetLastError();
 }
@@ -717,20 +717,10 @@ hipError_t launch_dense_stream_passes(const uint8_t *w, const float *x, float *y
     const int groups = static_cast<int>((waves + WAVES - 1) / WAVES);
     const size_t lds = static_cast<size_t>(k) * 4 + static_cast<size_t>(WAVES) * kDot8MaxRowsPerWave * 4;
     auto kernel = &dense_stream<F16, WAVES, DEPTH, XPASSES>;
-    if (lds > 64 * 1024) {
-        constexpr int kMaxDevices = 64;
-        static bool opted[kMaxDevices] = {};
-        int device = 0;
-        hipError_t rc = hipGetDevice(&device);
-        if (rc != hipSuccess) return rc;
-        if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
-        if (!opted[device]) {
-            rc = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     static_cast<int>(lds));
-            if (rc != hipSuccess) return rc;
-            opted[device] = true;
-        }
-    }
+    // opted into the whole LDS once per device and kernel, so a later call
+    // with a larger K on the same instance stays inside the grant
+    const hipError_t rc = kk::opt_in_lds(reinterpret_cast<const void *>(kernel), lds);
+    if (rc != hipSuccess) return rc;
     hipLaunchKernelGGL(kernel, dim3(groups), dim3(64 * WAVES), lds, stream, w, x, y, k, n);
     return hipGetLastError();
 }
@@ -779,11 +769,6 @@ extern "C" int kk_dense_matmul(int type, const void *w, const float *x, float *y
         const int groups = groups_for(n, info.cus, 16);
         hipLaunchKernelGGL(gemv_general, dim3(groups), dim3(kThreads), 0, stream, wb, type, x, y, k, n, batch);
         return hipGetLastError();
-    }
-    if (type == 2 && batch == 1 && kk::tuning_or(kk::kQ4GemvPlanes, 0) != 0 &&
-        kk_q4_gemv_planes_supported(w, x, k, n)) {
-        if (route) *route = "q4_gemv_planes";
-        return kk_q4_gemv_planes(w, x, y, k, n, info.cus, stream);
     }
     if (type == 2) {
         if (route) *route = "q4_gemv_dot8";
@@ -839,9 +824,6 @@ extern "C" int kk_q4_gemv_pair_swiglu(const void *w_gate, const void *w_up, cons
                                      int batch, hipStream_t stream) {
     if (!y || !kk_q4_gemv_pair_swiglu_supported(w_gate, w_up, x, k, n, batch)) return hipErrorInvalidValue;
     const DeviceInfo info = device_info();
-    if (batch == 1 && kk::tuning_or(kk::kQ4GemvPlanes, 0) != 0 && kk_q4_gemv_planes_supported(w_gate, x, k, n) &&
-        kk_q4_gemv_planes_supported(w_up, x, k, n))
-        return kk_q4_gemv_planes_pair_swiglu(w_gate, w_up, x, y, k, n, info.cus, stream);
     const uint8_t *wg = static_cast<const uint8_t *>(w_gate);
     const uint8_t *wu = static_cast<const uint8_t *>(w_up);
     const int pair_batch = k <= 8192 ? 2 : 1;   // staged digits: B * K <= 16384

@@ -16,6 +16,7 @@
 //   final    [4] f32           max0, max1
 #include "device_common.h"
 #include "launch.h"
+#include "lds_opt_in.h"
 #include "tuning.h"
 
 #include <algorithm>
@@ -935,18 +936,8 @@ extern "C" int kk_i8_matmul(const void *workspace, const int8_t *w, const float 
     if (route) *route = "i8_mfma_gemm";
     if (k % kIgK == 0 && static_cast<long long>(2 * batch) * k <= 0x7fffffffLL &&
         static_cast<long long>(n) * k <= 0x7fffffffLL) {
-        constexpr int kMaxDevices = 64;
-        static bool configured[kMaxDevices] = {};
-        int device = 0;
-        hipError_t rc = hipGetDevice(&device);
+        const hipError_t rc = kk::opt_in_lds(reinterpret_cast<const void *>(&i8_lds_gemm), kIgLdsBytes);
         if (rc != hipSuccess) return rc;
-        if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
-        if (!configured[device]) {
-            rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&i8_lds_gemm),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, kIgLdsBytes);
-            if (rc != hipSuccess) return rc;
-            configured[device] = true;
-        }
         const int m_tiles = (2 * batch + kIgRows - 1) / kIgRows;
         const int tiles = m_tiles * ((n + kIgRows - 1) / kIgRows);
         const int tiles_per_xcd = (tiles + 7) / 8;

@@ -15,14 +15,6 @@ extern "C" {
 int kk_dense_matmul(int type, const void *w, const float *x, float *y, int k, int n, int batch,
                     hipStream_t stream, const char **route);
 
-// Batch-1 Q4_0 GEMV on int8 MFMA over activation digit planes: K % 128 == 0,
-// K <= 16384, 4-byte aligned weights, 16-byte aligned X; `cus` sizes the grid.
-int kk_q4_gemv_planes_supported(const void *w, const float *x, int k, int n);
-int kk_q4_gemv_planes(const void *w, const float *x, float *y, int k, int n, int cus, hipStream_t stream);
-// The same for a gate/up pair: y = SiLU(X w_gate^T) * (X w_up^T), each sum bit
-// for bit the single-matrix kernel's.
-int kk_q4_gemv_planes_pair_swiglu(const void *w_gate, const void *w_up, const float *x, float *y, int k, int n,
-                                  int cus, hipStream_t stream);
 
 // Prefill GEMM on fp16 MFMA for Q4_0 (type 2) and F16 (type 1) weights. The
 // workspace (kk_gemm_workspace_bytes) holds the fp16 activations and their

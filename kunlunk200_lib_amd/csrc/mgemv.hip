@@ -26,6 +26,7 @@
 // scale.
 #include "device_common.h"
 #include "launch.h"
+#include "lds_opt_in.h"
 #include "tuning.h"
 
 #include <algorithm>
@@ -522,20 +523,13 @@ __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restr
 }
 
 // Launch q4_lds_gemv<SB> (dynamic LDS above 64 KiB opted into once per
-// device; callers hold the runtime lock).
+// device).
 template <int SB, bool PACKED>
 hipError_t launch_lds_gemv(const uint8_t *w, const _Float16 *frag, const float *row_inv, float *y, int k, int n,
-                           int batch, int device, hipStream_t stream) {
+                           int batch, hipStream_t stream) {
     using L = LgShape<SB, PACKED>;
-    constexpr int kMaxDevices = 64;
-    static bool configured[kMaxDevices] = {};
-    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
-    if (!configured[device]) {
-        const hipError_t rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&q4_lds_gemv<SB, PACKED>),
-                                                  hipFuncAttributeMaxDynamicSharedMemorySize, L::LdsBytes);
-        if (rc != hipSuccess) return rc;
-        configured[device] = true;
-    }
+    const hipError_t rc = kk::opt_in_lds(reinterpret_cast<const void *>(&q4_lds_gemv<SB, PACKED>), L::LdsBytes);
+    if (rc != hipSuccess) return rc;
     const int tiles = (n + kLgRows - 1) / kLgRows;
     const int tiles_per_xcd = (tiles + 7) / 8;
     hipLaunchKernelGGL((q4_lds_gemv<SB, PACKED>), dim3(tiles_per_xcd * 8), dim3(kLgThreads), L::LdsBytes, stream, w, frag,
@@ -572,26 +566,15 @@ extern "C" int kk_q4_mfma_gemv(const void *w, const float *x, float *y, int k, i
                            blocks_pad, frag, row_inv);
     hipError_t rc = hipGetLastError();
     if (rc != hipSuccess) return rc;
-    // dynamic LDS above 64 KiB is opted into once per device (callers hold the runtime lock)
-    constexpr int kMaxDevices = 64;
-    static bool configured[kMaxDevices] = {};
-    int device = 0;
-    rc = hipGetDevice(&device);
+    rc = kk::opt_in_lds(reinterpret_cast<const void *>(&q4_mfma_gemv), kLdsBytes);
     if (rc != hipSuccess) return rc;
-    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
-    if (!configured[device]) {
-        rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&q4_mfma_gemv),
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-        if (rc != hipSuccess) return rc;
-        configured[device] = true;
-    }
     if (streamed) {
         const uint8_t *wb = static_cast<const uint8_t *>(w);
         if (k % 512 == 0)
-            return packed ? launch_lds_gemv<16, true>(wb, frag, row_inv, y, k, n, batch, device, stream)
-                          : launch_lds_gemv<16, false>(wb, frag, row_inv, y, k, n, batch, device, stream);
-        return packed ? launch_lds_gemv<8, true>(wb, frag, row_inv, y, k, n, batch, device, stream)
-                      : launch_lds_gemv<8, false>(wb, frag, row_inv, y, k, n, batch, device, stream);
+            return packed ? launch_lds_gemv<16, true>(wb, frag, row_inv, y, k, n, batch, stream)
+                          : launch_lds_gemv<16, false>(wb, frag, row_inv, y, k, n, batch, stream);
+        return packed ? launch_lds_gemv<8, true>(wb, frag, row_inv, y, k, n, batch, stream)
+                      : launch_lds_gemv<8, false>(wb, frag, row_inv, y, k, n, batch, stream);
     }
     const int tiles = (n + kTileRows - 1) / kTileRows;
     const int groups = std::max(1, std::min((tiles + kWaves - 1) / kWaves, cus));
@@ -947,25 +930,14 @@ extern "C" int kk_dense_mfma_gemv(int type, const void *w, const float *x, float
         batch > 16 || (reinterpret_cast<uintptr_t>(w) & 15) || (reinterpret_cast<uintptr_t>(x) & 15))
         return hipErrorInvalidValue;
     if (type == 1 && batch <= 8 && k <= 4096 && kk::tuning_or(kk::kDenseStream, 1) != 0) {
-        constexpr int kMaxDevices = 64;
-        static bool opted[kMaxDevices] = {};
-        static int cus_of[kMaxDevices] = {};
         int device = 0;
         hipError_t rc = hipGetDevice(&device);
         if (rc != hipSuccess) return rc;
-        if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
-        if (!opted[device]) {
-            rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&f16_stream_gemv),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, kF16sLdsBytes);
-            if (rc != hipSuccess) return rc;
-            int cus = 256;
-            if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
-                cus = 256;
-            cus_of[device] = cus;
-            opted[device] = true;
-        }
+        rc = kk::opt_in_lds(reinterpret_cast<const void *>(&f16_stream_gemv), kF16sLdsBytes);
+        if (rc != hipSuccess) return rc;
+        const int cus = kk::cu_count(device);
         const int tiles = (n + 15) / 16;
-        const int t = std::max(1, std::min(kF16sMaxTiles, (tiles + cus_of[device] - 1) / cus_of[device]));
+        const int t = std::max(1, std::min(kF16sMaxTiles, (tiles + cus - 1) / cus));
         hipLaunchKernelGGL(f16_stream_gemv, dim3((tiles + t - 1) / t), dim3(kWave * kF16sWaves), kF16sLdsBytes, stream,
                            static_cast<const uint8_t *>(w), x, y, k, n, batch, t);
         return hipGetLastError();

@@ -38,6 +38,7 @@
 // moves: banks 0-1 are the hi rows, banks 2-3 the lo rows).
 #include "device_common.h"
 #include "launch.h"
+#include "lds_opt_in.h"
 
 #include <algorithm>
 
@@ -286,18 +287,8 @@ extern "C" int kk_q4_stream_gemv_supported(const void *w, const float *x, int k,
 extern "C" int kk_q4_stream_gemv(const void *w, const float *x, float *y, int k, int n, int batch, int cus,
                                  hipStream_t stream) {
     if (!kk_q4_stream_gemv_supported(w, x, k, n, batch) || !y || cus <= 0) return hipErrorInvalidValue;
-    constexpr int kMaxDevices = 64;
-    static bool opted[kMaxDevices] = {};   // dynamic LDS above 64 KiB, once per device (callers hold the runtime lock)
-    int device = 0;
-    hipError_t rc = hipGetDevice(&device);
+    const hipError_t rc = kk::opt_in_lds(reinterpret_cast<const void *>(&q4_stream_gemv), kLdsBytes);
     if (rc != hipSuccess) return rc;
-    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
-    if (!opted[device]) {
-        rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&q4_stream_gemv),
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-        if (rc != hipSuccess) return rc;
-        opted[device] = true;
-    }
     const int tiles = (n + kTileRows - 1) / kTileRows;
     const int t = std::max(1, std::min(kMaxTiles, (tiles + cus - 1) / cus));
     hipLaunchKernelGGL(q4_stream_gemv, dim3((tiles + t - 1) / t), dim3(kWave * kWaves), kLdsBytes, stream,

@@ -24,7 +24,6 @@ constexpr KnobName kNames[] = {
     {kGemmBn, "KUNLUN_GEMM_BN"},
     {kGemvGeneral, "KUNLUN_GEMV_GENERAL"},
     {kI8FusedQuantLimit, "KUNLUN_I8_FUSED_QUANT_LIMIT"},
-    {kQ4GemvPlanes, "KUNLUN_Q4_GEMV_PLANES"},
     {kQ4Bdiag, "KUNLUN_Q4_BDIAG"},
     {kDenseStream, "KUNLUN_DENSE_STREAM"},
     {kQ4StreamMin, "KUNLUN_Q4_STREAM_MIN"},

@@ -16,7 +16,6 @@ enum Knob {
     kGemmBn,              // KUNLUN_GEMM_BN=64|128: register-staged GEMM tile width
     kGemvGeneral,         // KUNLUN_GEMV_GENERAL=1: every GEMV on the general kernel
     kI8FusedQuantLimit,   // KUNLUN_I8_FUSED_QUANT_LIMIT: single-workgroup quantizer limit
-    kQ4GemvPlanes,        // KUNLUN_Q4_GEMV_PLANES=1: batch-1 Q4_0 GEMV on the LDS-staged digit-plane kernel
     kQ4Bdiag,             // KUNLUN_Q4_BDIAG=0: the Q4_0 MFMA GEMV batch range on the LDS-staged kernels instead
     kDenseStream,         // KUNLUN_DENSE_STREAM=0: F16 batch 2..8 at K <= 4096 on the K-split kernel, not the streamed one
     kQ4StreamMin,         // KUNLUN_Q4_STREAM_MIN: smallest batch (default 5, up to 8) on the streamed Q4_0 GEMV at K = 4096

@@ -18,8 +18,8 @@ kernels/q4-device.h:3-12).
   one 512-value chunk keep the north-star bound.
 * Q4_0: rows whose block scales are F16 subnormals (all blocks, or every other
   block beside normal scales), with random nibbles and Gaussian activations,
-  on every Q4_0 route: q4_gemv_dot8 (batch 1 and 2), q4_gemv_planes (batch 1
-  under KUNLUN_Q4_GEMV_PLANES=1), the streamed q4_stream_gemv (K = 4096,
+  on every Q4_0 route: q4_gemv_dot8 (batch 1 and 2), the streamed
+  q4_stream_gemv (K = 4096,
   batch 5..8), the block-diagonal q4_bdiag_gemv, the
   streamed and the register-staged q4_mfma_gemv (under KUNLUN_Q4_BDIAG=0),
   the LDS GEMM and the register-staged GEMM, native_q4_matmul and common_q4_matmul (M = 1 and M > 1). Each route meets
@@ -189,7 +189,6 @@ def gemm_bound_ok(y, gold, dec, x, tol):
 # (k, batch, w_offset, route, tolerance): the route a default matmul takes
 Q4_ROUTES = [
     (4096, 1, 0, "q4_gemv_dot8", 1e-4),
-    (4096, 1, 0, "q4_gemv_planes", 1e-4),      # opt-in batch-1 route (KUNLUN_Q4_GEMV_PLANES=1)
     (1088, 1, 0, "q4_gemv_dot8", 1e-4),        # K % 128 != 0
     (4096, 2, 0, "q4_gemv_dot8", 1e-4),
     (4096, 8, 0, "q4_stream_gemv", 1e-4),      # streamed MFMA GEMV (K = 4096, batch 5..8)
@@ -208,8 +207,6 @@ Q4_ROUTES = [
 @pytest.mark.parametrize("k,batch,w_offset,route,tol", Q4_ROUTES,
                          ids=[f"{r}-k{k}-b{b}-o{o}" for k, b, o, r, _ in Q4_ROUTES])
 def test_q4_subnormal_scales(gpu, oracle, knobs, k, batch, w_offset, route, tol, scales):
-    if route == "q4_gemv_planes":
-        knobs("KUNLUN_Q4_GEMV_PLANES", "1")
     if route == "q4_mfma_gemv":
         knobs("KUNLUN_Q4_BDIAG", "0")
     if route != "q4_stream_gemv":

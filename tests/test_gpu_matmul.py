@@ -130,7 +130,7 @@ def test_q4_misaligned_weights_use_general_kernel(gpu, oracle):
     _, route = _dense_case(oracle, kl.WeightType.q4_0, w, x, k, n, batch, w_offset=2)
     assert route == "gemv_general"
     _, route = _dense_case(oracle, kl.WeightType.q4_0, w, x, k, n, batch, w_offset=0)
-    assert route in ("q4_gemv_planes", "q4_gemv_dot8", "q4_bdiag_gemv", "q4_mfma_gemv")
+    assert route in ("q4_gemv_dot8", "q4_bdiag_gemv", "q4_mfma_gemv")
 
 
 def test_unaligned_activation_uses_general_kernel(gpu, oracle):
@@ -293,17 +293,6 @@ def test_q4_baseline_configs_default_route(gpu, oracle, k, n, batch, route):
     x = gaussian((batch, k), 1.0, seed + 1)
     _, got = _dense_case(oracle, kl.WeightType.q4_0, w, x, k, n, batch)
     assert got == route
-
-
-@pytest.mark.parametrize("k,n", [(4096, 4096), (4096, 32000), (11008, 4096), (12288, 96), (256, 16)])
-def test_q4_planes_opt_in(gpu, oracle, knobs, k, n):
-    # the LDS-staged digit-plane batch-1 GEMV, taken under KUNLUN_Q4_GEMV_PLANES=1
-    knobs("KUNLUN_Q4_GEMV_PLANES", "1")
-    seed = 7 * k + n
-    w = gaussian((n, k), 0.02, seed)
-    x = gaussian((1, k), 1.0, seed + 1)
-    _, got = _dense_case(oracle, kl.WeightType.q4_0, w, x, k, n, 1)
-    assert got == "q4_gemv_planes"
 
 
 def two_fc_rowwise_i8(oracle, w, x):

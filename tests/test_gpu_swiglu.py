@@ -308,14 +308,11 @@ DECODE_PAIR_CASES = [(4096, 11008, 1, False), (4096, 300, 2, False), (12352, 70,
                      (256, 65, 1, False), (64, 1, 2, False), (1024, 129, 1, True)]
 
 
-@pytest.mark.parametrize("planes", [False, True], ids=["default", "planes"])
 @pytest.mark.parametrize("k,n,batch,inf", DECODE_PAIR_CASES)
-def test_matmul_swiglu_decode_pair_fused(gpu, oracle, knobs, k, n, batch, inf, planes):
+def test_matmul_swiglu_decode_pair_fused(gpu, oracle, knobs, k, n, batch, inf):
     # batch 1..2 Q4_0: gate and up rows in one GEMV pass with SwiGLU as the
     # epilogue. The gate and up sums are the standalone GEMV's own, so the
     # result equals two matmul calls plus swiglu on the device bit for bit.
-    if planes:
-        knobs("KUNLUN_Q4_GEMV_PLANES", "1")
     seed = 5 * k + n + batch
     wg = gaussian((n, k), 0.02, seed)
     wu = gaussian((n, k), 0.02, seed + 1)
@@ -329,9 +326,7 @@ def test_matmul_swiglu_decode_pair_fused(gpu, oracle, knobs, k, n, batch, inf, p
     from gpu_util import run_matmul
     g, r1, _ = run_matmul(kl.WeightType.q4_0, pg, x, k, n, batch)
     u, r2, _ = run_matmul(kl.WeightType.q4_0, pu, x, k, n, batch)
-    # the dot8 GEMV, or under KUNLUN_Q4_GEMV_PLANES=1 at batch 1 and K % 256 == 0
-    # the digit-plane GEMV (the fused pair then takes the same kernel)
-    assert r1 == r2 == ("q4_gemv_planes" if planes and batch == 1 and k % 256 == 0 else "q4_gemv_dot8")
+    assert r1 == r2 == "q4_gemv_dot8"
     expected = device_swiglu(g, u)
     print(f"  decode pair k={k} n={n} b={batch} inf={inf}", flush=True)
     assert np.array_equal(fused.view(np.uint32), expected.view(np.uint32))
