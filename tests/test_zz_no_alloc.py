@@ -83,3 +83,80 @@ def test_noalloc_rejects_beyond_scratch(gpu):
             assert kl.matmul_noalloc(0, yb.data, wb.data, xb.data, k, n, 1, kl.WeightType.rowwise_i8)[0] == \
                 kl.NOALLOC_INVALID
             assert kl.matmul_noalloc(0, yb.data, wb.data, xb.data, k + 16, n, 1, Q4)[0] == kl.NOALLOC_INVALID
+
+
+# Two host threads whose first no-alloc calls overlap, each on its own HIP
+# stream, in a fresh process (so the per-device set-up and every launcher's
+# one-time LDS opt-in happen under the race), on the routes that use no
+# scratch (calls overlapping on one GPU may share only those). Each thread's
+# results must equal the same calls made one at a time.
+_TWO_THREADS = r"""
+import ctypes, sys, threading
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+import kunlunk200_lib_amd as kl
+hip = ctypes.CDLL("libamdhip64.so")
+hip.hipStreamCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+hip.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
+hip.hipStreamDestroy.argtypes = [ctypes.c_void_p]
+Q4, F32 = kl.WeightType.q4_0, kl.WeightType.f32
+# scratch-free routes: batch-1 dot8, block-diagonal, F32 MFMA, streamed Q4_0, F32 MFMA (small)
+CASES = [(Q4, 4096, 3000, 1), (Q4, 1024, 2048, 4), (F32, 1024, 256, 8), (Q4, 4096, 1000, 8), (F32, 512, 65, 2)]
+rng = np.random.default_rng(7)
+jobs = []
+for type_, k, n, batch in CASES:
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    payload = kl.quantize_q4_0(w) if type_ == Q4 else w
+    x = rng.standard_normal((batch, k)).astype(np.float32)
+    wb, xb = kl.Buffer(0, payload.nbytes), kl.Buffer(0, x.nbytes)
+    wb.upload(payload)
+    xb.upload(x)
+    jobs.append((type_, k, n, batch, wb, xb))
+outs = [[kl.Buffer(0, batch * n * 4) for (_, k, n, batch, _, _) in jobs] for _ in range(3)]
+kl.select(0)
+streams = []
+for _ in range(2):
+    s = ctypes.c_void_p()
+    assert hip.hipStreamCreate(ctypes.byref(s)) == 0
+    streams.append(s)
+status = [[None] * len(jobs) for _ in range(3)]
+start = threading.Barrier(2)
+
+def worker(t):
+    kl.select(0)
+    order = range(len(jobs)) if t == 0 else reversed(range(len(jobs)))
+    start.wait()
+    for i in order:
+        type_, k, n, batch, wb, xb = jobs[i]
+        status[t][i] = kl.matmul_noalloc(0, outs[t][i].data, wb.data, xb.data, k, n, batch, type_, streams[t].value)
+    assert hip.hipStreamSynchronize(streams[t]) == 0
+
+threads = [threading.Thread(target=worker, args=(t,)) for t in range(2)]
+for t in threads:
+    t.start()
+for t in threads:
+    t.join()
+# the same calls one at a time on the library's stream
+for i, (type_, k, n, batch, wb, xb) in enumerate(jobs):
+    status[2][i] = kl.matmul_noalloc(0, outs[2][i].data, wb.data, xb.data, k, n, batch, type_, kl.stream(0))
+    kl.check(kl.wait())
+    ys = [outs[t][i].download(batch * n, np.float32) for t in range(3)]
+    assert status[0][i] == status[1][i] == status[2][i] and status[2][i][0] == 0, [status[t][i] for t in range(3)]
+    for t in range(2):
+        assert np.array_equal(ys[t].view(np.uint32), ys[2].view(np.uint32)), (status[2][i], "thread", t)
+    print("two-thread noalloc", status[2][i][1], k, n, batch, "equal", flush=True)
+for s in streams:
+    hip.hipStreamDestroy(s)
+print("TWO_THREADS_OK", flush=True)
+"""
+
+
+def test_noalloc_two_threads_first_calls(gpu):
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    proc = subprocess.run([sys.executable, "-c", _TWO_THREADS, root], capture_output=True, text=True, timeout=100)
+    print(proc.stdout, flush=True)
+    assert proc.returncode == 0, proc.stdout[-2000:] + proc.stderr[-3000:]
+    assert "TWO_THREADS_OK" in proc.stdout
