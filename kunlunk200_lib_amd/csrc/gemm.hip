@@ -635,12 +635,15 @@ struct QlShape {
     static constexpr int BN = 4 * WN;                                   // weight rows per tile
     static constexpr int RG = BM / 16, CG = WN / 16;                    // MFMA tiles per wave
     static constexpr int ABytes = BM * kQlK * 2;                        // one stage of activations
-    static constexpr int BBytes = BN * kQlRowPair;                      // one stage pair of weights
     static constexpr int ACopiesPerWave = BM * 16 / 64 / 8;             // 1 KB each, per stage
-    static constexpr int BCopies = BN * (kQlRowPair / 16) / 64;         // 1 KB each, per stage pair
-    static_assert(BCopies * 64 == BN * (kQlRowPair / 16), "whole weight copies");
-    static constexpr int HalfCopies = BCopies / 2;                      // PAIR: gate rows, then up rows
-    static_assert(!PAIR || HalfCopies * 64 == BN / 2 * (kQlRowPair / 16), "pair halves in whole copies");
+    // weights: 1 KB copies per stage pair; PAIR: the gate rows' copies, then
+    // the up rows' from HalfCopies on (each half padded to whole copies; the
+    // up rows start at UpBase in the stage-pair buffer)
+    static constexpr int HalfCopies = (BN / 2 * (kQlRowPair / 16) + 63) / 64;
+    static constexpr int BCopies = PAIR ? 2 * HalfCopies : BN * (kQlRowPair / 16) / 64;
+    static_assert(PAIR || BCopies * 64 == BN * (kQlRowPair / 16), "whole weight copies");
+    static constexpr int UpBase = PAIR ? HalfCopies * 1024 : BN / 2 * kQlRowPair;
+    static constexpr int BBytes = PAIR ? BCopies * 1024 : BN * kQlRowPair;   // one stage pair of weights
     static constexpr int BCopiesPerWave = (BCopies + 7) / 8;            // waves below BCopies % 8 (if
     static constexpr int BCopiesRem = BCopies % 8;                      // not 0) issue one more
     static constexpr int TileStride = BN + 4;                           // floats per LDS output row
@@ -690,8 +693,9 @@ __device__ __forceinline__ void ql_copy_b(const uint32_t (&b_off)[S::BCopiesPerW
 }
 
 // PAIR: the stage's weight rows are the tile's BN/2 gate rows (matrix w), then
-// its BN/2 up rows (matrix w2); a wave's first CG/2 column tiles are gate and
-// its last CG/2 are up for the same output columns.
+// its BN/2 up rows (matrix w2, from S::UpBase); waves 0-1 (tile columns
+// 0 .. BN/2) take the gate rows and waves 2-3 the up rows of the same output
+// columns, which the epilogue pairs in LDS.
 template <int BM, int WN, bool PAIR>
 __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restrict__ w, const uint8_t *__restrict__ w2,
                                                          const _Float16 *__restrict__ x16,
@@ -699,7 +703,6 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
                                                          int m_rows, int n_rows, int k_pad, int stages,
                                                          uint32_t row_bytes, int m_tiles, int tiles, int tiles_per_xcd) {
     using S = QlShape<BM, WN, PAIR>;
-    static_assert(!PAIR || S::CG % 2 == 0, "pair tiles hold gate and up column tiles");
     constexpr int kOut = PAIR ? S::BN / 2 : S::BN;             // output columns per tile
     extern __shared__ __align__(16) uint8_t ql_lds[];
 
@@ -744,7 +747,7 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
 #pragma unroll
     for (int t = 0; t < S::BCopiesPerWave; ++t) {
         const int i = wid + 8 * t;
-        const int q = (PAIR && i >= S::HalfCopies ? i - S::HalfCopies : i) * 64 + lane;
+        const int q = (PAIR && i >= S::HalfCopies ? i - S::HalfCopies : i) * 64 + lane;   // past the rows: clamped
         const int row = min(q / (kQlRowPair / 16), kRows - 1);
         const int chunk = q - (q / (kQlRowPair / 16)) * (kQlRowPair / 16);
         const int wrow = min(n0 + row, n_rows - 1) - n0;
@@ -769,9 +772,9 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
     auto read_b = [&](const uint8_t *b_lds, int j, uint32_t (&nib)[S::CG], uint32_t (&sbits)[S::CG]) {
 #pragma unroll
         for (int cg = 0; cg < S::CG; ++cg) {
-            const int brow = !PAIR ? wn * WN + cg * 16
-                                   : (cg < S::CG / 2 ? 0 : S::BN / 2) + wn * (WN / 2) + (cg % (S::CG / 2)) * 16;
-            const uint8_t *blk = b_lds + (brow + c16) * kQlRowPair + 18 * j;
+            const uint8_t *blk = !PAIR ? b_lds + (wn * WN + cg * 16 + c16) * kQlRowPair + 18 * j
+                                       : b_lds + (wn >= 2 ? S::UpBase : 0) +
+                                             ((wn & 1) * WN + cg * 16 + c16) * kQlRowPair + 18 * j;
             sbits[cg] = *reinterpret_cast<const uint16_t *>(blk);
             if ((j & 1) == 0) {   // even block: starts on a dword, nibble dword g at +2 + 4g
                 const uint32_t *p = reinterpret_cast<const uint32_t *>(blk + 4 * g);
@@ -916,7 +919,7 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
         for (int item = threadIdx.x; item < S::BN * (BM / 8); item += kQlThreads) {
             const int j = item % S::BN, p8 = item / S::BN;
             const int h = PAIR ? j / (S::BN / 2) : 0, jr = PAIR ? j % (S::BN / 2) : j;   // matrix, row in it
-            const int col = PAIR ? (jr / (WN / 2)) * WN + h * (WN / 2) + jr % (WN / 2) : j;   // tile column
+            const int col = j;   // tile column (PAIR: gate rows 0 .. BN/2, up rows BN/2 .. BN)
             if (n0 + jr >= n_rows) continue;
             const uint8_t *wrow = (h ? w2 : w) + static_cast<size_t>(n0 + jr) * row_bytes;
             const uint32_t *mask = tiny_masks + j * kTinyMaskWords;
@@ -931,46 +934,36 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
         }
         __syncthreads();
     }
+    if (kh == 0) {
+#pragma unroll
+        for (int rg = 0; rg < S::RG; ++rg)
+#pragma unroll
+            for (int cg = 0; cg < S::CG; ++cg)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = rg * 16 + 4 * g + r;
+                    float *t = tile_lds + row * kTs + wn * WN + cg * 16 + c16;
+                    *t = (acc[rg][cg][r] + *t) * scale_lds[row];
+                }
+    }
     if constexpr (PAIR) {
-        // SiLU(gate) * up into acc's gate slots, then (after every read of the
-        // tile) into output columns 0 .. BN/2
-        constexpr int kHalf = S::CG / 2;
-        if (kh == 0) {
+        // SiLU(gate) * up into output columns 0 .. BN/2 (after every read of the tile)
+        __syncthreads();
+        constexpr int kHalf = S::BN / 2;
+        float pv[(BM * kHalf + kQlThreads - 1) / kQlThreads];
 #pragma unroll
-            for (int rg = 0; rg < S::RG; ++rg)
-#pragma unroll
-                for (int cg = 0; cg < kHalf; ++cg)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int row = rg * 16 + 4 * g + r;
-                        const float s = scale_lds[row];
-                        const float gs = (acc[rg][cg][r] + tile_lds[row * kTs + wn * WN + cg * 16 + c16]) * s;
-                        const float us = (acc[rg][cg + kHalf][r] + tile_lds[row * kTs + wn * WN + (cg + kHalf) * 16 + c16]) * s;
-                        acc[rg][cg][r] = kk::swiglu_value(gs, us);
-                    }
+        for (int t = 0; t * kQlThreads < BM * kHalf; ++t) {
+            const int i = t * kQlThreads + static_cast<int>(threadIdx.x);
+            if (i < BM * kHalf) {
+                const int row = i / kHalf, c = i - row * kHalf;
+                pv[t] = kk::swiglu_value(tile_lds[row * kTs + c], tile_lds[row * kTs + kHalf + c]);
+            }
         }
         __syncthreads();
-        if (kh == 0) {
 #pragma unroll
-            for (int rg = 0; rg < S::RG; ++rg)
-#pragma unroll
-                for (int cg = 0; cg < kHalf; ++cg)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        tile_lds[(rg * 16 + 4 * g + r) * kTs + wn * (WN / 2) + cg * 16 + c16] = acc[rg][cg][r];
-        }
-    } else {
-        if (kh == 0) {
-#pragma unroll
-            for (int rg = 0; rg < S::RG; ++rg)
-#pragma unroll
-                for (int cg = 0; cg < S::CG; ++cg)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int row = rg * 16 + 4 * g + r;
-                        float *t = tile_lds + row * kTs + wn * WN + cg * 16 + c16;
-                        *t = (acc[rg][cg][r] + *t) * scale_lds[row];
-                    }
+        for (int t = 0; t * kQlThreads < BM * kHalf; ++t) {
+            const int i = t * kQlThreads + static_cast<int>(threadIdx.x);
+            if (i < BM * kHalf) tile_lds[(i / kHalf) * kTs + i % kHalf] = pv[t];
         }
     }
     __syncthreads();
@@ -1042,7 +1035,7 @@ struct QlTile {
 // (KUNLUN_GEMM_TILE=BMxWN, e.g. 128x48) forces a candidate.
 QlTile pick_ql_tile(int batch, int n, bool pair) {
     static const QlTile kAll[] = {{128, 48}, {128, 32}, {64, 64}, {64, 32}};
-    auto allowed = [pair](const QlTile &t) { return !pair || t.wn % 32 == 0; };
+    auto allowed = [](const QlTile &) { return true; };
     const int forced = kk::tuning(kk::kGemmTile);
     if (forced > 0)
         for (const QlTile &t : kAll)
@@ -1088,8 +1081,7 @@ hipError_t launch_ql(const void *w, const void *w2, const _Float16 *x16, const f
     if (t.bm == 128 && t.wn == 32) return launch_ql_gemm<128, 32, PAIR>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
     if (t.bm == 64 && t.wn == 64) return launch_ql_gemm<64, 64, PAIR>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
     if (t.bm == 64 && t.wn == 32) return launch_ql_gemm<64, 32, PAIR>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
-    if constexpr (!PAIR)
-        if (t.bm == 128 && t.wn == 48) return launch_ql_gemm<128, 48, false>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
+    if (t.bm == 128 && t.wn == 48) return launch_ql_gemm<128, 48, PAIR>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
     return hipErrorInvalidValue;
 }
 
