@@ -618,9 +618,16 @@ __global__ __launch_bounds__(kGemmThreads) void mfma_gemm(const uint8_t *__restr
 // positions 8(l/16) .. +8 in the prepass's block order. No weight value is
 // decoded twice and no decoded weight passes through LDS.
 //
-// Activation row r of a stage is 16 chunks of 16 B; chunk c sits at position
-// c ^ (r & 15), so the 16 lanes reading one operand row group hit 16
-// distinct bank quads. MFMA layout (wave64): A[l%16][8(l/16) .. +8),
+// LONG (the 64 x 128 tile, which leaves LDS to spare): 256-K stages, each
+// one stage pair of weights, in rings of three activation stages and three
+// weight buffers; a wave takes blocks 2*(w>>2), +1 and 4 + 2*(w>>2), +1 of a
+// stage, the blocks and order two 128-K stages give it, so every tile sums
+// in the same order. Half the stage barriers (K4096 x N4096 at batch 512:
+// 38.9-39.4 -> 37.4 us per call).
+//
+// Activation row r of a stage is 16 (LONG: 32) chunks of 16 B; chunk c sits
+// at position c ^ (r & 15), so the 16 lanes reading one operand row group hit
+// 16 distinct bank quads. MFMA layout (wave64): A[l%16][8(l/16) .. +8),
 // B[8(l/16) .. +8)[l%16], D[4(l/16) + r][l%16].
 //
 // Tiles are numbered weight-tile major and dealt to the 8 XCDs in contiguous
@@ -630,12 +637,15 @@ constexpr int kQlABufs = 3;                 // activation stages in LDS
 constexpr int kQlThreads = 512;
 constexpr int kQlRowPair = 144;             // raw weight bytes per row and stage pair (8 blocks = 9 x 16 B)
 
-template <int BM, int WN, bool PAIR>
+template <int BM, int WN, bool PAIR, bool LONG>
 struct QlShape {
     static constexpr int BN = 4 * WN;                                   // weight rows per tile
     static constexpr int RG = BM / 16, CG = WN / 16;                    // MFMA tiles per wave
-    static constexpr int ABytes = BM * kQlK * 2;                        // one stage of activations
-    static constexpr int ACopiesPerWave = BM * 16 / 64 / 8;             // 1 KB each, per stage
+    static constexpr int KS = LONG ? 2 * kQlK : kQlK;                   // K per stage
+    static constexpr int Chunks = KS / 8;                               // 16-byte chunks per activation row
+    static constexpr int ABytes = BM * KS * 2;                          // one stage of activations
+    static constexpr int ACopiesPerWave = BM * Chunks / 64 / 8;         // 1 KB each, per stage
+    static constexpr int BBufs = LONG ? 3 : 2;                          // weight buffers (stage pairs)
     // weights: 1 KB copies per stage pair; PAIR: the gate rows' copies, then
     // the up rows' from HalfCopies on (each half padded to whole copies; the
     // up rows start at UpBase in the stage-pair buffer)
@@ -648,7 +658,7 @@ struct QlShape {
     static constexpr int BCopiesRem = BCopies % 8;                      // not 0) issue one more
     static constexpr int TileStride = BN + 4;                           // floats per LDS output row
     static constexpr int XferBytes = BM * TileStride * 4;
-    static constexpr int CopyBytes = kQlABufs * ABytes + 2 * BBytes;
+    static constexpr int CopyBytes = kQlABufs * ABytes + BBufs * BBytes;
     static constexpr int RingBytes = CopyBytes > XferBytes ? CopyBytes : XferBytes;
     static constexpr int LdsBytes = RingBytes + BM * 4;                 // + the tile's row scales
     static_assert(ACopiesPerWave + BCopiesPerWave <= 15, "vmcnt immediate");
@@ -672,7 +682,7 @@ __device__ __forceinline__ void ql_copy_a(const uint32_t (&a_off)[S::ACopiesPerW
 #pragma unroll
     for (int t = 0; t < S::ACopiesPerWave; ++t)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) uint8_t *)ql_lds + buf + (wid + 8 * t) * 1024,
-                                                 16, a_off[t], s * (kQlK * 2), 0, 0);
+                                                 16, a_off[t], s * (S::KS * 2), 0, 0);
 }
 
 template <typename S, bool PAIR>
@@ -681,7 +691,7 @@ __device__ __forceinline__ void ql_copy_b(const uint32_t (&b_off)[S::BCopiesPerW
     extern __shared__ __align__(16) uint8_t ql_lds[];
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(b_tile, 0, b_extent, 0x00020000);
     const __amdgpu_buffer_rsrc_t rsrc2 = __builtin_amdgcn_make_buffer_rsrc(b_tile2, 0, b_extent, 0x00020000);
-    const int buf = kQlABufs * S::ABytes + (p & 1) * S::BBytes;
+    const int buf = kQlABufs * S::ABytes + (p % S::BBufs) * S::BBytes;
 #pragma unroll
     for (int t = 0; t < S::BCopiesPerWave; ++t) {
         const int i = wid + 8 * t;
@@ -696,13 +706,13 @@ __device__ __forceinline__ void ql_copy_b(const uint32_t (&b_off)[S::BCopiesPerW
 // its BN/2 up rows (matrix w2, from S::UpBase); waves 0-1 (tile columns
 // 0 .. BN/2) take the gate rows and waves 2-3 the up rows of the same output
 // columns, which the epilogue pairs in LDS.
-template <int BM, int WN, bool PAIR>
+template <int BM, int WN, bool PAIR, bool LONG>
 __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restrict__ w, const uint8_t *__restrict__ w2,
                                                          const _Float16 *__restrict__ x16,
                                                          const float *__restrict__ row_inv, float *__restrict__ y,
                                                          int m_rows, int n_rows, int k_pad, int stages,
                                                          uint32_t row_bytes, int m_tiles, int tiles, int tiles_per_xcd) {
-    using S = QlShape<BM, WN, PAIR>;
+    using S = QlShape<BM, WN, PAIR, LONG>;
     constexpr int kOut = PAIR ? S::BN / 2 : S::BN;             // output columns per tile
     extern __shared__ __align__(16) uint8_t ql_lds[];
 
@@ -734,8 +744,9 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
     uint32_t a_off[S::ACopiesPerWave];
 #pragma unroll
     for (int t = 0; t < S::ACopiesPerWave; ++t) {
-        const int r = 4 * (wid + 8 * t) + g;
-        a_off[t] = static_cast<uint32_t>(r * k_pad + 8 * (c16 ^ (r & 15))) * 2;
+        constexpr int kRowsPerCopy = 64 / S::Chunks;
+        const int r = kRowsPerCopy * (wid + 8 * t) + lane / S::Chunks, pos = lane % S::Chunks;
+        a_off[t] = static_cast<uint32_t>(r * k_pad + 8 * (pos ^ (r & 15))) * 2;
     }
     // B copy i: 16-byte chunks 64c .. 64c+63 (c = i, or i - HalfCopies for the
     // up rows of PAIR) of the [row][144 B] stage-pair bytes, 9 chunks per row.
@@ -785,10 +796,11 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
         }
     };
     auto read_a = [&](const uint8_t *a_lds, int j, int rg) {
-        return *reinterpret_cast<const half8 *>(a_lds + (rg * 16 + c16) * 256 + ((4 * j + g) ^ c16) * 16);
+        return *reinterpret_cast<const half8 *>(a_lds + (rg * 16 + c16) * (S::KS * 2) + ((4 * j + g) ^ c16) * 16);
     };
-    auto compute = [&](const uint8_t *a_lds, const uint8_t *b_lds) {
-        const int j0 = 2 * kh, j1 = j0 + 1;                     // this k-group's blocks of the stage
+    // blocks jb, jb + 1 of the stage (jb = 2 kh, and for LONG also 4 + 2 kh)
+    auto compute = [&](const uint8_t *a_lds, const uint8_t *b_lds, int jb) {
+        const int j0 = jb, j1 = j0 + 1;
         uint32_t nib[S::CG], sbits[S::CG];
         half8 b0[S::CG], b1[S::CG];
         read_b(b_lds, j0, nib, sbits);
@@ -862,13 +874,20 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
     // B((s+1)/2) in flight. The barrier then makes every wave's copies
     // visible and ends all reads of the buffers the next copies refill
     // (stage s-1's activations, stage pair s/2 - 1's weights).
+    // LONG (256-K stages, one stage pair of weights each, three weight
+    // buffers): A(0), B(0), A(1), B(1); at stage s A(s+2) and B(s+2); the top
+    // of stage s leaves A(s+1) and B(s+1) in flight. The k-groups take the
+    // same blocks in the same order as two 128-K stages would give them.
     ql_copy_a<S>(a_off, a_tile, a_extent, wid, 0);
     ql_copy_b<S, PAIR>(b_off, b_tile, b_tile2, b_extent, wid, 0);
-    if (stages > 1) ql_copy_a<S>(a_off, a_tile, a_extent, wid, 1);
+    if (stages > 1) {
+        ql_copy_a<S>(a_off, a_tile, a_extent, wid, 1);
+        if (LONG) ql_copy_b<S, PAIR>(b_off, b_tile, b_tile2, b_extent, wid, 1);
+    }
     for (int s = 0; s < stages; ++s) {
         if (s + 1 >= stages)
             __builtin_amdgcn_s_waitcnt(0x0F70);
-        else if ((s & 1) == 0)
+        else if (!LONG && (s & 1) == 0)
             __builtin_amdgcn_s_waitcnt(0x0F70 | S::ACopiesPerWave);
         else if (my_b_copies == S::BCopiesPerWave)              // wave-uniform
             __builtin_amdgcn_s_waitcnt(0x0F70 | (S::ACopiesPerWave + S::BCopiesPerWave));
@@ -881,10 +900,20 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
         asm volatile("" ::: "memory");
         if (s + 2 < stages) {
             ql_copy_a<S>(a_off, a_tile, a_extent, wid, s + 2);
-            if ((s & 1) == 0) ql_copy_b<S, PAIR>(b_off, b_tile, b_tile2, b_extent, wid, s / 2 + 1);
+            if (LONG)
+                ql_copy_b<S, PAIR>(b_off, b_tile, b_tile2, b_extent, wid, s + 2);
+            else if ((s & 1) == 0)
+                ql_copy_b<S, PAIR>(b_off, b_tile, b_tile2, b_extent, wid, s / 2 + 1);
         }
-        compute(ql_lds + (s % kQlABufs) * S::ABytes,
-                ql_lds + kQlABufs * S::ABytes + ((s >> 1) & 1) * S::BBytes + (s & 1) * (kQlRowPair / 2));
+        const uint8_t *a_lds = ql_lds + (s % kQlABufs) * S::ABytes;
+        if (LONG) {
+            const uint8_t *b_lds = ql_lds + kQlABufs * S::ABytes + (s % S::BBufs) * S::BBytes;
+            compute(a_lds, b_lds, 2 * kh);
+            compute(a_lds, b_lds, 4 + 2 * kh);
+        } else {
+            compute(a_lds, ql_lds + kQlABufs * S::ABytes + ((s >> 1) & 1) * S::BBytes + (s & 1) * (kQlRowPair / 2),
+                    2 * kh);
+        }
     }
 
     // Epilogue. k-group 1 writes its sums into a row-major LDS tile (row
@@ -1057,20 +1086,20 @@ QlTile pick_ql_tile(int batch, int n, bool pair) {
     return pick;
 }
 
-template <int BM, int WN, bool PAIR>
+template <int BM, int WN, bool PAIR, bool LONG = false>
 hipError_t launch_ql_gemm(const void *w, const void *w2, const _Float16 *x16, const float *row_inv, float *y, int batch,
                           int n, int k, int k_pad, hipStream_t stream) {
-    using S = QlShape<BM, WN, PAIR>;
-    hipError_t rc = kk::opt_in_lds(reinterpret_cast<const void *>(&q4_lds_gemm<BM, WN, PAIR>), S::LdsBytes);
+    using S = QlShape<BM, WN, PAIR, LONG>;
+    hipError_t rc = kk::opt_in_lds(reinterpret_cast<const void *>(&q4_lds_gemm<BM, WN, PAIR, LONG>), S::LdsBytes);
     if (rc != hipSuccess) return rc;
     const int out = PAIR ? S::BN / 2 : S::BN;
     const int m_tiles = (batch + BM - 1) / BM;
     const int tiles = m_tiles * ((n + out - 1) / out);
     const int tiles_per_xcd = (tiles + kXcds - 1) / kXcds;
     const uint32_t row_bytes = static_cast<uint32_t>(k / 32 * 18);
-    hipLaunchKernelGGL((q4_lds_gemm<BM, WN, PAIR>), dim3(tiles_per_xcd * kXcds), dim3(kQlThreads), S::LdsBytes, stream,
-                       static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(w2), x16, row_inv, y, batch, n,
-                       k_pad, k / kQlK, row_bytes, m_tiles, tiles, tiles_per_xcd);
+    hipLaunchKernelGGL((q4_lds_gemm<BM, WN, PAIR, LONG>), dim3(tiles_per_xcd * kXcds), dim3(kQlThreads), S::LdsBytes,
+                       stream, static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(w2), x16, row_inv, y, batch,
+                       n, k_pad, k / S::KS, row_bytes, m_tiles, tiles, tiles_per_xcd);
     return hipGetLastError();
 }
 
@@ -1080,7 +1109,7 @@ hipError_t launch_ql(const void *w, const void *w2, const _Float16 *x16, const f
     const QlTile t = pick_ql_tile(batch, n, PAIR);
     if (t.bm == 128 && t.wn == 32) return launch_ql_gemm<128, 32, PAIR>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
     if (t.bm == 64 && t.wn == 64) return launch_ql_gemm<64, 64, PAIR>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
-    if (t.bm == 64 && t.wn == 32) return launch_ql_gemm<64, 32, PAIR>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
+    if (t.bm == 64 && t.wn == 32) return launch_ql_gemm<64, 32, PAIR, true>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
     if (t.bm == 128 && t.wn == 48) return launch_ql_gemm<128, 48, PAIR>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
     return hipErrorInvalidValue;
 }
