@@ -231,6 +231,23 @@ def test_q4_subnormal_scales(gpu, oracle, knobs, k, batch, w_offset, route, tol,
         assert res["reference"], res
 
 
+@pytest.mark.parametrize("tile", ["128x48", "128x32", "64x64", "64x32"])
+def test_q4_subnormal_scales_gemm_tiles(gpu, oracle, knobs, tile):
+    # the subnormal-scale correction of every LDS GEMM tile (partial M and N tiles)
+    knobs("KUNLUN_GEMM_TILE", tile)
+    k, n, batch = 512, 200, 160
+    q4 = q4_subnormal(k, n, 91, True, tiny=True)
+    dec = oracle.q4_decode(q4, k, n)
+    x = np.random.default_rng(92).standard_normal((batch, k)).astype(np.float32)
+    y, got_route, guard_ok = run_matmul(kl.WeightType.q4_0, q4, x, k, n, batch)
+    assert got_route == "q4_gemm_mfma" and guard_ok
+    gold = oracle.gold(dec, x, threads=16)
+    assert np.all(np.isfinite(y))
+    ok, ratio = gemm_bound_ok(y, gold, dec, x, 2e-3)
+    print(f"  q4 subnormal scales tile {tile}: max err / bound = {ratio:.3g}", flush=True)
+    assert ok, f"tile {tile}: error {ratio:.3g} x the bound"
+
+
 @pytest.mark.parametrize("mixed", [False, True], ids=["all_subnormal", "mixed"])
 def test_native_q4_subnormal_scales(gpu, oracle, mixed):
     from test_gpu_native_q4 import NativeCase, check

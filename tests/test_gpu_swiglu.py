@@ -352,7 +352,7 @@ def test_matmul_swiglu_decode_pair_unfused_fallbacks(gpu, oracle):
         assert finite and ok, worst
 
 
-@pytest.mark.parametrize("tile", ["128x32", "64x64", "64x32"])
+@pytest.mark.parametrize("tile", ["128x48", "128x32", "64x64", "64x32"])
 def test_matmul_swiglu_tile_variants(gpu, oracle, knobs, tile):
     # the pair tiles of the LDS-copy Q4_0 kernel: gate and up column tiles per wave
     knobs("KUNLUN_GEMM_TILE", tile)
