@@ -354,6 +354,7 @@ def gemm_leg(kernel, events, stream, device: int, reps: int) -> dict:
 
 
 SMALL_BATCH_Q4 = (4096, 14336, (2, 4, 8, 16))
+DECODE_PAIR_BATCHES = (1, 4, 8, 16)                    # matmul_swiglu at decode batch sizes
 SMALL_DENSE = (4096, 4096, (1, 8))                   # F16 / F32 part of configs[2]
 DECODE_PAIR = (4096, 11008)                          # gate/up pair of the decode layer (matmul_swiglu, batch 1)
 
@@ -362,7 +363,7 @@ def small_batch_leg(kernel, events, stream, device: int, reps: int) -> dict:
     """Q4_0 K4096 x N14336 at batch 2..16 and F16/F32 4096^2 at
     batch 1 and 8, each over rotating weight copies (>= 640 MB) so weights stream
     from HBM. GB/s = algorithmic bytes (weights + 4bk + 4bn) / launch time. Also
-    the decode gate/up pair (matmul_swiglu, Q4_0 K4096 x 2 x N11008, batch 1)."""
+    the decode gate/up pair (matmul_swiglu, Q4_0 K4096 x 2 x N11008, batch 1, 4, 8 and 16)."""
     out = {}
     rng = np.random.Generator(np.random.PCG64(21))
 
@@ -417,32 +418,33 @@ def small_batch_leg(kernel, events, stream, device: int, reps: int) -> dict:
             kl.check(kl.copy(u.data, first_u.data, nbytes, kl.CopyKind.device_to_device))
             kl.check(kl.wait())
         pairs.append((g, u))
-    xb = kl.Buffer(device, 4 * k)
-    xb.upload(rng.standard_normal(k, dtype=np.float32))
-    yb = kl.Buffer(device, 4 * n)
-    with kl.runtime_mutex():
-        for i in range(5):
-            g, u = pairs[i % len(pairs)]
-            kl.matmul_swiglu(kernel, device, yb.data, g.data, u.data, xb.data, k, n, 1, kl.WeightType.q4_0)
-        kl.select(device)
-        kl.check(kl.wait())
-        start, stop = events.create(), events.create()
-        events.record(start, stream)
-        for i in range(reps):
-            g, u = pairs[i % len(pairs)]
-            kl.matmul_swiglu(kernel, device, yb.data, g.data, u.data, xb.data, k, n, 1, kl.WeightType.q4_0)
-        events.record(stop, stream)
-        ms = events.elapsed_ms(start, stop) / reps
-        kl.check(kl.wait())
-    total = 2 * nbytes + 4 * k + 4 * n
-    out[f"q4_pair_swiglu_k{k}_n{n}_b1"] = {"us": round(ms * 1e3, 3), "gbps": round(total / (ms * 1e-3) / 1e9, 1),
-                                          "hbm_frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-                                          "route": kernel.route}
+    for batch in DECODE_PAIR_BATCHES:
+        xb = kl.Buffer(device, 4 * batch * k)
+        xb.upload(rng.standard_normal((batch, k), dtype=np.float32))
+        yb = kl.Buffer(device, 4 * batch * n)
+        with kl.runtime_mutex():
+            for i in range(5):
+                g, u = pairs[i % len(pairs)]
+                kl.matmul_swiglu(kernel, device, yb.data, g.data, u.data, xb.data, k, n, batch, kl.WeightType.q4_0)
+            kl.select(device)
+            kl.check(kl.wait())
+            start, stop = events.create(), events.create()
+            events.record(start, stream)
+            for i in range(reps):
+                g, u = pairs[i % len(pairs)]
+                kl.matmul_swiglu(kernel, device, yb.data, g.data, u.data, xb.data, k, n, batch, kl.WeightType.q4_0)
+            events.record(stop, stream)
+            ms = events.elapsed_ms(start, stop) / reps
+            kl.check(kl.wait())
+        total = 2 * nbytes + 4 * batch * k + 4 * batch * n
+        out[f"q4_pair_swiglu_k{k}_n{n}_b{batch}"] = {
+            "us": round(ms * 1e3, 3), "gbps": round(total / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "route": kernel.route}
+        xb.close()
+        yb.close()
     for g, u in pairs:
         g.close()
         u.close()
-    xb.close()
-    yb.close()
 
     k, n, batches = SMALL_DENSE
     w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))

@@ -110,7 +110,11 @@ __device__ __forceinline__ int scale_offset(int q_groups, int steps, int step, i
 // Q = column groups of four (batch <= 4Q), SPW = steps per wave, ITEMS =
 // activation items per thread (4Q * steps * 32 items over the workgroup).
 template <int Q, int SPW, int ITEMS>
-__global__ __launch_bounds__(kThreads) void q4_bdiag_gemv(const uint8_t *__restrict__ w, const float *__restrict__ x,
+// w2 (gate/up pair, else null): rows n_split .. n - 1 are rows 0 .. of w2
+// (n = 2 n_split), so y = [batch][2 n_split], the w rows then the w2 rows.
+__global__ __launch_bounds__(kThreads) void q4_bdiag_gemv(const uint8_t *__restrict__ w,
+                                                        const uint8_t *__restrict__ w2, int n_split,
+                                                        const float *__restrict__ x,
                                                         float *__restrict__ y, int k, int n, int batch, int steps,
                                                         int parts) {
     extern __shared__ __align__(16) uint8_t lds[];
@@ -143,7 +147,9 @@ __global__ __launch_bounds__(kThreads) void q4_bdiag_gemv(const uint8_t *__restr
     uint32_t ring[SPW][9];
     auto load_step = [&](int j) {
         const int p = min(4 * (s_first + j) + h, pairs - 1);
-        const uint32_t *src = reinterpret_cast<const uint32_t *>(w + static_cast<size_t>(row) * row_bytes +
+        const bool second = w2 && row >= n_split;
+        const uint32_t *src = reinterpret_cast<const uint32_t *>((second ? w2 : w) +
+                                                                 static_cast<size_t>(second ? row - n_split : row) * row_bytes +
                                                                  static_cast<size_t>(p) * 36);
         const kk::u32x4_a4 a = kk::load_u32x4(src), c = kk::load_u32x4(src + 4);
         ring[j][0] = a.x; ring[j][1] = a.y; ring[j][2] = a.z; ring[j][3] = a.w;
@@ -331,9 +337,11 @@ extern "C" int kk_q4_bdiag_gemv_supported(const void *w, const float *x, int k, 
 
 // Tiles per workgroup: the fewest (1, 2, 4, 8, 16) with which the workgroups
 // the CUs hold at once cover every tile (else the last candidate that fits).
-extern "C" int kk_q4_bdiag_gemv(const void *w, const float *x, float *y, int k, int n, int batch, int cus,
-                                hipStream_t stream) {
-    if (!kk_q4_bdiag_gemv_supported(w, x, k, n, batch) || !y || cus <= 0) return hipErrorInvalidValue;
+namespace {
+hipError_t launch_bdiag(const void *w, const void *w2, const float *x, float *y, int k, int n, int batch, int cus,
+                        hipStream_t stream) {
+    const int n_split = w2 ? n : 0;
+    if (w2) n *= 2;
     int device = 0;
     hipError_t rc = hipGetDevice(&device);
     if (rc != hipSuccess) return rc;
@@ -354,7 +362,26 @@ extern "C" int kk_q4_bdiag_gemv(const void *w, const float *x, float *y, int k, 
     if (!kernel) return hipErrorInvalidConfiguration;
     const int groups = (tiles + plan.tiles_per_group - 1) / plan.tiles_per_group;
     const uint8_t *wb = static_cast<const uint8_t *>(w);
-    void *args[] = {&wb, &x, &y, &k, &n, &batch, &plan.steps, &plan.parts};
+    const uint8_t *wb2 = static_cast<const uint8_t *>(w2);
+    int split = n_split;
+    void *args[] = {&wb, &wb2, &split, &x, &y, &k, &n, &batch, &plan.steps, &plan.parts};
     rc = hipLaunchKernel(kernel, dim3(groups), dim3(kThreads), args, plan.lds_bytes, stream);
     return rc != hipSuccess ? rc : hipGetLastError();
+}
+} // namespace
+
+extern "C" int kk_q4_bdiag_gemv(const void *w, const float *x, float *y, int k, int n, int batch, int cus,
+                                hipStream_t stream) {
+    if (!kk_q4_bdiag_gemv_supported(w, x, k, n, batch) || !y || cus <= 0) return hipErrorInvalidValue;
+    return launch_bdiag(w, nullptr, x, y, k, n, batch, cus, stream);
+}
+
+// Gate/up pair: both matrices in one launch (X staged once per workgroup),
+// y = [batch][2n], the gate products then the up products of each row.
+extern "C" int kk_q4_bdiag_gemv_pair(const void *w_gate, const void *w_up, const float *x, float *y, int k, int n,
+                                     int batch, int cus, hipStream_t stream) {
+    if (!kk_q4_bdiag_gemv_supported(w_gate, x, k, n, batch) || !kk_q4_bdiag_gemv_supported(w_up, x, k, n, batch) ||
+        !y || cus <= 0 || n > (1 << 29))
+        return hipErrorInvalidValue;
+    return launch_bdiag(w_gate, w_up, x, y, k, n, batch, cus, stream);
 }

@@ -56,12 +56,18 @@ int kk_q4_mfma_gemv(const void *w, const float *x, float *y, int k, int n, int b
 // ceil(batch/4) x 4480 bytes <= 160 KiB); `cus` sizes the grid.
 int kk_q4_bdiag_gemv_supported(const void *w, const float *x, int k, int n, int batch);
 int kk_q4_bdiag_gemv(const void *w, const float *x, float *y, int k, int n, int batch, int cus, hipStream_t stream);
+// The gate/up pair in one launch: y = [batch][2n] (gate products, then up).
+int kk_q4_bdiag_gemv_pair(const void *w_gate, const void *w_up, const float *x, float *y, int k, int n, int batch,
+                          int cus, hipStream_t stream);
 
 // Q4_0 GEMV for batch 1..8 at K = 4096 on fp16 MFMA, one pass over W with
 // weight rows streamed through per-wave LDS (no workspace): 16-byte aligned
 // weights and X; `cus` sizes the grid.
 int kk_q4_stream_gemv_supported(const void *w, const float *x, int k, int n, int batch);
 int kk_q4_stream_gemv(const void *w, const float *x, float *y, int k, int n, int batch, int cus, hipStream_t stream);
+// The gate/up pair in one launch: y = [batch][2n] (gate products, then up).
+int kk_q4_stream_gemv_pair(const void *w_gate, const void *w_up, const float *x, float *y, int k, int n, int batch,
+                           int cus, hipStream_t stream);
 
 // F32 (type 0) / F16 (type 1) GEMV for batch 1..16 on fp32 MFMA, one pass over
 // W; 16-byte aligned weights and activations.

@@ -121,6 +121,50 @@ Kernel::~Kernel() {
     delete impl_;
 }
 
+// The F32/F16/Q4_0 product's route for one matrix (matmul's, and each half of
+// an unfused gate/up pair): the prefill GEMM, the small-batch MFMA GEMVs,
+// else the single-pass GEMVs.
+static void dispatch_dense(Kernel::Impl & impl, detail::DeviceContext & ctx, int id, void * y, const void * w,
+                    const void * x, int k, int n, int batch, WeightType type) {
+    if ((type == WeightType::q4_0 || (type == WeightType::f16 && ((uintptr_t)w & 15) == 0)) &&
+        batch >= gemm_min_batch() && ((uintptr_t)x & 15) == 0) {
+        grow(id, ctx, impl.gemm_workspace, impl.gemm_workspace_size, kk_gemm_workspace_bytes(k, n, batch));
+        detail::check_hip((hipError_t)kk_gemm((int)type, w, static_cast<const float *>(x), static_cast<float *>(y), k,
+                                              n, batch, impl.gemm_workspace, ctx.stream, &impl.route),
+                          "kk_gemm");
+    } else if ((type == WeightType::f32 || type == WeightType::f16) && dense_mfma_batch(batch) &&
+               ((uintptr_t)w & 15) == 0 && ((uintptr_t)x & 15) == 0) {
+        detail::check_hip((hipError_t)kk_dense_mfma_gemv((int)type, w, static_cast<const float *>(x),
+                                                         static_cast<float *>(y), k, n, batch, ctx.stream),
+                          "kk_dense_mfma_gemv");
+        impl.route = type == WeightType::f16 ? "f16_mfma_gemv" : "f32_mfma_gemv";
+    } else if (type == WeightType::q4_0 && kk::q4_stream_batch(batch) &&
+               kk_q4_stream_gemv_supported(w, static_cast<const float *>(x), k, n, batch)) {
+        detail::check_hip((hipError_t)kk_q4_stream_gemv(w, static_cast<const float *>(x), static_cast<float *>(y), k, n,
+                                                        batch, ctx.cus, ctx.stream),
+                          "kk_q4_stream_gemv");
+        impl.route = "q4_stream_gemv";
+    } else if (type == WeightType::q4_0 && kk::q4_bdiag_batch(batch) &&
+               kk_q4_bdiag_gemv_supported(w, static_cast<const float *>(x), k, n, batch)) {
+        detail::check_hip((hipError_t)kk_q4_bdiag_gemv(w, static_cast<const float *>(x), static_cast<float *>(y), k, n,
+                                                       batch, ctx.cus, ctx.stream),
+                          "kk_q4_bdiag_gemv");
+        impl.route = "q4_bdiag_gemv";
+    } else if (type == WeightType::q4_0 && q4_mfma_batch(batch, k % 256 == 0 && ((uintptr_t)w & 15) == 0) &&
+               k % 64 == 0 && ((uintptr_t)w & 3) == 0) {
+        grow(id, ctx, impl.gemm_workspace, impl.gemm_workspace_size, kk_q4_mfma_gemv_workspace_bytes(k));
+        detail::check_hip((hipError_t)kk_q4_mfma_gemv(w, static_cast<const float *>(x), static_cast<float *>(y), k, n,
+                                                      batch, impl.gemm_workspace, ctx.cus, ctx.stream),
+                          "kk_q4_mfma_gemv");
+        impl.route = "q4_mfma_gemv";
+    } else {
+        detail::check_hip((hipError_t)kk_dense_matmul((int)type, w, static_cast<const float *>(x),
+                                                      static_cast<float *>(y), k, n, batch, ctx.stream,
+                                                      &impl.route),
+                          "kk_dense_matmul");
+    }
+}
+
 void matmul(Kernel & kernel, int id, void * y, const void * w, const void * x, int k, int n, int batch,
             WeightType type, const float * scales, const float * maximum, int tile) {
     std::lock_guard<std::recursive_mutex> lock(detail::mutex());
@@ -167,42 +211,8 @@ void matmul(Kernel & kernel, int id, void * y, const void * w, const void * x, i
                                                    maximum, static_cast<float *>(y), k, n, batch, ctx.stream,
                                                    &impl.route),
                           "kk_i8_matmul");
-    } else if ((type == WeightType::q4_0 || (type == WeightType::f16 && ((uintptr_t)w & 15) == 0)) &&
-               batch >= gemm_min_batch() && ((uintptr_t)x & 15) == 0) {
-        grow(id, ctx, impl.gemm_workspace, impl.gemm_workspace_size, kk_gemm_workspace_bytes(k, n, batch));
-        detail::check_hip((hipError_t)kk_gemm((int)type, w, static_cast<const float *>(x), static_cast<float *>(y), k,
-                                              n, batch, impl.gemm_workspace, ctx.stream, &impl.route),
-                          "kk_gemm");
-    } else if ((type == WeightType::f32 || type == WeightType::f16) && dense_mfma_batch(batch) &&
-               ((uintptr_t)w & 15) == 0 && ((uintptr_t)x & 15) == 0) {
-        detail::check_hip((hipError_t)kk_dense_mfma_gemv((int)type, w, static_cast<const float *>(x),
-                                                         static_cast<float *>(y), k, n, batch, ctx.stream),
-                          "kk_dense_mfma_gemv");
-        impl.route = type == WeightType::f16 ? "f16_mfma_gemv" : "f32_mfma_gemv";
-    } else if (type == WeightType::q4_0 && kk::q4_stream_batch(batch) &&
-               kk_q4_stream_gemv_supported(w, static_cast<const float *>(x), k, n, batch)) {
-        detail::check_hip((hipError_t)kk_q4_stream_gemv(w, static_cast<const float *>(x), static_cast<float *>(y), k, n,
-                                                        batch, ctx.cus, ctx.stream),
-                          "kk_q4_stream_gemv");
-        impl.route = "q4_stream_gemv";
-    } else if (type == WeightType::q4_0 && kk::q4_bdiag_batch(batch) &&
-               kk_q4_bdiag_gemv_supported(w, static_cast<const float *>(x), k, n, batch)) {
-        detail::check_hip((hipError_t)kk_q4_bdiag_gemv(w, static_cast<const float *>(x), static_cast<float *>(y), k, n,
-                                                       batch, ctx.cus, ctx.stream),
-                          "kk_q4_bdiag_gemv");
-        impl.route = "q4_bdiag_gemv";
-    } else if (type == WeightType::q4_0 && q4_mfma_batch(batch, k % 256 == 0 && ((uintptr_t)w & 15) == 0) &&
-               k % 64 == 0 && ((uintptr_t)w & 3) == 0) {
-        grow(id, ctx, impl.gemm_workspace, impl.gemm_workspace_size, kk_q4_mfma_gemv_workspace_bytes(k));
-        detail::check_hip((hipError_t)kk_q4_mfma_gemv(w, static_cast<const float *>(x), static_cast<float *>(y), k, n,
-                                                      batch, impl.gemm_workspace, ctx.cus, ctx.stream),
-                          "kk_q4_mfma_gemv");
-        impl.route = "q4_mfma_gemv";
     } else {
-        detail::check_hip((hipError_t)kk_dense_matmul((int)type, w, static_cast<const float *>(x),
-                                                      static_cast<float *>(y), k, n, batch, ctx.stream,
-                                                      &impl.route),
-                          "kk_dense_matmul");
+        dispatch_dense(impl, ctx, id, y, w, x, k, n, batch, type);
     }
     detail::last_route = impl.route;
     detail::count_matmul(id);
@@ -235,19 +245,40 @@ void matmul_swiglu(Kernel & kernel, int id, void * y, const void * w_gate, const
                                                              static_cast<float *>(y), k, n, batch, ctx.stream),
                           "kk_q4_gemv_pair_swiglu");
         impl.route = "q4_gemv_fused_pair_swiglu";
+    } else if (type == WeightType::q4_0 &&
+               ((kk::q4_stream_batch(batch) &&
+                 kk_q4_stream_gemv_supported(w_gate, static_cast<const float *>(x), k, n, batch) &&
+                 kk_q4_stream_gemv_supported(w_up, static_cast<const float *>(x), k, n, batch)) ||
+                (kk::q4_bdiag_batch(batch) &&
+                 kk_q4_bdiag_gemv_supported(w_gate, static_cast<const float *>(x), k, n, batch) &&
+                 kk_q4_bdiag_gemv_supported(w_up, static_cast<const float *>(x), k, n, batch)))) {
+        // small batch: both products in one launch into [batch][2n] (each row's
+        // gate values, then its up values), then SwiGLU
+        grow(id, ctx, impl.pair_workspace, impl.pair_workspace_size, (size_t)batch * n * 8);
+        float * stacked = static_cast<float *>(impl.pair_workspace);
+        const bool streamed = kk::q4_stream_batch(batch) &&
+                              kk_q4_stream_gemv_supported(w_gate, static_cast<const float *>(x), k, n, batch) &&
+                              kk_q4_stream_gemv_supported(w_up, static_cast<const float *>(x), k, n, batch);
+        if (streamed)
+            detail::check_hip((hipError_t)kk_q4_stream_gemv_pair(w_gate, w_up, static_cast<const float *>(x), stacked,
+                                                                 k, n, batch, ctx.cus, ctx.stream),
+                              "kk_q4_stream_gemv_pair");
+        else
+            detail::check_hip((hipError_t)kk_q4_bdiag_gemv_pair(w_gate, w_up, static_cast<const float *>(x), stacked,
+                                                                k, n, batch, ctx.cus, ctx.stream),
+                              "kk_q4_bdiag_gemv_pair");
+        detail::check_hip((hipError_t)kk_swiglu(y, stacked, stacked + n, n, batch, n * 8, n * 8, n * 4, 4, ctx.stream),
+                          "kk_swiglu");
+        impl.route = streamed ? "q4_stream_pair_swiglu" : "q4_bdiag_pair_swiglu";
     } else {
         // gate and up rows side by side in the workspace: [batch][2n] F32
         const size_t half = (size_t)batch * n * 4;
         grow(id, ctx, impl.pair_workspace, impl.pair_workspace_size, 2 * half);
         float * gate = static_cast<float *>(impl.pair_workspace);
         float * up = reinterpret_cast<float *>(static_cast<char *>(impl.pair_workspace) + half);
-        const char * route = nullptr;
-        detail::check_hip((hipError_t)kk_dense_matmul((int)type, w_gate, static_cast<const float *>(x), gate, k, n,
-                                                      batch, ctx.stream, &route),
-                          "kk_dense_matmul");
-        detail::check_hip((hipError_t)kk_dense_matmul((int)type, w_up, static_cast<const float *>(x), up, k, n,
-                                                      batch, ctx.stream, &route),
-                          "kk_dense_matmul");
+        // each product on matmul's own route for its shape
+        dispatch_dense(impl, ctx, id, gate, w_gate, x, k, n, batch, type);
+        dispatch_dense(impl, ctx, id, up, w_up, x, k, n, batch, type);
         detail::check_hip((hipError_t)kk_swiglu(y, gate, up, n, batch, n * 4, n * 4, n * 4, 4, ctx.stream),
                           "kk_swiglu");
         impl.route = type == WeightType::q4_0 ? "q4_gemv_pair_swiglu"

@@ -78,14 +78,18 @@ __device__ __forceinline__ uint32_t from_partner(uint32_t old, uint32_t src) {
         __builtin_amdgcn_update_dpp(static_cast<int>(old), static_cast<int>(src), kXor8, 0xf, BANKS, false));
 }
 
+// w2 (gate/up pair, else null): tiles T .. 2T - 1 (T = ceil(n / 32)) are the
+// tiles of w2, and y is [batch][2n]: the w rows' products, then the w2 rows'.
 __global__ __launch_bounds__(kWave * kWaves) void q4_stream_gemv(const uint8_t *__restrict__ w,
+                                                               const uint8_t *__restrict__ w2,
                                                                const float *__restrict__ x, float *__restrict__ y,
                                                                int n, int batch, int tiles_per_group) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & (kWave - 1);
     const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
     const int r16 = lane & 15, g = lane >> 4;
-    const int tiles = (n + kTileRows - 1) / kTileRows;
+    const int mtiles = (n + kTileRows - 1) / kTileRows;          // tiles per matrix
+    const int tiles = w2 ? 2 * mtiles : mtiles;
     const int tile0 = blockIdx.x * tiles_per_group;
     const int c = wid;                                            // this wave's K chunk
     uint8_t *stage = lds + wid * kStageBytes;
@@ -105,9 +109,11 @@ __global__ __launch_bounds__(kWave * kWaves) void q4_stream_gemv(const uint8_t *
     __builtin_amdgcn_sched_barrier(0);
     const size_t total = static_cast<size_t>(n) * kRowBytes;
     auto tile_buffer = [&](int t) {
-        const size_t off = min(static_cast<size_t>(tile0 + t) * kTileRows * kRowBytes, total);
+        const int gt = tile0 + t;
+        const bool second = w2 && gt >= mtiles;                   // wave-uniform
+        const size_t off = min(static_cast<size_t>(second ? gt - mtiles : gt) * kTileRows * kRowBytes, total);
         const uint32_t extent = static_cast<uint32_t>(min(total - off, static_cast<size_t>(0xfffffff0u)));
-        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(w + off), 0, extent, 0x00020000);
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>((second ? w2 : w) + off), 0, extent, 0x00020000);
     };
     uint32_t goff[kPiecesPerLane], loff[kPiecesPerLane];   // piece offsets in the tile and in the stage
 #pragma unroll
@@ -266,13 +272,15 @@ __global__ __launch_bounds__(kWave * kWaves) void q4_stream_gemv(const uint8_t *
     // 5. column m, row 32 t + 16 rg + nn: lane (nn, m / 4) element m % 4 of every wave
     for (int idx = threadIdx.x; idx < tiles_per_group * 256; idx += kWave * kWaves) {
         const int t = idx >> 8, rg = (idx >> 7) & 1, m = (idx >> 4) & 7, nn = idx & 15;
-        const int out_row = (tile0 + t) * kTileRows + rg * 16 + nn;
-        if (m >= batch || tile0 + t >= tiles || out_row >= n) continue;
+        const int gt = tile0 + t;
+        const bool second = w2 && gt >= mtiles;
+        const int out_row = (second ? gt - mtiles : gt) * kTileRows + rg * 16 + nn;
+        if (m >= batch || gt >= tiles || out_row >= n) continue;
         const int src = (m >> 2) * 16 + nn;
         float sum = 0.0f;
 #pragma unroll
         for (int ww = 0; ww < kWaves; ++ww) sum += partial[((t * 2 + rg) * kWaves + ww) * 32 + src][m & 3];
-        y[static_cast<size_t>(m) * n + out_row] = sum;
+        y[static_cast<size_t>(m) * (w2 ? 2 * n : n) + (second ? n : 0) + out_row] = sum;
     }
 }
 
@@ -284,14 +292,31 @@ extern "C" int kk_q4_stream_gemv_supported(const void *w, const float *x, int k,
 }
 
 // Tiles per workgroup: ceil(tiles / CUs), at most 4 (then more workgroups than CUs).
+namespace {
+hipError_t launch_stream(const void *w, const void *w2, const float *x, float *y, int n, int batch, int cus,
+                         hipStream_t stream) {
+    const hipError_t rc = kk::opt_in_lds(reinterpret_cast<const void *>(&q4_stream_gemv), kLdsBytes);
+    if (rc != hipSuccess) return rc;
+    const int tiles = (w2 ? 2 : 1) * ((n + kTileRows - 1) / kTileRows);
+    const int t = std::max(1, std::min(kMaxTiles, (tiles + cus - 1) / cus));
+    hipLaunchKernelGGL(q4_stream_gemv, dim3((tiles + t - 1) / t), dim3(kWave * kWaves), kLdsBytes, stream,
+                       static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(w2), x, y, n, batch, t);
+    return hipGetLastError();
+}
+} // namespace
+
 extern "C" int kk_q4_stream_gemv(const void *w, const float *x, float *y, int k, int n, int batch, int cus,
                                  hipStream_t stream) {
     if (!kk_q4_stream_gemv_supported(w, x, k, n, batch) || !y || cus <= 0) return hipErrorInvalidValue;
-    const hipError_t rc = kk::opt_in_lds(reinterpret_cast<const void *>(&q4_stream_gemv), kLdsBytes);
-    if (rc != hipSuccess) return rc;
-    const int tiles = (n + kTileRows - 1) / kTileRows;
-    const int t = std::max(1, std::min(kMaxTiles, (tiles + cus - 1) / cus));
-    hipLaunchKernelGGL(q4_stream_gemv, dim3((tiles + t - 1) / t), dim3(kWave * kWaves), kLdsBytes, stream,
-                       static_cast<const uint8_t *>(w), x, y, n, batch, t);
-    return hipGetLastError();
+    return launch_stream(w, nullptr, x, y, n, batch, cus, stream);
+}
+
+// Gate/up pair: both matrices in one launch (X read once per workgroup),
+// y = [batch][2n], the gate products then the up products of each row.
+extern "C" int kk_q4_stream_gemv_pair(const void *w_gate, const void *w_up, const float *x, float *y, int k, int n,
+                                      int batch, int cus, hipStream_t stream) {
+    if (!kk_q4_stream_gemv_supported(w_gate, x, k, n, batch) || !kk_q4_stream_gemv_supported(w_up, x, k, n, batch) ||
+        !y || cus <= 0)
+        return hipErrorInvalidValue;
+    return launch_stream(w_gate, w_up, x, y, n, batch, cus, stream);
 }

@@ -337,8 +337,9 @@ def test_matmul_swiglu_decode_pair_fused(gpu, oracle, knobs, k, n, batch, inf):
         assert finite and ok, worst
 
 
-def test_matmul_swiglu_decode_pair_unfused_fallbacks(gpu, oracle):
-    # batch 1 fuses; batch 3 takes two single-pass GEMVs plus swiglu
+def test_matmul_swiglu_decode_pair_routes(gpu, oracle):
+    # batch 1 fuses SiLU * up into the GEMV; batch 3 runs both products in one
+    # block-diagonal launch, then swiglu
     k, n = 512, 96
     wg = gaussian((n, k), 0.02, 71)
     wu = gaussian((n, k), 0.02, 72)
@@ -348,8 +349,29 @@ def test_matmul_swiglu_decode_pair_unfused_fallbacks(gpu, oracle):
         x = gaussian((batch, k), 1.0, 73 + batch)
         y, route = run_pair(kl.WeightType.q4_0, pg, pu, x, k, n, batch)
         finite, ok, worst = check_pair(y, x, dg, du, oracle, 1e-4)
-        assert route == ("q4_gemv_fused_pair_swiglu" if batch == 1 else "q4_gemv_pair_swiglu")
+        assert route == ("q4_gemv_fused_pair_swiglu" if batch == 1 else "q4_bdiag_pair_swiglu")
         assert finite and ok, worst
+
+
+# Small-batch pairs in one launch: the gate and up rows stacked as one matrix
+# of 2n rows (n = 300: the streamed kernel's 32-row tiles and the
+# block-diagonal kernel's 16-row tiles end inside the gate matrix). Batch 16
+# at K 4096 fits neither kernel and stays on two GEMVs plus swiglu.
+@pytest.mark.parametrize("batch,route", [(3, "q4_bdiag_pair_swiglu"), (4, "q4_bdiag_pair_swiglu"),
+                                         (5, "q4_stream_pair_swiglu"), (8, "q4_stream_pair_swiglu"),
+                                         (16, "q4_gemv_pair_swiglu")])
+def test_matmul_swiglu_small_batch_one_launch(gpu, oracle, batch, route):
+    k, n = 4096, 300
+    wg = gaussian((n, k), 0.02, 81)
+    wu = gaussian((n, k), 0.02, 82)
+    pg, dg = weight_payload(kl.WeightType.q4_0, wg, oracle)
+    pu, du = weight_payload(kl.WeightType.q4_0, wu, oracle)
+    x = gaussian((batch, k), 1.0, 83 + batch)
+    y, got = run_pair(kl.WeightType.q4_0, pg, pu, x, k, n, batch)
+    finite, ok, worst = check_pair(y, x, dg, du, oracle, 1e-4)
+    print(f"  pair b{batch} {got} worst/bound={worst:.3g}", flush=True)
+    assert got == route
+    assert finite and ok, worst
 
 
 @pytest.mark.parametrize("tile", ["128x48", "128x32", "64x64", "64x32"])
