@@ -126,8 +126,23 @@ Kernel::~Kernel() {
 // else the single-pass GEMVs.
 static void dispatch_dense(Kernel::Impl & impl, detail::DeviceContext & ctx, int id, void * y, const void * w,
                     const void * x, int k, int n, int batch, WeightType type) {
-    if ((type == WeightType::q4_0 || (type == WeightType::f16 && ((uintptr_t)w & 15) == 0)) &&
-        batch >= gemm_min_batch() && ((uintptr_t)x & 15) == 0) {
+    const bool gemm = (type == WeightType::q4_0 || (type == WeightType::f16 && ((uintptr_t)w & 15) == 0)) &&
+                      batch >= gemm_min_batch() && ((uintptr_t)x & 15) == 0;
+    if (!gemm && batch > 16) {
+        // batches between the small-batch kernels and the GEMM: chunks of 16
+        // columns, each on the route a 16-column call takes (one pass over
+        // the weights per chunk, against one per 2-4 columns on the general
+        // GEMV). X and Y chunks keep their alignment (K % 32 == 0).
+        const char * first = nullptr;
+        for (int b0 = 0; b0 < batch; b0 += 16) {
+            dispatch_dense(impl, ctx, id, static_cast<char *>(y) + (size_t)b0 * n * 4, w,
+                           static_cast<const char *>(x) + (size_t)b0 * k * 4, k, n, std::min(16, batch - b0), type);
+            if (!first) first = impl.route;
+        }
+        impl.route = first;
+        return;
+    }
+    if (gemm) {
         grow(id, ctx, impl.gemm_workspace, impl.gemm_workspace_size, kk_gemm_workspace_bytes(k, n, batch));
         detail::check_hip((hipError_t)kk_gemm((int)type, w, static_cast<const float *>(x), static_cast<float *>(y), k,
                                               n, batch, impl.gemm_workspace, ctx.stream, &impl.route),

@@ -21,6 +21,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdio>
 #include <mutex>
@@ -64,6 +65,32 @@ int too_large(size_t need) {
     return KUNLUN_NOALLOC_TOO_LARGE;
 }
 
+// kunlun_matmul's route for at most 16 columns (X 16-byte aligned or not),
+// with its scratch in the device's array
+hipError_t small_batch(DeviceScratch &d, int type, const void *w, const float *xf, float *yf, int k, int n, int batch,
+                       uintptr_t wa, hipStream_t s, const char **taken) {
+    const uintptr_t xa = reinterpret_cast<uintptr_t>(xf);
+    if ((type == 0 || type == 1) && kk::dense_mfma_batch(batch) && (wa & 15) == 0 && (xa & 15) == 0) {
+        *taken = type == 1 ? "f16_mfma_gemv" : "f32_mfma_gemv";
+        return static_cast<hipError_t>(kk_dense_mfma_gemv(type, w, xf, yf, k, n, batch, s));
+    }
+    if (type == 2 && kk::q4_stream_batch(batch) && kk_q4_stream_gemv_supported(w, xf, k, n, batch)) {
+        *taken = "q4_stream_gemv";
+        return static_cast<hipError_t>(kk_q4_stream_gemv(w, xf, yf, k, n, batch, d.cus, s));
+    }
+    if (type == 2 && kk::q4_bdiag_batch(batch) && kk_q4_bdiag_gemv_supported(w, xf, k, n, batch)) {
+        *taken = "q4_bdiag_gemv";
+        return static_cast<hipError_t>(kk_q4_bdiag_gemv(w, xf, yf, k, n, batch, d.cus, s));
+    }
+    if (type == 2 && kk::q4_mfma_batch(batch, k % 256 == 0 && (wa & 15) == 0) && k % 64 == 0 && (wa & 3) == 0) {
+        const size_t need = kk_q4_mfma_gemv_workspace_bytes(k);
+        if (need > kScratchBytes) return static_cast<hipError_t>(too_large(need));
+        *taken = "q4_mfma_gemv";
+        return static_cast<hipError_t>(kk_q4_mfma_gemv(w, xf, yf, k, n, batch, d.ptr, d.cus, s));
+    }
+    return static_cast<hipError_t>(kk_dense_matmul(type, w, xf, yf, k, n, batch, s, taken));
+}
+
 } // namespace
 
 extern "C" int kunlun_matmul_noalloc(int device, void *y, const void *w, const void *x, int k, int n, int batch,
@@ -93,27 +120,22 @@ extern "C" int kunlun_matmul_noalloc(int device, void *y, const void *w, const v
     float *yf = static_cast<float *>(y);
     const uintptr_t wa = reinterpret_cast<uintptr_t>(w), xa = reinterpret_cast<uintptr_t>(x);
     const char *taken = nullptr;
-    if ((type == 2 || (type == 1 && (wa & 15) == 0)) && batch >= kk::gemm_min_batch() && (xa & 15) == 0) {
+    const bool gemm = (type == 2 || (type == 1 && (wa & 15) == 0)) && batch >= kk::gemm_min_batch() && (xa & 15) == 0;
+    if (gemm) {
         const size_t need = kk_gemm_workspace_bytes(k, n, batch);
         if (need > kScratchBytes) return too_large(need);
         rc = static_cast<hipError_t>(kk_gemm(type, w, xf, yf, k, n, batch, d.ptr, s, &taken));
-    } else if ((type == 0 || type == 1) && kk::dense_mfma_batch(batch) && (wa & 15) == 0 && (xa & 15) == 0) {
-        rc = static_cast<hipError_t>(kk_dense_mfma_gemv(type, w, xf, yf, k, n, batch, s));
-        taken = type == 1 ? "f16_mfma_gemv" : "f32_mfma_gemv";
-    } else if (type == 2 && kk::q4_stream_batch(batch) && kk_q4_stream_gemv_supported(w, xf, k, n, batch)) {
-        rc = static_cast<hipError_t>(kk_q4_stream_gemv(w, xf, yf, k, n, batch, d.cus, s));
-        taken = "q4_stream_gemv";
-    } else if (type == 2 && kk::q4_bdiag_batch(batch) && kk_q4_bdiag_gemv_supported(w, xf, k, n, batch)) {
-        rc = static_cast<hipError_t>(kk_q4_bdiag_gemv(w, xf, yf, k, n, batch, d.cus, s));
-        taken = "q4_bdiag_gemv";
-    } else if (type == 2 && kk::q4_mfma_batch(batch, k % 256 == 0 && (wa & 15) == 0) && k % 64 == 0 &&
-               (wa & 3) == 0) {
-        const size_t need = kk_q4_mfma_gemv_workspace_bytes(k);
-        if (need > kScratchBytes) return too_large(need);
-        rc = static_cast<hipError_t>(kk_q4_mfma_gemv(w, xf, yf, k, n, batch, d.ptr, d.cus, s));
-        taken = "q4_mfma_gemv";
     } else {
-        rc = static_cast<hipError_t>(kk_dense_matmul(type, w, xf, yf, k, n, batch, s, &taken));
+        // kunlun_matmul's small-batch routes; above 16 columns, chunks of 16
+        // (as kunlun_matmul runs them), in stream order on the one array
+        for (int b0 = 0; b0 < batch && rc == hipSuccess; b0 += 16) {
+            const int bc = std::min(16, batch - b0);
+            const char *chunk_route = nullptr;
+            rc = small_batch(d, type, w, xf + static_cast<size_t>(b0) * k, yf + static_cast<size_t>(b0) * n, k, n, bc,
+                             wa, s, &chunk_route);
+            if (!taken) taken = chunk_route;
+        }
+        if (rc == static_cast<hipError_t>(KUNLUN_NOALLOC_TOO_LARGE)) return rc;
     }
     if (route) *route = taken;
     return rc;

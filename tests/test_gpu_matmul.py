@@ -133,6 +133,18 @@ def test_q4_misaligned_weights_use_general_kernel(gpu, oracle):
     assert route in ("q4_gemv_dot8", "q4_bdiag_gemv", "q4_mfma_gemv")
 
 
+# batches between the small-batch kernels (<= 16) and the GEMM (>= 64): chunks
+# of 16 columns, each on the small-batch route a 16-column call takes
+@pytest.mark.parametrize("type_", DENSE, ids=lambda t: TYPE_NAME[t])
+@pytest.mark.parametrize("k,n,batch", [(4096, 300, 33), (512, 130, 17), (1088, 65, 48)])
+def test_mid_batch_chunks(gpu, oracle, type_, k, n, batch):
+    seed = k + n + batch + int(type_)
+    w = gaussian((n, k), 0.02, seed)
+    x = gaussian((batch, k), 1.0, seed + 1)
+    _, route = _dense_case(oracle, type_, w, x, k, n, batch)
+    assert route in ("q4_stream_gemv", "q4_bdiag_gemv", "q4_mfma_gemv", "f16_mfma_gemv", "f32_mfma_gemv")
+
+
 def test_unaligned_activation_uses_general_kernel(gpu, oracle):
     k, n, batch = 1024, 129, 1
     w = gaussian((n, k), 0.02, 13)

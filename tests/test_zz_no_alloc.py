@@ -23,6 +23,7 @@ CASES = [
     (Q4, "q4_stream_gemv", (4096, 2048, 8), (4096, 300, 5)),      # streamed MFMA GEMV (K = 4096), no scratch
     (Q4, "q4_bdiag_gemv", (1024, 2048, 8), (1024, 300, 4)),       # block-diagonal MFMA GEMV, no scratch
     (Q4, "q4_mfma_gemv", (4096, 2048, 16), (4096, 300, 12)),      # LDS-staged MFMA GEMV, scratch: X fragments
+    (Q4, "q4_mfma_gemv", (4096, 520, 40), (4096, 300, 33)),       # chunks of 16 columns, the array reused in order
     (Q4, "q4_gemv_dot8", (4096, 1024, 1), (1024, 129, 1)),        # no scratch
     (F32, "f32_mfma_gemv", (1024, 256, 8), (512, 65, 2)),         # no scratch
 ]
