@@ -109,11 +109,14 @@ __device__ __forceinline__ int scale_offset(int q_groups, int steps, int step, i
 
 // Q = column groups of four (batch <= 4Q), SPW = steps per wave, ITEMS =
 // activation items per thread (4Q * steps * 32 items over the workgroup).
+// w2 (gate/up pair, else null): tile 2i holds rows 16i .. 16i + 15 of w (the
+// gate matrix), tile 2i + 1 the same rows of w2 (the up matrix); n is the
+// row count of each and the workgroup's tile count is even, so both tiles of
+// a pair meet in one workgroup, whose epilogue writes y = SiLU(gate) * up
+// ([batch][n], kk::swiglu_value).
 template <int Q, int SPW, int ITEMS>
-// w2 (gate/up pair, else null): rows n_split .. n - 1 are rows 0 .. of w2
-// (n = 2 n_split), so y = [batch][2 n_split], the w rows then the w2 rows.
 __global__ __launch_bounds__(kThreads) void q4_bdiag_gemv(const uint8_t *__restrict__ w,
-                                                        const uint8_t *__restrict__ w2, int n_split,
+                                                        const uint8_t *__restrict__ w2,
                                                         const float *__restrict__ x,
                                                         float *__restrict__ y, int k, int n, int batch, int steps,
                                                         int parts) {
@@ -126,7 +129,9 @@ __global__ __launch_bounds__(kThreads) void q4_bdiag_gemv(const uint8_t *__restr
     const int nl = lane & 15, h = lane >> 4;
     const int part = wid % parts;
     const int tile = blockIdx.x * (kWaves / parts) + wid / parts;
-    const int row = min(tile * kTileRows + nl, n - 1);
+    const bool second = w2 && (tile & 1);                       // wave-uniform: an up tile of the pair
+    const int row_tile = w2 ? tile >> 1 : tile;
+    const int row = min(row_tile * kTileRows + nl, n - 1);
     const int s_first = part * SPW;
 
     // 1. this thread's activation items (column b, pair p, block blk, dword
@@ -147,9 +152,7 @@ __global__ __launch_bounds__(kThreads) void q4_bdiag_gemv(const uint8_t *__restr
     uint32_t ring[SPW][9];
     auto load_step = [&](int j) {
         const int p = min(4 * (s_first + j) + h, pairs - 1);
-        const bool second = w2 && row >= n_split;
-        const uint32_t *src = reinterpret_cast<const uint32_t *>((second ? w2 : w) +
-                                                                 static_cast<size_t>(second ? row - n_split : row) * row_bytes +
+        const uint32_t *src = reinterpret_cast<const uint32_t *>((second ? w2 : w) + static_cast<size_t>(row) * row_bytes +
                                                                  static_cast<size_t>(p) * 36);
         const kk::u32x4_a4 a = kk::load_u32x4(src), c = kk::load_u32x4(src + 4);
         ring[j][0] = a.x; ring[j][1] = a.y; ring[j][2] = a.z; ring[j][3] = a.w;
@@ -273,12 +276,18 @@ __global__ __launch_bounds__(kThreads) void q4_bdiag_gemv(const uint8_t *__restr
         red[(q * kWaves + wid) * kWave + lane] = h == 0 ? acc[q][0] : h == 1 ? acc[q][1] : h == 2 ? acc[q][2] : acc[q][3];
     }
     __syncthreads();
-    if (part != 0) return;
-    const int out_row = tile * kTileRows + nl;
+    if (part != 0 || second) return;
+    const int out_row = row_tile * kTileRows + nl;
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
         float sum = 0.0f;
         for (int pp = 0; pp < parts; ++pp) sum += red[(q * kWaves + wid + pp) * kWave + lane];
+        if (w2) {
+            // the up tile's waves follow this tile's in the workgroup
+            float up = 0.0f;
+            for (int pp = 0; pp < parts; ++pp) up += red[(q * kWaves + wid + parts + pp) * kWave + lane];
+            sum = kk::swiglu_value(sum, up);
+        }
         if (out_row < n && 4 * q + h < batch) y[static_cast<size_t>(4 * q + h) * n + out_row] = sum;
     }
 }
@@ -340,16 +349,15 @@ extern "C" int kk_q4_bdiag_gemv_supported(const void *w, const float *x, int k, 
 namespace {
 hipError_t launch_bdiag(const void *w, const void *w2, const float *x, float *y, int k, int n, int batch, int cus,
                         hipStream_t stream) {
-    const int n_split = w2 ? n : 0;
-    if (w2) n *= 2;
     int device = 0;
     hipError_t rc = hipGetDevice(&device);
     if (rc != hipSuccess) return rc;
     const int q = (batch + 3) / 4;
-    const int tiles = (n + kTileRows - 1) / kTileRows;
+    const int tiles = (w2 ? 2 : 1) * ((n + kTileRows - 1) / kTileRows);
     BdPlan plan;
     const void *kernel = nullptr;
     for (int t : kTileChoices) {
+        if (w2 && t == 1) continue;                             // a pair's two tiles share a workgroup
         const BdPlan p = bdiag_candidate(k, batch, t);
         if (p.parts == 0) continue;
         const void *kp = bdiag_kernel_for(q, p);
@@ -363,8 +371,7 @@ hipError_t launch_bdiag(const void *w, const void *w2, const float *x, float *y,
     const int groups = (tiles + plan.tiles_per_group - 1) / plan.tiles_per_group;
     const uint8_t *wb = static_cast<const uint8_t *>(w);
     const uint8_t *wb2 = static_cast<const uint8_t *>(w2);
-    int split = n_split;
-    void *args[] = {&wb, &wb2, &split, &x, &y, &k, &n, &batch, &plan.steps, &plan.parts};
+    void *args[] = {&wb, &wb2, &x, &y, &k, &n, &batch, &plan.steps, &plan.parts};
     rc = hipLaunchKernel(kernel, dim3(groups), dim3(kThreads), args, plan.lds_bytes, stream);
     return rc != hipSuccess ? rc : hipGetLastError();
 }
@@ -377,11 +384,11 @@ extern "C" int kk_q4_bdiag_gemv(const void *w, const float *x, float *y, int k, 
 }
 
 // Gate/up pair: both matrices in one launch (X staged once per workgroup),
-// y = [batch][2n], the gate products then the up products of each row.
-extern "C" int kk_q4_bdiag_gemv_pair(const void *w_gate, const void *w_up, const float *x, float *y, int k, int n,
-                                     int batch, int cus, hipStream_t stream) {
+// y = [batch][n] = SiLU(X w_gate^T) * (X w_up^T).
+extern "C" int kk_q4_bdiag_gemv_pair_swiglu(const void *w_gate, const void *w_up, const float *x, float *y, int k,
+                                            int n, int batch, int cus, hipStream_t stream) {
     if (!kk_q4_bdiag_gemv_supported(w_gate, x, k, n, batch) || !kk_q4_bdiag_gemv_supported(w_up, x, k, n, batch) ||
-        !y || cus <= 0 || n > (1 << 29))
+        !w_up || !y || cus <= 0 || n > (1 << 29))
         return hipErrorInvalidValue;
     return launch_bdiag(w_gate, w_up, x, y, k, n, batch, cus, stream);
 }

@@ -49,6 +49,14 @@ size_t kk_q4_mfma_gemv_workspace_bytes(int k);
 int kk_q4_mfma_gemv(const void *w, const float *x, float *y, int k, int n, int batch, void *workspace, int cus,
                     hipStream_t stream);
 
+// The gate/up pair on the LDS-staged Q4_0 MFMA GEMV (K % 512 == 0, 16-byte
+// aligned weights and X, batch <= 16): one activation prepass into
+// `workspace` (kk_q4_mfma_gemv_workspace_bytes), then both products with
+// SwiGLU in the epilogue: y = [batch][n] = SiLU(X w_gate^T) * (X w_up^T).
+int kk_q4_mfma_pair_swiglu_supported(const void *w_gate, const void *w_up, const float *x, int k, int n, int batch);
+int kk_q4_mfma_gemv_pair_swiglu(const void *w_gate, const void *w_up, const float *x, float *y, int k, int n,
+                                int batch, void *workspace, hipStream_t stream);
+
 // Q4_0 GEMV for batch 1..16 on fp16 MFMA with block-diagonal activation
 // operands (one pass over W, lanes streaming whole block pairs, no
 // workspace): K % 64 == 0, 4-byte aligned weights, 16-byte aligned X, and
@@ -56,18 +64,20 @@ int kk_q4_mfma_gemv(const void *w, const float *x, float *y, int k, int n, int b
 // ceil(batch/4) x 4480 bytes <= 160 KiB); `cus` sizes the grid.
 int kk_q4_bdiag_gemv_supported(const void *w, const float *x, int k, int n, int batch);
 int kk_q4_bdiag_gemv(const void *w, const float *x, float *y, int k, int n, int batch, int cus, hipStream_t stream);
-// The gate/up pair in one launch: y = [batch][2n] (gate products, then up).
-int kk_q4_bdiag_gemv_pair(const void *w_gate, const void *w_up, const float *x, float *y, int k, int n, int batch,
-                          int cus, hipStream_t stream);
+// The gate/up pair in one launch, SwiGLU in its epilogue: y = [batch][n] =
+// SiLU(X w_gate^T) * (X w_up^T) (kk::swiglu_value).
+int kk_q4_bdiag_gemv_pair_swiglu(const void *w_gate, const void *w_up, const float *x, float *y, int k, int n,
+                                 int batch, int cus, hipStream_t stream);
 
 // Q4_0 GEMV for batch 1..8 at K = 4096 on fp16 MFMA, one pass over W with
 // weight rows streamed through per-wave LDS (no workspace): 16-byte aligned
 // weights and X; `cus` sizes the grid.
 int kk_q4_stream_gemv_supported(const void *w, const float *x, int k, int n, int batch);
 int kk_q4_stream_gemv(const void *w, const float *x, float *y, int k, int n, int batch, int cus, hipStream_t stream);
-// The gate/up pair in one launch: y = [batch][2n] (gate products, then up).
-int kk_q4_stream_gemv_pair(const void *w_gate, const void *w_up, const float *x, float *y, int k, int n, int batch,
-                           int cus, hipStream_t stream);
+// The gate/up pair in one launch, SwiGLU in its epilogue: y = [batch][n] =
+// SiLU(X w_gate^T) * (X w_up^T) (kk::swiglu_value).
+int kk_q4_stream_gemv_pair_swiglu(const void *w_gate, const void *w_up, const float *x, float *y, int k, int n,
+                                  int batch, int cus, hipStream_t stream);
 
 // F32 (type 0) / F16 (type 1) GEMV for batch 1..16 on fp32 MFMA, one pass over
 // W; 16-byte aligned weights and activations.

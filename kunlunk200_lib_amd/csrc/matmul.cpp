@@ -267,24 +267,31 @@ void matmul_swiglu(Kernel & kernel, int id, void * y, const void * w_gate, const
                 (kk::q4_bdiag_batch(batch) &&
                  kk_q4_bdiag_gemv_supported(w_gate, static_cast<const float *>(x), k, n, batch) &&
                  kk_q4_bdiag_gemv_supported(w_up, static_cast<const float *>(x), k, n, batch)))) {
-        // small batch: both products in one launch into [batch][2n] (each row's
-        // gate values, then its up values), then SwiGLU
-        grow(id, ctx, impl.pair_workspace, impl.pair_workspace_size, (size_t)batch * n * 8);
-        float * stacked = static_cast<float *>(impl.pair_workspace);
+        // small batch: both products and SwiGLU in one launch
         const bool streamed = kk::q4_stream_batch(batch) &&
                               kk_q4_stream_gemv_supported(w_gate, static_cast<const float *>(x), k, n, batch) &&
                               kk_q4_stream_gemv_supported(w_up, static_cast<const float *>(x), k, n, batch);
         if (streamed)
-            detail::check_hip((hipError_t)kk_q4_stream_gemv_pair(w_gate, w_up, static_cast<const float *>(x), stacked,
-                                                                 k, n, batch, ctx.cus, ctx.stream),
-                              "kk_q4_stream_gemv_pair");
+            detail::check_hip((hipError_t)kk_q4_stream_gemv_pair_swiglu(w_gate, w_up, static_cast<const float *>(x),
+                                                                        static_cast<float *>(y), k, n, batch, ctx.cus,
+                                                                        ctx.stream),
+                              "kk_q4_stream_gemv_pair_swiglu");
         else
-            detail::check_hip((hipError_t)kk_q4_bdiag_gemv_pair(w_gate, w_up, static_cast<const float *>(x), stacked,
-                                                                k, n, batch, ctx.cus, ctx.stream),
-                              "kk_q4_bdiag_gemv_pair");
-        detail::check_hip((hipError_t)kk_swiglu(y, stacked, stacked + n, n, batch, n * 8, n * 8, n * 4, 4, ctx.stream),
-                          "kk_swiglu");
+            detail::check_hip((hipError_t)kk_q4_bdiag_gemv_pair_swiglu(w_gate, w_up, static_cast<const float *>(x),
+                                                                       static_cast<float *>(y), k, n, batch, ctx.cus,
+                                                                       ctx.stream),
+                              "kk_q4_bdiag_gemv_pair_swiglu");
         impl.route = streamed ? "q4_stream_pair_swiglu" : "q4_bdiag_pair_swiglu";
+    } else if (type == WeightType::q4_0 && q4_mfma_batch(batch, true) &&
+               kk_q4_mfma_pair_swiglu_supported(w_gate, w_up, static_cast<const float *>(x), k, n, batch)) {
+        // the LDS-staged MFMA GEMV: one activation prepass, both products and
+        // SwiGLU in one launch
+        grow(id, ctx, impl.gemm_workspace, impl.gemm_workspace_size, kk_q4_mfma_gemv_workspace_bytes(k));
+        detail::check_hip((hipError_t)kk_q4_mfma_gemv_pair_swiglu(w_gate, w_up, static_cast<const float *>(x),
+                                                                  static_cast<float *>(y), k, n, batch,
+                                                                  impl.gemm_workspace, ctx.stream),
+                          "kk_q4_mfma_gemv_pair_swiglu");
+        impl.route = "q4_mfma_pair_swiglu";
     } else {
         // gate and up rows side by side in the workspace: [batch][2n] F32
         const size_t half = (size_t)batch * n * 4;

@@ -377,8 +377,11 @@ __device__ __forceinline__ uint32_t lg_and_or(uint32_t a, uint32_t mask, uint32_
 // (those below BCopies). (A separate function: the host pass rejects a
 // kernel-local lambda that hands captured values to these builtins, and then
 // drops the launch stub.)
-template <int SB, bool PACKED>
+// PAIR: copies below BCopies / 2 come from w_tile (the gate rows), the rest
+// from w2_tile (the up rows; b_off relative to it).
+template <int SB, bool PACKED, bool PAIR>
 __device__ __forceinline__ void lg_copy_stage(const uint8_t *frag, int frag_bytes, uint8_t *w_tile, int w_extent,
+                                              uint8_t *w2_tile, int w2_extent,
                                               const uint32_t (&b_off)[LgShape<SB, PACKED>::BCopiesPerWave], int wid,
                                               int lane, int s) {
     using L = LgShape<SB, PACKED>;
@@ -393,19 +396,34 @@ __device__ __forceinline__ void lg_copy_stage(const uint8_t *frag, int frag_byte
         __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, buf + (wid + 8 * t) * 1024, 16,
                                                  (wid + 8 * t) * 1024 + lane * 16, s * L::AStageBytes, 0, 0);
 #pragma unroll
-    for (int t = 0; t < L::BCopiesPerWave; ++t)
-        if (wid + 8 * t < L::BCopies)                           // wave-uniform
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, buf + L::AStageBytes + (wid + 8 * t) * 1024, 16,
-                                                     b_off[t], s * L::RowStage, 0, 2);   // non-temporal: read once
+    for (int t = 0; t < L::BCopiesPerWave; ++t) {
+        const int copy = wid + 8 * t;                           // wave-uniform
+        if (copy >= L::BCopies) continue;
+        if (PAIR && copy >= L::BCopies / 2) {
+            const __amdgpu_buffer_rsrc_t b2_rsrc = __builtin_amdgcn_make_buffer_rsrc(w2_tile, 0, w2_extent, 0x00020000);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(b2_rsrc, buf + L::AStageBytes + copy * 1024, 16, b_off[t],
+                                                     s * L::RowStage, 0, 2);
+        } else {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, buf + L::AStageBytes + copy * 1024, 16, b_off[t],
+                                                     s * L::RowStage, 0, 2);   // non-temporal: read once
+        }
+    }
 }
 
-template <int SB, bool PACKED>
+// PAIR (w2 the up matrix; SB = 16, so each weight copy lies in one half):
+// the workgroup's rows 0..31 are rows 32i .. 32i + 31 of w (the gate
+// matrix), rows 32..63 the same rows of w2, and y = SiLU(gate) * up
+// ([batch][n], kk::swiglu_value) from the gate tiles' waves.
+template <int SB, bool PACKED, bool PAIR = false>
 __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restrict__ w,
+                                                         const uint8_t *__restrict__ w2,
                                                          const _Float16 *__restrict__ frag,
                                                          const float *__restrict__ row_inv, float *__restrict__ y,
                                                          int n, int batch, int stages, uint32_t row_bytes,
                                                          int tiles, int tiles_per_xcd) {
     using L = LgShape<SB, PACKED>;
+    static_assert(!PAIR || (L::BCopies % 2 == 0 && (L::BCopies / 2) * 64 == (kLgRows / 2) * (L::RowStage / 16)),
+                  "a pair's weight copies split at the half");
     extern __shared__ __align__(16) uint8_t lg_lds[];
     const int bid = blockIdx.x;
     const int tile = (bid % 8) * tiles_per_xcd + bid / 8;       // contiguous row ranges per XCD
@@ -414,19 +432,22 @@ __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restr
     const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
     const int kh = wid >> 2, wt = wid & 3;
     const int g = lane >> 4, c16 = lane & 15;
-    const int n0 = tile * kLgRows;
+    constexpr int kOutRows = PAIR ? kLgRows / 2 : kLgRows;      // output rows per workgroup
+    const int n0 = tile * kOutRows;
 
     // weight copy i: 16-byte chunks 64i .. 64i+63 of the stage's [row][RowStage]
     // bytes; rows past n repeat row n - 1 and are never stored
     constexpr int kChunks = L::RowStage / 16;                   // per row: 9 / 18
-    const int w_extent = min(kLgRows, n - n0) * static_cast<int>(row_bytes);
+    const int w_extent = min(kOutRows, n - n0) * static_cast<int>(row_bytes);
     uint8_t *const w_tile = const_cast<uint8_t *>(w + static_cast<size_t>(n0) * row_bytes);
+    uint8_t *const w2_tile = PAIR ? const_cast<uint8_t *>(w2 + static_cast<size_t>(n0) * row_bytes) : nullptr;
     uint32_t b_off[L::BCopiesPerWave];
 #pragma unroll
     for (int t = 0; t < L::BCopiesPerWave; ++t) {
         const int q = min(wid + 8 * t, L::BCopies - 1) * 64 + lane;
         const int row = q / kChunks, chunk = q - (q / kChunks) * kChunks;
-        b_off[t] = static_cast<uint32_t>(min(n0 + row, n - 1) - n0) * row_bytes + 16 * chunk;
+        const int mrow = PAIR ? row % kOutRows : row;           // row of its own matrix's tile
+        b_off[t] = static_cast<uint32_t>(min(n0 + mrow, n - 1) - n0) * row_bytes + 16 * chunk;
     }
     const int frag_bytes = stages * L::AStageBytes;
     const uint8_t *fbytes = reinterpret_cast<const uint8_t *>(frag);
@@ -446,12 +467,13 @@ __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restr
     // s+1 .. min(s+Slots-2, stages-1) may still be in flight.
     const int ahead0 = min(L::Slots - 1, stages);
     for (int s = 0; s < ahead0; ++s)
-        lg_copy_stage<SB, PACKED>(fbytes, frag_bytes, w_tile, w_extent, b_off, wid, lane, s);
+        lg_copy_stage<SB, PACKED, PAIR>(fbytes, frag_bytes, w_tile, w_extent, w2_tile, w_extent, b_off, wid, lane, s);
     for (int s = 0; s < stages; ++s) {
         wait_vmcnt_dyn(my_copies * min(L::Slots - 2, stages - 1 - s));
         lds_barrier();
         if (s + L::Slots - 1 < stages)
-            lg_copy_stage<SB, PACKED>(fbytes, frag_bytes, w_tile, w_extent, b_off, wid, lane, s + L::Slots - 1);
+            lg_copy_stage<SB, PACKED, PAIR>(fbytes, frag_bytes, w_tile, w_extent, w2_tile, w_extent, b_off, wid, lane,
+                                            s + L::Slots - 1);
         const uint8_t *abuf = lg_lds + (s % L::Slots) * L::StageBytes;
         const uint8_t *brow = abuf + L::AStageBytes + (wt * 16 + c16) * L::RowStage;
         uint32_t qs[L::WaveBlocks], d16[L::WaveBlocks];
@@ -503,14 +525,33 @@ __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restr
     float4v *xfer = reinterpret_cast<float4v *>(lg_lds);
     if (kh == 1) xfer[wt * kWave + lane] = acc;
     __syncthreads();
-    if (kh == 1) return;
+    if (!PAIR && kh == 1) return;
     acc += xfer[wt * kWave + lane];
     if constexpr (PACKED) {
         // D rows 8..15 (lanes 32..63) are the lo parts of batch rows 0..7
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[r] += __shfl_down(acc[r], 32);
-        if (g >= 2) return;
     }
+    if constexpr (PAIR) {
+        // the up tiles (waves 2, 3 of k-group 0) hand their sums to the gate
+        // tiles (waves 0, 1) through LDS; every wave takes part in the barrier
+        float4v *upx = xfer + 4 * kWave;
+        if (kh == 0 && wt >= 2) upx[(wt - 2) * kWave + lane] = acc;
+        __syncthreads();
+        if (kh == 1 || wt >= 2 || (PACKED && g >= 2)) return;
+        const float4v up = upx[wt * kWave + lane];
+        const int rr = n0 + wt * 16 + c16;
+        if (rr < n) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = 4 * g + r;
+                if (m < batch)
+                    y[static_cast<size_t>(m) * n + rr] = kk::swiglu_value(acc[r] * row_inv[m], up[r] * row_inv[m]);
+            }
+        }
+        return;
+    }
+    if (PACKED && g >= 2) return;
     // D reg r of lane (c16, g): batch row 4g + r, weight row n0 + 16 wt + c16
     const int rr = n0 + wt * 16 + c16;
     if (rr < n) {
@@ -524,16 +565,17 @@ __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restr
 
 // Launch q4_lds_gemv<SB> (dynamic LDS above 64 KiB opted into once per
 // device).
-template <int SB, bool PACKED>
-hipError_t launch_lds_gemv(const uint8_t *w, const _Float16 *frag, const float *row_inv, float *y, int k, int n,
-                           int batch, hipStream_t stream) {
+template <int SB, bool PACKED, bool PAIR = false>
+hipError_t launch_lds_gemv(const uint8_t *w, const uint8_t *w2, const _Float16 *frag, const float *row_inv, float *y,
+                           int k, int n, int batch, hipStream_t stream) {
     using L = LgShape<SB, PACKED>;
-    const hipError_t rc = kk::opt_in_lds(reinterpret_cast<const void *>(&q4_lds_gemv<SB, PACKED>), L::LdsBytes);
+    const hipError_t rc = kk::opt_in_lds(reinterpret_cast<const void *>(&q4_lds_gemv<SB, PACKED, PAIR>), L::LdsBytes);
     if (rc != hipSuccess) return rc;
-    const int tiles = (n + kLgRows - 1) / kLgRows;
+    const int out_rows = PAIR ? kLgRows / 2 : kLgRows;
+    const int tiles = (n + out_rows - 1) / out_rows;
     const int tiles_per_xcd = (tiles + 7) / 8;
-    hipLaunchKernelGGL((q4_lds_gemv<SB, PACKED>), dim3(tiles_per_xcd * 8), dim3(kLgThreads), L::LdsBytes, stream, w, frag,
-                       row_inv, y, n, batch, k / (SB * 32), static_cast<uint32_t>(k / 32 * 18), tiles,
+    hipLaunchKernelGGL((q4_lds_gemv<SB, PACKED, PAIR>), dim3(tiles_per_xcd * 8), dim3(kLgThreads), L::LdsBytes, stream,
+                       w, w2, frag, row_inv, y, n, batch, k / (SB * 32), static_cast<uint32_t>(k / 32 * 18), tiles,
                        tiles_per_xcd);
     return hipGetLastError();
 }
@@ -571,16 +613,47 @@ extern "C" int kk_q4_mfma_gemv(const void *w, const float *x, float *y, int k, i
     if (streamed) {
         const uint8_t *wb = static_cast<const uint8_t *>(w);
         if (k % 512 == 0)
-            return packed ? launch_lds_gemv<16, true>(wb, frag, row_inv, y, k, n, batch, stream)
-                          : launch_lds_gemv<16, false>(wb, frag, row_inv, y, k, n, batch, stream);
-        return packed ? launch_lds_gemv<8, true>(wb, frag, row_inv, y, k, n, batch, stream)
-                      : launch_lds_gemv<8, false>(wb, frag, row_inv, y, k, n, batch, stream);
+            return packed ? launch_lds_gemv<16, true>(wb, nullptr, frag, row_inv, y, k, n, batch, stream)
+                          : launch_lds_gemv<16, false>(wb, nullptr, frag, row_inv, y, k, n, batch, stream);
+        return packed ? launch_lds_gemv<8, true>(wb, nullptr, frag, row_inv, y, k, n, batch, stream)
+                      : launch_lds_gemv<8, false>(wb, nullptr, frag, row_inv, y, k, n, batch, stream);
     }
     const int tiles = (n + kTileRows - 1) / kTileRows;
     const int groups = std::max(1, std::min((tiles + kWaves - 1) / kWaves, cus));
     hipLaunchKernelGGL(q4_mfma_gemv, dim3(groups), dim3(kThreads), kLdsBytes, stream, static_cast<const uint8_t *>(w),
                        frag, row_inv, y, k, n, batch, tiles);
     return hipGetLastError();
+}
+
+// Gate/up pair on the streamed kernel at K % 512 == 0 (16-byte aligned weights
+// and X): one prepass, then both products and SwiGLU in one launch.
+extern "C" int kk_q4_mfma_pair_swiglu_supported(const void *w_gate, const void *w_up, const float *x, int k, int n,
+                                                int batch) {
+    return w_gate && w_up && x && k > 0 && k % 512 == 0 && k <= 16384 && n >= 1 && batch >= 1 &&
+           batch <= kBatchRows && (reinterpret_cast<uintptr_t>(w_gate) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(w_up) & 15) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+}
+
+extern "C" int kk_q4_mfma_gemv_pair_swiglu(const void *w_gate, const void *w_up, const float *x, float *y, int k,
+                                           int n, int batch, void *workspace, hipStream_t stream) {
+    if (!kk_q4_mfma_pair_swiglu_supported(w_gate, w_up, x, k, n, batch) || !y || !workspace)
+        return hipErrorInvalidValue;
+    const int blocks_pad = ((k >> 5) + kChunkBlocks - 1) / kChunkBlocks * kChunkBlocks;
+    _Float16 *frag = static_cast<_Float16 *>(workspace);
+    float *row_inv = reinterpret_cast<float *>(static_cast<char *>(workspace) +
+                                               static_cast<size_t>(blocks_pad) * kFragBlockBytes);
+    const bool packed = batch <= kBatchRows / 2;
+    if (packed)
+        hipLaunchKernelGGL(x_to_frag<true>, dim3(kBatchRows / 2), dim3(kPrepassThreads), 0, stream, x, batch, k,
+                           blocks_pad, frag, row_inv);
+    else
+        hipLaunchKernelGGL(x_to_frag<false>, dim3(kBatchRows), dim3(kPrepassThreads), 0, stream, x, batch, k,
+                           blocks_pad, frag, row_inv);
+    const hipError_t rc = hipGetLastError();
+    if (rc != hipSuccess) return rc;
+    const uint8_t *wg = static_cast<const uint8_t *>(w_gate), *wu = static_cast<const uint8_t *>(w_up);
+    return packed ? launch_lds_gemv<16, true, true>(wg, wu, frag, row_inv, y, k, n, batch, stream)
+                  : launch_lds_gemv<16, false, true>(wg, wu, frag, row_inv, y, k, n, batch, stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -78,8 +78,9 @@ __device__ __forceinline__ uint32_t from_partner(uint32_t old, uint32_t src) {
         __builtin_amdgcn_update_dpp(static_cast<int>(old), static_cast<int>(src), kXor8, 0xf, BANKS, false));
 }
 
-// w2 (gate/up pair, else null): tiles T .. 2T - 1 (T = ceil(n / 32)) are the
-// tiles of w2, and y is [batch][2n]: the w rows' products, then the w2 rows'.
+// w2 (gate/up pair, else null): tile i holds rows 16i .. 16i + 15 of w (the
+// gate matrix) as its rows 0..15 and the same rows of w2 (the up matrix) as
+// rows 16..31, and y = SiLU(gate) * up ([batch][n], kk::swiglu_value).
 __global__ __launch_bounds__(kWave * kWaves) void q4_stream_gemv(const uint8_t *__restrict__ w,
                                                                const uint8_t *__restrict__ w2,
                                                                const float *__restrict__ x, float *__restrict__ y,
@@ -88,8 +89,8 @@ __global__ __launch_bounds__(kWave * kWaves) void q4_stream_gemv(const uint8_t *
     const int lane = threadIdx.x & (kWave - 1);
     const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
     const int r16 = lane & 15, g = lane >> 4;
-    const int mtiles = (n + kTileRows - 1) / kTileRows;          // tiles per matrix
-    const int tiles = w2 ? 2 * mtiles : mtiles;
+    const int tile_out = w2 ? kTileRows / 2 : kTileRows;         // output rows per tile
+    const int tiles = (n + tile_out - 1) / tile_out;
     const int tile0 = blockIdx.x * tiles_per_group;
     const int c = wid;                                            // this wave's K chunk
     uint8_t *stage = lds + wid * kStageBytes;
@@ -108,12 +109,11 @@ __global__ __launch_bounds__(kWave * kWaves) void q4_stream_gemv(const uint8_t *
     // 2. the first two tiles' pieces (issued after X: the memory counter is in order)
     __builtin_amdgcn_sched_barrier(0);
     const size_t total = static_cast<size_t>(n) * kRowBytes;
-    auto tile_buffer = [&](int t) {
-        const int gt = tile0 + t;
-        const bool second = w2 && gt >= mtiles;                   // wave-uniform
-        const size_t off = min(static_cast<size_t>(second ? gt - mtiles : gt) * kTileRows * kRowBytes, total);
-        const uint32_t extent = static_cast<uint32_t>(min(total - off, static_cast<size_t>(0xfffffff0u)));
-        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>((second ? w2 : w) + off), 0, extent, 0x00020000);
+    // rows [row0, row0 + rows) of `base`, the ones past n reading as zero
+    auto rows_buffer = [&](const uint8_t *base, size_t row0, size_t rows) {
+        const size_t off = min(row0 * kRowBytes, total);
+        const uint32_t extent = static_cast<uint32_t>(min(min(total - off, rows * kRowBytes), static_cast<size_t>(0xfffffff0u)));
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base + off), 0, extent, 0x00020000);
     };
     uint32_t goff[kPiecesPerLane], loff[kPiecesPerLane];   // piece offsets in the tile and in the stage
 #pragma unroll
@@ -122,9 +122,22 @@ __global__ __launch_bounds__(kWave * kWaves) void q4_stream_gemv(const uint8_t *
         goff[i] = static_cast<uint32_t>(row * kRowBytes + c * kChunkBytes + piece * 16);
         loff[i] = static_cast<uint32_t>(row * kStageStride + piece * 16);
     }
+    auto load_at = [&](__amdgpu_buffer_rsrc_t rsrc, uint32_t off) {
+        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(off), 0, 2));
+    };
+    // pair tiles: pieces 0..255 are gate rows 0..13, 288..575 up rows 16..31;
+    // load 4 (pieces 256..319) spans both: each half's lanes read the other
+    // matrix's buffer out of bounds (zero) and the two loads are or-ed
+    constexpr uint32_t kOutOfBounds = 0x7ffffff0u;
+    constexpr uint32_t kUpHalf = (kTileRows / 2) * kRowBytes;
     auto load = [&](int t, int i) {
-        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(tile_buffer(t),
-                                                                              static_cast<int>(goff[i]), 0, 2));
+        if (!w2) return load_at(rows_buffer(w, static_cast<size_t>(tile0 + t) * kTileRows, kTileRows), goff[i]);
+        const size_t row0 = static_cast<size_t>(tile0 + t) * (kTileRows / 2);
+        if (i * kWave + kWave <= kTileRows / 2 * 18) return load_at(rows_buffer(w, row0, kTileRows / 2), goff[i]);
+        if (i * kWave >= kTileRows / 2 * 18) return load_at(rows_buffer(w2, row0, kTileRows / 2), goff[i] - kUpHalf);
+        const bool up = i * kWave + lane >= kTileRows / 2 * 18;
+        return load_at(rows_buffer(w, row0, kTileRows / 2), up ? kOutOfBounds : goff[i]) |
+               load_at(rows_buffer(w2, row0, kTileRows / 2), up ? goff[i] - kUpHalf : kOutOfBounds);
     };
     u32x4 ring_a[kPiecesPerLane], ring_b[kPiecesPerLane];
 #pragma unroll
@@ -269,18 +282,23 @@ __global__ __launch_bounds__(kWave * kWaves) void q4_stream_gemv(const uint8_t *
         }
     }
     __syncthreads();
-    // 5. column m, row 32 t + 16 rg + nn: lane (nn, m / 4) element m % 4 of every wave
-    for (int idx = threadIdx.x; idx < tiles_per_group * 256; idx += kWave * kWaves) {
-        const int t = idx >> 8, rg = (idx >> 7) & 1, m = (idx >> 4) & 7, nn = idx & 15;
-        const int gt = tile0 + t;
-        const bool second = w2 && gt >= mtiles;
-        const int out_row = (second ? gt - mtiles : gt) * kTileRows + rg * 16 + nn;
-        if (m >= batch || gt >= tiles || out_row >= n) continue;
+    // 5. column m, tile row 16 rg + nn: lane (nn, m / 4) element m % 4 of every
+    //    wave, added in wave order (pair tiles: rg 0 the gate row, rg 1 the up row)
+    auto row_sum = [&](int t, int rg, int m, int nn) {
         const int src = (m >> 2) * 16 + nn;
         float sum = 0.0f;
 #pragma unroll
         for (int ww = 0; ww < kWaves; ++ww) sum += partial[((t * 2 + rg) * kWaves + ww) * 32 + src][m & 3];
-        y[static_cast<size_t>(m) * (w2 ? 2 * n : n) + (second ? n : 0) + out_row] = sum;
+        return sum;
+    };
+    const int per_tile = w2 ? 128 : 256;
+    for (int idx = threadIdx.x; idx < tiles_per_group * per_tile; idx += kWave * kWaves) {
+        const int t = idx / per_tile, rg = w2 ? 0 : (idx >> 7) & 1, m = (idx >> 4) & 7, nn = idx & 15;
+        const int gt = tile0 + t;
+        const int out_row = gt * tile_out + rg * 16 + nn;
+        if (m >= batch || gt >= tiles || out_row >= n) continue;
+        const float v = w2 ? kk::swiglu_value(row_sum(t, 0, m, nn), row_sum(t, 1, m, nn)) : row_sum(t, rg, m, nn);
+        y[static_cast<size_t>(m) * n + out_row] = v;
     }
 }
 
@@ -297,7 +315,8 @@ hipError_t launch_stream(const void *w, const void *w2, const float *x, float *y
                          hipStream_t stream) {
     const hipError_t rc = kk::opt_in_lds(reinterpret_cast<const void *>(&q4_stream_gemv), kLdsBytes);
     if (rc != hipSuccess) return rc;
-    const int tiles = (w2 ? 2 : 1) * ((n + kTileRows - 1) / kTileRows);
+    const int tile_out = w2 ? kTileRows / 2 : kTileRows;     // a pair tile: 16 gate and 16 up rows
+    const int tiles = (n + tile_out - 1) / tile_out;
     const int t = std::max(1, std::min(kMaxTiles, (tiles + cus - 1) / cus));
     hipLaunchKernelGGL(q4_stream_gemv, dim3((tiles + t - 1) / t), dim3(kWave * kWaves), kLdsBytes, stream,
                        static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(w2), x, y, n, batch, t);
@@ -312,9 +331,9 @@ extern "C" int kk_q4_stream_gemv(const void *w, const float *x, float *y, int k,
 }
 
 // Gate/up pair: both matrices in one launch (X read once per workgroup),
-// y = [batch][2n], the gate products then the up products of each row.
-extern "C" int kk_q4_stream_gemv_pair(const void *w_gate, const void *w_up, const float *x, float *y, int k, int n,
-                                      int batch, int cus, hipStream_t stream) {
+// y = [batch][n] = SiLU(X w_gate^T) * (X w_up^T).
+extern "C" int kk_q4_stream_gemv_pair_swiglu(const void *w_gate, const void *w_up, const float *x, float *y, int k,
+                                             int n, int batch, int cus, hipStream_t stream) {
     if (!kk_q4_stream_gemv_supported(w_gate, x, k, n, batch) || !kk_q4_stream_gemv_supported(w_up, x, k, n, batch) ||
         !y || cus <= 0)
         return hipErrorInvalidValue;

@@ -269,6 +269,21 @@ def test_rowwise_i8_large_activation_path(gpu, oracle):
     assert np.array_equal(y.view(np.uint32), expect.view(np.uint32))
 
 
+@pytest.mark.parametrize("k,n,batch", [(4096, 64, 300), (4096, 48, 600), (16384, 32, 300), (2080, 40, 1009)])
+def test_rowwise_i8_quantizer_pass_shapes(gpu, oracle, k, n, batch):
+    # the three passes at 2 and 4 float4 groups per thread (X above 1M and 2M
+    # values), their grid-stride loop (above 4M values) and a grid whose last
+    # workgroup is partial (2080 * 1009 values); the outliers that set max0
+    # sit in the last group and in the middle
+    w = gaussian((n, k), 0.02, k + n + batch)
+    x = gaussian((batch, k), 1.0, k + n + batch + 1)
+    x[batch - 1, k - 1] = -23.5
+    x[batch // 2, 5] = 19.0
+    y, _, guard_ok = run_matmul(kl.WeightType.rowwise_i8, None, x, k, n, batch, w_f32=w)
+    assert guard_ok
+    assert np.array_equal(y.view(np.uint32), oracle.rowwise_i8_matmul(w, x).view(np.uint32))
+
+
 @pytest.mark.parametrize("k,batch", [(64, 1), (4096, 20)])
 def test_rowwise_i8_nonfinite_activation_aborts_at_wait(gpu, k, batch):
     # reference src/k200.cpp:213 aborts on a non-finite activation; here the

@@ -338,8 +338,8 @@ def test_matmul_swiglu_decode_pair_fused(gpu, oracle, knobs, k, n, batch, inf):
 
 
 def test_matmul_swiglu_decode_pair_routes(gpu, oracle):
-    # batch 1 fuses SiLU * up into the GEMV; batch 3 runs both products in one
-    # block-diagonal launch, then swiglu
+    # batch 1 fuses SiLU * up into the GEMV; batch 3 runs both products and
+    # SiLU * up in one block-diagonal launch
     k, n = 512, 96
     wg = gaussian((n, k), 0.02, 71)
     wu = gaussian((n, k), 0.02, 72)
@@ -353,15 +353,16 @@ def test_matmul_swiglu_decode_pair_routes(gpu, oracle):
         assert finite and ok, worst
 
 
-# Small-batch pairs in one launch: the gate and up rows stacked as one matrix
-# of 2n rows (n = 300: the streamed kernel's 32-row tiles and the
-# block-diagonal kernel's 16-row tiles end inside the gate matrix). Batch 16
-# at K 4096 fits neither kernel and stays on two GEMVs plus swiglu.
-@pytest.mark.parametrize("batch,route", [(3, "q4_bdiag_pair_swiglu"), (4, "q4_bdiag_pair_swiglu"),
-                                         (5, "q4_stream_pair_swiglu"), (8, "q4_stream_pair_swiglu"),
-                                         (16, "q4_gemv_pair_swiglu")])
-def test_matmul_swiglu_small_batch_one_launch(gpu, oracle, batch, route):
-    k, n = 4096, 300
+# Small-batch pairs in one launch with SiLU * up in the epilogue: a tile (or
+# pair of tiles) holds the same rows of the gate and the up matrix (n = 300:
+# the last tile ends inside both). Batch 9..16 at K 4096, and batch 8 at K
+# 8192, take the LDS-staged kernel after one activation prepass.
+@pytest.mark.parametrize("batch,k,route", [(3, 4096, "q4_bdiag_pair_swiglu"), (4, 4096, "q4_bdiag_pair_swiglu"),
+                                           (5, 4096, "q4_stream_pair_swiglu"), (8, 4096, "q4_stream_pair_swiglu"),
+                                           (12, 4096, "q4_mfma_pair_swiglu"), (16, 4096, "q4_mfma_pair_swiglu"),
+                                           (8, 8192, "q4_mfma_pair_swiglu"), (16, 2560, "q4_mfma_pair_swiglu")])
+def test_matmul_swiglu_small_batch_one_launch(gpu, oracle, batch, k, route):
+    n = 300
     wg = gaussian((n, k), 0.02, 81)
     wu = gaussian((n, k), 0.02, 82)
     pg, dg = weight_payload(kl.WeightType.q4_0, wg, oracle)
@@ -389,3 +390,29 @@ def test_matmul_swiglu_tile_variants(gpu, oracle, knobs, tile):
     print(f"  pair tile {tile} worst/bound={worst:.3g}", flush=True)
     assert route == "q4_gemm_swiglu_mfma"
     assert finite and ok
+
+
+# The fused small-batch pairs whose per-row arithmetic is the single-matrix
+# kernel's own (the streamed GEMV, and the LDS-staged one after the same
+# prepass) equal two matmul calls plus swiglu on the device bit for bit.
+@pytest.mark.parametrize("batch,k,pair_route,single_route", [(8, 4096, "q4_stream_pair_swiglu", "q4_stream_gemv"),
+                                                             (6, 4096, "q4_stream_pair_swiglu", "q4_stream_gemv"),
+                                                             (16, 4096, "q4_mfma_pair_swiglu", "q4_mfma_gemv"),
+                                                             (7, 8192, "q4_mfma_pair_swiglu", "q4_mfma_gemv")])
+def test_matmul_swiglu_small_batch_matches_two_matmuls(gpu, oracle, batch, k, pair_route, single_route):
+    n = 1000
+    wg = gaussian((n, k), 0.02, 91 + batch)
+    wu = gaussian((n, k), 0.02, 92 + batch)
+    x = gaussian((batch, k), 1.0, 93 + batch)
+    x[batch - 1, 17] = 40.0
+    pg, _ = weight_payload(kl.WeightType.q4_0, wg, oracle)
+    pu, _ = weight_payload(kl.WeightType.q4_0, wu, oracle)
+    fused, route = run_pair(kl.WeightType.q4_0, pg, pu, x, k, n, batch)
+    assert route == pair_route
+    from gpu_util import run_matmul
+    g, r1, _ = run_matmul(kl.WeightType.q4_0, pg, x, k, n, batch)
+    u, r2, _ = run_matmul(kl.WeightType.q4_0, pu, x, k, n, batch)
+    assert r1 == r2 == single_route
+    expected = device_swiglu(g, u)
+    print(f"  pair b{batch} k={k} {route} vs two {single_route}", flush=True)
+    assert np.array_equal(fused.view(np.uint32), expected.view(np.uint32))
