@@ -704,12 +704,13 @@ hipError_t launch_q4_dot8_slices(const uint8_t *w, const uint8_t *w2, const floa
             // us, N32000 13.25 against 13.9-14.3 us)
             return launch_q4_dot8_cfg<1, 1, 3, false, 6, 4, true, true>(w, w2, x, y, k, n, y_stride, stream, info, 4);
         }
-        // (the early refill measured slower here: K11008 x N4096 8.0 against
-        // 7.8 us)
+        // 2 slices in flight with the early refill (K11008 x N4096: 7.59 us
+        // against 7.80-7.83 us for 3 refilled after each decode, 8.0 for 3
+        // with the early refill, 8.55 for 4, 9.3-10.0 with all 6 in flight)
         const long long waves = std::max<long long>(1, std::min<long long>(n, static_cast<long long>(info.cus) * 8));
         if ((n + waves - 1) / waves * SLICES <= 2)
             return launch_q4_dot8_cfg<1, SLICES, 2, false, 6, 8>(w, w2, x, y, k, n, y_stride, stream, info, 8);
-        return launch_q4_dot8_cfg<1, SLICES, 3, false, 6, 8, true>(w, w2, x, y, k, n, y_stride, stream, info, 8);
+        return launch_q4_dot8_cfg<1, SLICES, 2, false, 6, 8, true, true>(w, w2, x, y, k, n, y_stride, stream, info, 8);
     }
     if constexpr (B == 1 && PAIR && SLICES == 1) {
         // gate/up pair, K <= 4096: 4 waves per CU over strided rows, 2 row
