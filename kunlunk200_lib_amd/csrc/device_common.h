@@ -173,22 +173,20 @@ __device__ __forceinline__ void fixed_point_digits(const float (&v)[8], float to
 // kernels/kunlun-swiglu.xpu:27-39): finite inputs give (g / (1 + e^-g)) * u;
 // otherwise NaN when g or u is NaN or g is -Inf, +-Inf with the product sign
 // when exactly one side is infinite and the other side (SiLU(g) for a finite
-// g) is non-zero, NaN for Inf * 0.
+// g) is non-zero, NaN for Inf * 0. SiLU(g) is computed once and the special
+// cases are selected from integer tests, without branches.
 __device__ __forceinline__ float swiglu_value(float g, float u) {
 #pragma clang fp contract(off)
+    const float act = g / (1.0f + expf(-g));
     const uint32_t gb = __float_as_uint(g), ub = __float_as_uint(u);
     const uint32_t ga = gb & 0x7fffffffu, ua = ub & 0x7fffffffu;
-    if (ga < 0x7f800000u && ua < 0x7f800000u) return (g / (1.0f + expf(-g))) * u;
-    const uint32_t sign = (gb ^ ub) & 0x80000000u;
-    uint32_t bits;
-    if (ga > 0x7f800000u || ua > 0x7f800000u || gb == 0xff800000u) {
-        bits = 0x7fc00000u;
-    } else if (ga == 0x7f800000u) {
-        bits = ua == 0 ? 0x7fc00000u : (sign | 0x7f800000u);
-    } else {
-        const float act = g / (1.0f + expf(-g));
-        bits = (__float_as_uint(act) & 0x7fffffffu) == 0 ? 0x7fc00000u : (sign | 0x7f800000u);
-    }
+    const uint32_t signed_inf = ((gb ^ ub) & 0x80000000u) | 0x7f800000u;
+    uint32_t bits = __float_as_uint(act * u);
+    bits = ga == 0x7f800000u ? (ua == 0 ? 0x7fc00000u : signed_inf) : bits;            // g = +Inf (-Inf below)
+    bits = ga < 0x7f800000u && ua == 0x7f800000u
+               ? ((__float_as_uint(act) & 0x7fffffffu) == 0 ? 0x7fc00000u : signed_inf)   // finite g, u = +-Inf
+               : bits;
+    bits = ga > 0x7f800000u || ua > 0x7f800000u || gb == 0xff800000u ? 0x7fc00000u : bits;
     return __uint_as_float(bits);
 }
 

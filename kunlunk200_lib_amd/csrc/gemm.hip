@@ -975,34 +975,20 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
                     *t = (acc[rg][cg][r] + *t) * scale_lds[row];
                 }
     }
-    if constexpr (PAIR) {
-        // SiLU(gate) * up into output columns 0 .. BN/2 (after every read of the tile)
-        __syncthreads();
-        constexpr int kHalf = S::BN / 2;
-        float pv[(BM * kHalf + kQlThreads - 1) / kQlThreads];
-#pragma unroll
-        for (int t = 0; t * kQlThreads < BM * kHalf; ++t) {
-            const int i = t * kQlThreads + static_cast<int>(threadIdx.x);
-            if (i < BM * kHalf) {
-                const int row = i / kHalf, c = i - row * kHalf;
-                pv[t] = kk::swiglu_value(tile_lds[row * kTs + c], tile_lds[row * kTs + kHalf + c]);
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int t = 0; t * kQlThreads < BM * kHalf; ++t) {
-            const int i = t * kQlThreads + static_cast<int>(threadIdx.x);
-            if (i < BM * kHalf) tile_lds[(i / kHalf) * kTs + i % kHalf] = pv[t];
-        }
-    }
     __syncthreads();
+    // PAIR: output column c is SiLU(tile column c) * (tile column BN/2 + c)
     constexpr int kQuads = kOut / 4;
     const bool vec = (n_rows & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
     for (int i = threadIdx.x; i < BM * kQuads; i += kQlThreads) {
         const int row = i / kQuads, q = i - row * kQuads;
         const int m = m0 + row, n = n0 + 4 * q;
         if (m >= m_rows || n >= n_rows) continue;
-        const float4v v = *reinterpret_cast<const float4v *>(tile_lds + row * kTs + 4 * q);
+        float4v v = *reinterpret_cast<const float4v *>(tile_lds + row * kTs + 4 * q);
+        if constexpr (PAIR) {
+            const float4v u = *reinterpret_cast<const float4v *>(tile_lds + row * kTs + S::BN / 2 + 4 * q);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) v[t] = kk::swiglu_value(v[t], u[t]);
+        }
         float *dst = y + static_cast<size_t>(m) * n_rows + n;
         if (vec && n + 3 < n_rows) {
             __builtin_nontemporal_store(v, reinterpret_cast<float4v *>(dst));   // streamed out, not kept in L2
