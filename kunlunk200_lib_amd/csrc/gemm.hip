@@ -602,12 +602,14 @@ __global__ __launch_bounds__(kGemmThreads) void mfma_gemm(const uint8_t *__restr
 // ---------------------------------------------------------------------------
 // q4_lds_gemm: Q4_0 weights, K % 256 == 0, 16-byte aligned weight pointers.
 //
-// Workgroup tile: BM activation rows x 4*WN weight rows; 8 waves. Wave w owns
-// weight rows WN*(w&3) .. +WN over all BM rows and takes K32 slices
-// 2*(w>>2), 2*(w>>2)+1 of every 128-K stage (two k-groups, whose sums meet in
-// LDS at the end in a fixed order).
+// Workgroup tile: BM activation rows x CW*WN weight rows; 2*CW waves (CW = 4,
+// or 8 for the 64 x 128 tile of one matrix: 16 waves, four per SIMD, hide
+// more of each wave's read -> decode -> MFMA latency). Wave w owns weight
+// rows WN*(w%CW) .. +WN over all BM rows and takes K32 slices 2*(w/CW),
+// 2*(w/CW)+1 of every 128-K stage (two k-groups, whose sums meet in LDS at
+// the end in a fixed order, so every tile sums in the same order).
 //
-// The 8 waves copy the activation tile (BM x 128 fp16 per stage) and the raw
+// The waves copy the activation tile (BM x 128 fp16 per stage) and the raw
 // Q4_0 bytes of the tile's weight rows (8 blocks = 144 B = nine 16-byte
 // chunks per row and stage pair) from global memory straight into LDS
 // (buffer_load_dwordx4 ... lds: 1 KB of LDS per wave instruction, no
@@ -620,7 +622,7 @@ __global__ __launch_bounds__(kGemmThreads) void mfma_gemm(const uint8_t *__restr
 //
 // LONG (the 64 x 128 tile, which leaves LDS to spare): 256-K stages, each
 // one stage pair of weights, in rings of three activation stages and three
-// weight buffers; a wave takes blocks 2*(w>>2), +1 and 4 + 2*(w>>2), +1 of a
+// weight buffers; a wave takes blocks 2*(w/CW), +1 and 4 + 2*(w/CW), +1 of a
 // stage, the blocks and order two 128-K stages give it, so every tile sums
 // in the same order. Half the stage barriers (K4096 x N4096 at batch 512:
 // 38.9-39.4 -> 37.4 us per call).
@@ -634,17 +636,20 @@ __global__ __launch_bounds__(kGemmThreads) void mfma_gemm(const uint8_t *__restr
 // ranges: the M tiles of one weight tile share an XCD and its L2.
 constexpr int kQlK = 128;                   // K per stage (4 Q4_0 blocks)
 constexpr int kQlABufs = 3;                 // activation stages in LDS
-constexpr int kQlThreads = 512;
 constexpr int kQlRowPair = 144;             // raw weight bytes per row and stage pair (8 blocks = 9 x 16 B)
 
-template <int BM, int WN, bool PAIR, bool LONG>
+template <int BM, int WN, bool PAIR, bool LONG, int CW = 4>
 struct QlShape {
-    static constexpr int BN = 4 * WN;                                   // weight rows per tile
+    static_assert(CW == 4 || (CW == 8 && !PAIR), "column waves per k-group");
+    static constexpr int Waves = 2 * CW;                                // two k-groups
+    static constexpr int Threads = 64 * Waves;
+    static constexpr int BN = CW * WN;                                  // weight rows per tile
     static constexpr int RG = BM / 16, CG = WN / 16;                    // MFMA tiles per wave
     static constexpr int KS = LONG ? 2 * kQlK : kQlK;                   // K per stage
     static constexpr int Chunks = KS / 8;                               // 16-byte chunks per activation row
     static constexpr int ABytes = BM * KS * 2;                          // one stage of activations
-    static constexpr int ACopiesPerWave = BM * Chunks / 64 / 8;         // 1 KB each, per stage
+    static constexpr int ACopiesPerWave = BM * Chunks / 64 / Waves;     // 1 KB each, per stage
+    static_assert(ACopiesPerWave * 64 * Waves == BM * Chunks, "whole activation copies per wave");
     static constexpr int BBufs = LONG ? 3 : 2;                          // weight buffers (stage pairs)
     // weights: 1 KB copies per stage pair; PAIR: the gate rows' copies, then
     // the up rows' from HalfCopies on (each half padded to whole copies; the
@@ -654,8 +659,8 @@ struct QlShape {
     static_assert(PAIR || BCopies * 64 == BN * (kQlRowPair / 16), "whole weight copies");
     static constexpr int UpBase = PAIR ? HalfCopies * 1024 : BN / 2 * kQlRowPair;
     static constexpr int BBytes = PAIR ? BCopies * 1024 : BN * kQlRowPair;   // one stage pair of weights
-    static constexpr int BCopiesPerWave = (BCopies + 7) / 8;            // waves below BCopies % 8 (if
-    static constexpr int BCopiesRem = BCopies % 8;                      // not 0) issue one more
+    static constexpr int BCopiesPerWave = (BCopies + Waves - 1) / Waves;   // waves below BCopies % Waves
+    static constexpr int BCopiesRem = BCopies % Waves;                     // (if not 0) issue one more
     static constexpr int TileStride = BN + 4;                           // floats per LDS output row
     static constexpr int XferBytes = BM * TileStride * 4;
     static constexpr int CopyBytes = kQlABufs * ABytes + BBufs * BBytes;
@@ -666,8 +671,8 @@ struct QlShape {
 };
 
 // Copies of a q4_lds_gemm workgroup's wave `wid` (buffer_load_dwordx4 ... lds,
-// 1 KB of LDS each): the activation copies wid + 8t of stage s into A buffer
-// s % 3, and the weight copies wid + 8t (below BCopies; PAIR: below
+// 1 KB of LDS each): the activation copies wid + Waves*t of stage s into A
+// buffer s % 3, and the weight copies wid + Waves*t (below BCopies; PAIR: below
 // HalfCopies from the gate matrix, the rest from the up matrix) of stage pair
 // p into B buffer p % 2. Offsets are per lane and fixed over stages; the stage
 // offset is the SGPR soffset. (Separate functions, not lambdas of the kernel:
@@ -681,7 +686,7 @@ __device__ __forceinline__ void ql_copy_a(const uint32_t (&a_off)[S::ACopiesPerW
     const int buf = (s % kQlABufs) * S::ABytes;
 #pragma unroll
     for (int t = 0; t < S::ACopiesPerWave; ++t)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) uint8_t *)ql_lds + buf + (wid + 8 * t) * 1024,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) uint8_t *)ql_lds + buf + (wid + S::Waves * t) * 1024,
                                                  16, a_off[t], s * (S::KS * 2), 0, 0);
 }
 
@@ -694,7 +699,7 @@ __device__ __forceinline__ void ql_copy_b(const uint32_t (&b_off)[S::BCopiesPerW
     const int buf = kQlABufs * S::ABytes + (p % S::BBufs) * S::BBytes;
 #pragma unroll
     for (int t = 0; t < S::BCopiesPerWave; ++t) {
-        const int i = wid + 8 * t;
+        const int i = wid + S::Waves * t;
         if (i < S::BCopies)                                     // wave-uniform
             __builtin_amdgcn_raw_ptr_buffer_load_lds(PAIR && i >= S::HalfCopies ? rsrc2 : rsrc,
                                                      (__attribute__((address_space(3))) uint8_t *)ql_lds + buf + i * 1024,
@@ -706,14 +711,15 @@ __device__ __forceinline__ void ql_copy_b(const uint32_t (&b_off)[S::BCopiesPerW
 // its BN/2 up rows (matrix w2, from S::UpBase); waves 0-1 (tile columns
 // 0 .. BN/2) take the gate rows and waves 2-3 the up rows of the same output
 // columns, which the epilogue pairs in LDS.
-template <int BM, int WN, bool PAIR, bool LONG>
-__global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restrict__ w, const uint8_t *__restrict__ w2,
+template <int BM, int WN, bool PAIR, bool LONG, int CW = 4>
+__global__ __launch_bounds__(128 * CW) void q4_lds_gemm(const uint8_t *__restrict__ w, const uint8_t *__restrict__ w2,
                                                          const _Float16 *__restrict__ x16,
                                                          const float *__restrict__ row_inv, float *__restrict__ y,
                                                          int m_rows, int n_rows, int k_pad, int stages,
                                                          uint32_t row_bytes, int m_tiles, int tiles, int tiles_per_xcd) {
-    using S = QlShape<BM, WN, PAIR, LONG>;
+    using S = QlShape<BM, WN, PAIR, LONG, CW>;
     constexpr int kOut = PAIR ? S::BN / 2 : S::BN;             // output columns per tile
+    constexpr int kQlThreads = S::Threads;
     extern __shared__ __align__(16) uint8_t ql_lds[];
 
     const int bid = blockIdx.x;
@@ -724,7 +730,7 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
     const int m0 = mt * BM, n0 = nt * kOut;
     const int lane = threadIdx.x & (kWave - 1);
     const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-    const int kh = wid >> 2, wn = wid & 3;
+    const int kh = wid / CW, wn = wid % CW;
     const int g = lane >> 4, c16 = lane & 15;
     // The tile's row scales, loaded before the first copy and handed to the
     // epilogue through LDS: no global load there (on gfx9 a wait for a load
@@ -745,7 +751,7 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
 #pragma unroll
     for (int t = 0; t < S::ACopiesPerWave; ++t) {
         constexpr int kRowsPerCopy = 64 / S::Chunks;
-        const int r = kRowsPerCopy * (wid + 8 * t) + lane / S::Chunks, pos = lane % S::Chunks;
+        const int r = kRowsPerCopy * (wid + S::Waves * t) + lane / S::Chunks, pos = lane % S::Chunks;
         a_off[t] = static_cast<uint32_t>(r * k_pad + 8 * (pos ^ (r & 15))) * 2;
     }
     // B copy i: 16-byte chunks 64c .. 64c+63 (c = i, or i - HalfCopies for the
@@ -757,7 +763,7 @@ __global__ __launch_bounds__(kQlThreads) void q4_lds_gemm(const uint8_t *__restr
     uint32_t b_off[S::BCopiesPerWave];
 #pragma unroll
     for (int t = 0; t < S::BCopiesPerWave; ++t) {
-        const int i = wid + 8 * t;
+        const int i = wid + S::Waves * t;
         const int q = (PAIR && i >= S::HalfCopies ? i - S::HalfCopies : i) * 64 + lane;   // past the rows: clamped
         const int row = min(q / (kQlRowPair / 16), kRows - 1);
         const int chunk = q - (q / (kQlRowPair / 16)) * (kQlRowPair / 16);
@@ -1072,18 +1078,18 @@ QlTile pick_ql_tile(int batch, int n, bool pair) {
     return pick;
 }
 
-template <int BM, int WN, bool PAIR, bool LONG = false>
+template <int BM, int WN, bool PAIR, bool LONG = false, int CW = 4>
 hipError_t launch_ql_gemm(const void *w, const void *w2, const _Float16 *x16, const float *row_inv, float *y, int batch,
                           int n, int k, int k_pad, hipStream_t stream) {
-    using S = QlShape<BM, WN, PAIR, LONG>;
-    hipError_t rc = kk::opt_in_lds(reinterpret_cast<const void *>(&q4_lds_gemm<BM, WN, PAIR, LONG>), S::LdsBytes);
+    using S = QlShape<BM, WN, PAIR, LONG, CW>;
+    hipError_t rc = kk::opt_in_lds(reinterpret_cast<const void *>(&q4_lds_gemm<BM, WN, PAIR, LONG, CW>), S::LdsBytes);
     if (rc != hipSuccess) return rc;
     const int out = PAIR ? S::BN / 2 : S::BN;
     const int m_tiles = (batch + BM - 1) / BM;
     const int tiles = m_tiles * ((n + out - 1) / out);
     const int tiles_per_xcd = (tiles + kXcds - 1) / kXcds;
     const uint32_t row_bytes = static_cast<uint32_t>(k / 32 * 18);
-    hipLaunchKernelGGL((q4_lds_gemm<BM, WN, PAIR, LONG>), dim3(tiles_per_xcd * kXcds), dim3(kQlThreads), S::LdsBytes,
+    hipLaunchKernelGGL((q4_lds_gemm<BM, WN, PAIR, LONG, CW>), dim3(tiles_per_xcd * kXcds), dim3(S::Threads), S::LdsBytes,
                        stream, static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(w2), x16, row_inv, y, batch,
                        n, k_pad, k / S::KS, row_bytes, m_tiles, tiles, tiles_per_xcd);
     return hipGetLastError();
@@ -1095,7 +1101,12 @@ hipError_t launch_ql(const void *w, const void *w2, const _Float16 *x16, const f
     const QlTile t = pick_ql_tile(batch, n, PAIR);
     if (t.bm == 128 && t.wn == 32) return launch_ql_gemm<128, 32, PAIR>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
     if (t.bm == 64 && t.wn == 64) return launch_ql_gemm<64, 64, PAIR>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
-    if (t.bm == 64 && t.wn == 32) return launch_ql_gemm<64, 32, PAIR, true>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
+    if (t.bm == 64 && t.wn == 32) {
+        // 64 x 128 tile: 16 waves of 64 x 16 for one matrix (twice the waves per SIMD to hide
+        // the read -> decode -> MFMA latency; same k-groups, so the same bits), 8 of 64 x 32 for a pair
+        if constexpr (PAIR) return launch_ql_gemm<64, 32, true, true>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
+        else return launch_ql_gemm<64, 16, false, true, 8>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
+    }
     if (t.bm == 128 && t.wn == 48) return launch_ql_gemm<128, 48, PAIR>(w, w2, x16, row_inv, y, batch, n, k, k_pad, stream);
     return hipErrorInvalidValue;
 }
