@@ -315,9 +315,11 @@ __global__ __launch_bounds__(kThreads) void q4_mfma_gemv(const uint8_t *__restri
 // ---------------------------------------------------------------------------
 // q4_lds_gemv<SB>: the same products, streamed (K % (32 SB) == 0, 16-byte
 // aligned weights). A workgroup owns 64 weight rows (four 16-row MFMA tiles);
-// its 8 waves are 2 k-groups x 4 tiles: wave w computes tile w & 3 over
-// blocks SB/2 (w >> 2) .. +SB/2-1 of every SB-block stage, and the k-groups'
-// sums meet in LDS at the end in a fixed order. Per stage the waves copy the
+// its 4 KG waves are KG k-groups x 4 tiles (KG = 4 for 16-block stages: 16
+// waves, four per SIMD, so more of each wave's LDS read -> decode -> MFMA
+// latency is hidden; KG = 2 for 8-block stages): wave w computes tile w & 3
+// over blocks SB/KG (w >> 2) .. +SB/KG-1 of every SB-block stage, and the
+// k-groups' sums meet in LDS at the end in a fixed order. Per stage the waves copy the
 // stage's A fragments (SB blocks x (hi, lo) = 2 SB KiB, from L2) and the 64
 // rows' raw bytes (18 SB B per row as 16-byte chunks, from HBM; consecutive
 // lanes take consecutive chunks, so one copy touches a few rows) straight
@@ -327,12 +329,14 @@ __global__ __launch_bounds__(kThreads) void q4_mfma_gemv(const uint8_t *__restri
 // the same LDS (3 x 50 KiB against 6 x 25 KiB). Weight rows sit 18 SB bytes
 // apart in LDS, so a tile's 16 rows read 16 distinct banks; A fragments are
 // lane-contiguous.
-constexpr int kLgThreads = 512;
 constexpr int kLgRows = 64;                                  // weight rows per workgroup
 
-template <int SB, bool PACKED>
+template <int SB, bool PACKED, int KG = 2>
 struct LgShape {
     static_assert(SB == 8 || SB == 16, "stage of 8 or 16 blocks");
+    static_assert(KG == 2 || (KG == 4 && SB == 16), "k-groups");
+    static constexpr int Waves = 4 * KG;                               // 4 row tiles x KG k-groups
+    static constexpr int Threads = 64 * Waves;
     static constexpr int RowStage = SB * 18;                           // bytes of a row per stage
     static constexpr int Slots = SB == 8 ? 6 : PACKED ? 4 : 3;         // ring stages
     static constexpr int ABlockBytes = PACKED ? kFragBlockBytes / 2 : kFragBlockBytes;
@@ -340,12 +344,13 @@ struct LgShape {
     static constexpr int BStageBytes = kLgRows * RowStage;             // 9 / 18 KiB
     static constexpr int StageBytes = AStageBytes + BStageBytes;
     static constexpr int ACopies = AStageBytes / 1024, BCopies = BStageBytes / 1024;
-    static constexpr int ACopiesPerWave = ACopies / 8;                 // 1 / 2 / 4
-    static constexpr int BCopiesPerWave = (BCopies + 7) / 8;           // 2 / 3 (waves below
-    static constexpr int BCopiesRem = BCopies % 8;                     // BCopies % 8 issue them all)
-    static constexpr int WaveBlocks = SB / 2;                          // blocks per wave and stage
+    static constexpr int ACopiesPerWave = ACopies / Waves;
+    static constexpr int BCopiesPerWave = (BCopies + Waves - 1) / Waves;   // waves below BCopies % Waves
+    static constexpr int BCopiesRem = BCopies % Waves;                     // issue them all
+    static constexpr int WaveBlocks = SB / KG;                         // blocks per wave and stage
     static constexpr int LdsBytes = Slots * StageBytes;                // 102 .. 150 KiB
-    static_assert(BCopies * 1024 == BStageBytes && ACopies % 8 == 0 && BCopiesRem != 0, "whole copies");
+    static_assert(BCopies * 1024 == BStageBytes && ACopies % Waves == 0 && BCopiesRem != 0, "whole copies");
+    static_assert(WaveBlocks % 2 == 0, "block parity follows the wave's block index");
     static_assert(LdsBytes <= 160 * 1024, "LDS");
 };
 
@@ -379,12 +384,12 @@ __device__ __forceinline__ uint32_t lg_and_or(uint32_t a, uint32_t mask, uint32_
 // drops the launch stub.)
 // PAIR: copies below BCopies / 2 come from w_tile (the gate rows), the rest
 // from w2_tile (the up rows; b_off relative to it).
-template <int SB, bool PACKED, bool PAIR>
+template <int SB, bool PACKED, bool PAIR, int KG>
 __device__ __forceinline__ void lg_copy_stage(const uint8_t *frag, int frag_bytes, uint8_t *w_tile, int w_extent,
                                               uint8_t *w2_tile, int w2_extent,
-                                              const uint32_t (&b_off)[LgShape<SB, PACKED>::BCopiesPerWave], int wid,
+                                              const uint32_t (&b_off)[LgShape<SB, PACKED, KG>::BCopiesPerWave], int wid,
                                               int lane, int s) {
-    using L = LgShape<SB, PACKED>;
+    using L = LgShape<SB, PACKED, KG>;
     extern __shared__ __align__(16) uint8_t lg_lds[];
     const __amdgpu_buffer_rsrc_t a_rsrc =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(frag), 0, frag_bytes, 0x00020000);
@@ -393,11 +398,11 @@ __device__ __forceinline__ void lg_copy_stage(const uint8_t *frag, int frag_byte
         (__attribute__((address_space(3))) uint8_t *)lg_lds + (s % L::Slots) * L::StageBytes;
 #pragma unroll
     for (int t = 0; t < L::ACopiesPerWave; ++t)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, buf + (wid + 8 * t) * 1024, 16,
-                                                 (wid + 8 * t) * 1024 + lane * 16, s * L::AStageBytes, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, buf + (wid + L::Waves * t) * 1024, 16,
+                                                 (wid + L::Waves * t) * 1024 + lane * 16, s * L::AStageBytes, 0, 0);
 #pragma unroll
     for (int t = 0; t < L::BCopiesPerWave; ++t) {
-        const int copy = wid + 8 * t;                           // wave-uniform
+        const int copy = wid + L::Waves * t;                    // wave-uniform
         if (copy >= L::BCopies) continue;
         if (PAIR && copy >= L::BCopies / 2) {
             const __amdgpu_buffer_rsrc_t b2_rsrc = __builtin_amdgcn_make_buffer_rsrc(w2_tile, 0, w2_extent, 0x00020000);
@@ -414,14 +419,14 @@ __device__ __forceinline__ void lg_copy_stage(const uint8_t *frag, int frag_byte
 // the workgroup's rows 0..31 are rows 32i .. 32i + 31 of w (the gate
 // matrix), rows 32..63 the same rows of w2, and y = SiLU(gate) * up
 // ([batch][n], kk::swiglu_value) from the gate tiles' waves.
-template <int SB, bool PACKED, bool PAIR = false>
-__global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restrict__ w,
+template <int SB, bool PACKED, bool PAIR = false, int KG = 2>
+__global__ __launch_bounds__(256 * KG) void q4_lds_gemv(const uint8_t *__restrict__ w,
                                                          const uint8_t *__restrict__ w2,
                                                          const _Float16 *__restrict__ frag,
                                                          const float *__restrict__ row_inv, float *__restrict__ y,
                                                          int n, int batch, int stages, uint32_t row_bytes,
                                                          int tiles, int tiles_per_xcd) {
-    using L = LgShape<SB, PACKED>;
+    using L = LgShape<SB, PACKED, KG>;
     static_assert(!PAIR || (L::BCopies % 2 == 0 && (L::BCopies / 2) * 64 == (kLgRows / 2) * (L::RowStage / 16)),
                   "a pair's weight copies split at the half");
     extern __shared__ __align__(16) uint8_t lg_lds[];
@@ -444,7 +449,7 @@ __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restr
     uint32_t b_off[L::BCopiesPerWave];
 #pragma unroll
     for (int t = 0; t < L::BCopiesPerWave; ++t) {
-        const int q = min(wid + 8 * t, L::BCopies - 1) * 64 + lane;
+        const int q = min(wid + L::Waves * t, L::BCopies - 1) * 64 + lane;
         const int row = q / kChunks, chunk = q - (q / kChunks) * kChunks;
         const int mrow = PAIR ? row % kOutRows : row;           // row of its own matrix's tile
         b_off[t] = static_cast<uint32_t>(min(n0 + mrow, n - 1) - n0) * row_bytes + 16 * chunk;
@@ -467,12 +472,12 @@ __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restr
     // s+1 .. min(s+Slots-2, stages-1) may still be in flight.
     const int ahead0 = min(L::Slots - 1, stages);
     for (int s = 0; s < ahead0; ++s)
-        lg_copy_stage<SB, PACKED, PAIR>(fbytes, frag_bytes, w_tile, w_extent, w2_tile, w_extent, b_off, wid, lane, s);
+        lg_copy_stage<SB, PACKED, PAIR, KG>(fbytes, frag_bytes, w_tile, w_extent, w2_tile, w_extent, b_off, wid, lane, s);
     for (int s = 0; s < stages; ++s) {
         wait_vmcnt_dyn(my_copies * min(L::Slots - 2, stages - 1 - s));
         lds_barrier();
         if (s + L::Slots - 1 < stages)
-            lg_copy_stage<SB, PACKED, PAIR>(fbytes, frag_bytes, w_tile, w_extent, w2_tile, w_extent, b_off, wid, lane,
+            lg_copy_stage<SB, PACKED, PAIR, KG>(fbytes, frag_bytes, w_tile, w_extent, w2_tile, w_extent, b_off, wid, lane,
                                             s + L::Slots - 1);
         const uint8_t *abuf = lg_lds + (s % L::Slots) * L::StageBytes;
         const uint8_t *brow = abuf + L::AStageBytes + (wt * 16 + c16) * L::RowStage;
@@ -519,14 +524,16 @@ __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restr
         }
     }
 
-    // k-group 1 hands its sums to k-group 0 through LDS (every copy has
-    // landed: the last wait was for all of them)
+    // k-groups 1 .. KG-1 hand their sums to k-group 0 through LDS (every
+    // copy has landed: the last wait was for all of them), which adds them
+    // in k-group order
     __syncthreads();
     float4v *xfer = reinterpret_cast<float4v *>(lg_lds);
-    if (kh == 1) xfer[wt * kWave + lane] = acc;
+    if (kh >= 1) xfer[((kh - 1) * 4 + wt) * kWave + lane] = acc;
     __syncthreads();
-    if (!PAIR && kh == 1) return;
-    acc += xfer[wt * kWave + lane];
+    if (!PAIR && kh >= 1) return;
+#pragma unroll
+    for (int h = 1; h < KG; ++h) acc += xfer[((h - 1) * 4 + wt) * kWave + lane];
     if constexpr (PACKED) {
         // D rows 8..15 (lanes 32..63) are the lo parts of batch rows 0..7
 #pragma unroll
@@ -535,10 +542,10 @@ __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restr
     if constexpr (PAIR) {
         // the up tiles (waves 2, 3 of k-group 0) hand their sums to the gate
         // tiles (waves 0, 1) through LDS; every wave takes part in the barrier
-        float4v *upx = xfer + 4 * kWave;
+        float4v *upx = xfer + (KG - 1) * 4 * kWave;
         if (kh == 0 && wt >= 2) upx[(wt - 2) * kWave + lane] = acc;
         __syncthreads();
-        if (kh == 1 || wt >= 2 || (PACKED && g >= 2)) return;
+        if (kh >= 1 || wt >= 2 || (PACKED && g >= 2)) return;
         const float4v up = upx[wt * kWave + lane];
         const int rr = n0 + wt * 16 + c16;
         if (rr < n) {
@@ -565,19 +572,26 @@ __global__ __launch_bounds__(kLgThreads) void q4_lds_gemv(const uint8_t *__restr
 
 // Launch q4_lds_gemv<SB> (dynamic LDS above 64 KiB opted into once per
 // device).
-template <int SB, bool PACKED, bool PAIR = false>
-hipError_t launch_lds_gemv(const uint8_t *w, const uint8_t *w2, const _Float16 *frag, const float *row_inv, float *y,
-                           int k, int n, int batch, hipStream_t stream) {
-    using L = LgShape<SB, PACKED>;
-    const hipError_t rc = kk::opt_in_lds(reinterpret_cast<const void *>(&q4_lds_gemv<SB, PACKED, PAIR>), L::LdsBytes);
+template <int SB, bool PACKED, bool PAIR = false, int KG = 2>
+hipError_t launch_lds_gemv_kg(const uint8_t *w, const uint8_t *w2, const _Float16 *frag, const float *row_inv, float *y,
+                              int k, int n, int batch, hipStream_t stream) {
+    using L = LgShape<SB, PACKED, KG>;
+    const hipError_t rc =
+        kk::opt_in_lds(reinterpret_cast<const void *>(&q4_lds_gemv<SB, PACKED, PAIR, KG>), L::LdsBytes);
     if (rc != hipSuccess) return rc;
     const int out_rows = PAIR ? kLgRows / 2 : kLgRows;
     const int tiles = (n + out_rows - 1) / out_rows;
     const int tiles_per_xcd = (tiles + 7) / 8;
-    hipLaunchKernelGGL((q4_lds_gemv<SB, PACKED, PAIR>), dim3(tiles_per_xcd * 8), dim3(kLgThreads), L::LdsBytes, stream,
+    hipLaunchKernelGGL((q4_lds_gemv<SB, PACKED, PAIR, KG>), dim3(tiles_per_xcd * 8), dim3(L::Threads), L::LdsBytes, stream,
                        w, w2, frag, row_inv, y, n, batch, k / (SB * 32), static_cast<uint32_t>(k / 32 * 18), tiles,
                        tiles_per_xcd);
     return hipGetLastError();
+}
+
+template <int SB, bool PACKED, bool PAIR = false>
+hipError_t launch_lds_gemv(const uint8_t *w, const uint8_t *w2, const _Float16 *frag, const float *row_inv, float *y,
+                           int k, int n, int batch, hipStream_t stream) {
+    return launch_lds_gemv_kg<SB, PACKED, PAIR, SB == 16 ? 4 : 2>(w, w2, frag, row_inv, y, k, n, batch, stream);
 }
 
 } // namespace
