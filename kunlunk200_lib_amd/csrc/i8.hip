@@ -732,8 +732,10 @@ hipError_t launch_i8_rows(const float *x, const int8_t *w, const float *scales, 
 }
 
 // Batch > 64, K % 128 == 0: LDS-staged int8 GEMM. Workgroup tile: 128 code
-// rows (64 batch rows) x 128 weight rows; 8 waves = 2 k-groups x (2 x 2)
-// wave tiles of 64 x 64. A stage is 128 K: k-group h takes the stage's 64-K
+// rows (64 batch rows) x 128 weight rows; 16 waves = 2 k-groups x (2 x 4)
+// wave tiles of 64 x 32 (four waves per SIMD: at 2 x 2 tiles of 64 x 64,
+// two per SIMD, K4096 x N4096 at batch 512 took 43.0-44.9 us per call
+// against 40.9-41.2). A stage is 128 K: k-group h takes the stage's 64-K
 // step h. Both operands arrive by buffer_load_dwordx4 ... lds (1 KB of LDS per
 // wave instruction, no registers), three stages ahead into a ring of four.
 // LDS rows are 128 B (8 chunks of 16 B); chunk ch of row r sits at position
@@ -745,21 +747,23 @@ constexpr int kIgSlots = 4;
 constexpr int kIgOpBytes = kIgRows * kIgK;    // 16 KiB per operand and stage
 constexpr int kIgStageBytes = 2 * kIgOpBytes;
 constexpr int kIgLdsBytes = kIgSlots * kIgStageBytes;   // 128 KiB
-constexpr int kIgCopiesPerWave = 4;           // 2 A + 2 B copies of 1 KiB per stage
 static_assert(kIgLdsBytes >= 4 * 64 * 64 * 4 && kIgLdsBytes <= 160 * 1024, "ring also holds the k-group sums");
 
-__device__ __forceinline__ void ig_wait(int stages_after) {   // vmcnt(4 * stages_after), 0..2
+// vmcnt(copies per stage * stages_after), stages_after 0..2
+template <int CPW>
+__device__ __forceinline__ void ig_wait(int stages_after) {
     if (stages_after <= 0) __builtin_amdgcn_s_waitcnt(0x0F70);
-    else if (stages_after == 1) __builtin_amdgcn_s_waitcnt(0x0F70 | kIgCopiesPerWave);
-    else __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * kIgCopiesPerWave));
+    else if (stages_after == 1) __builtin_amdgcn_s_waitcnt(0x0F70 | CPW);
+    else __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * CPW));
 }
 
-// Stage s's copies of wave `wid`: A copies wid, wid + 8 and B copies wid,
-// wid + 8 (copy i: rows 8i .. 8i+7 of the tile, lane -> row 8i + l/8,
+// Stage s's copies of wave `wid` of W waves: A copies wid + W t and B copies
+// wid + W t (copy i: rows 8i .. 8i+7 of the tile, lane -> row 8i + l/8,
 // position l % 8). (A separate function: the host pass rejects a kernel-local
 // lambda that hands captured values to these builtins.)
+template <int W>
 __device__ __forceinline__ void ig_copy_stage(const int8_t *a_tile, int a_extent, const int8_t *b_tile, int b_extent,
-                                              const uint32_t (&a_off)[2], const uint32_t (&b_off)[2], int wid,
+                                              const uint32_t (&a_off)[16 / W], const uint32_t (&b_off)[16 / W], int wid,
                                               int s) {
     extern __shared__ __align__(16) uint8_t ig_lds[];
     const __amdgpu_buffer_rsrc_t a_rsrc =
@@ -769,14 +773,17 @@ __device__ __forceinline__ void ig_copy_stage(const int8_t *a_tile, int a_extent
     __attribute__((address_space(3))) uint8_t *buf =
         (__attribute__((address_space(3))) uint8_t *)ig_lds + (s % kIgSlots) * kIgStageBytes;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, buf + (wid + 8 * t) * 1024, 16, a_off[t], s * kIgK, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, buf + kIgOpBytes + (wid + 8 * t) * 1024, 16, b_off[t],
+    for (int t = 0; t < 16 / W; ++t) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, buf + (wid + W * t) * 1024, 16, a_off[t], s * kIgK, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, buf + kIgOpBytes + (wid + W * t) * 1024, 16, b_off[t],
                                                  s * kIgK, 0, 0);
     }
 }
 
-__global__ __launch_bounds__(512) void i8_lds_gemm(const int8_t *__restrict__ codes, const int8_t *__restrict__ w,
+// CW column waves per k-group and row half: wave tiles of 64 x (128 / CW)
+// (CW = 2: 8 waves of 64 x 64; CW = 4: 16 waves of 64 x 32, four per SIMD).
+template <int CW>
+__global__ __launch_bounds__(256 * CW) void i8_lds_gemm(const int8_t *__restrict__ codes, const int8_t *__restrict__ w,
                                                    const float *__restrict__ scales, const float *__restrict__ maxima,
                                                    const float *__restrict__ final_max, float *__restrict__ y,
                                                    int k, int n, int batch, int m_tiles, int tiles, int tiles_per_xcd) {
@@ -789,7 +796,9 @@ __global__ __launch_bounds__(512) void i8_lds_gemm(const int8_t *__restrict__ co
     const int m0 = mt * kIgRows, n0 = nt * kIgRows;
     const int lane = threadIdx.x & (kWave - 1);
     const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-    const int kg = wid >> 2, wm = (wid >> 1) & 1, wn = wid & 1;
+    constexpr int kWaves = 4 * CW, kCopies = 16 / kWaves;      // copies per operand, wave and stage
+    constexpr int kWn = 128 / CW, kNt = kWn / 16;              // wave tile columns, 16-column MFMA tiles
+    const int kg = wid / (2 * CW), wm = (wid / CW) & 1, wn = wid % CW;
     const int g = lane >> 4, c = lane & 15;
 
     // copy offsets: lane l of copy i -> tile row 8i + l/8 (clamped to the last
@@ -797,10 +806,10 @@ __global__ __launch_bounds__(512) void i8_lds_gemm(const int8_t *__restrict__ co
     const int a_rows = min(kIgRows, rows - m0), b_rows = min(kIgRows, n - n0);
     const int8_t *a_tile = codes + static_cast<size_t>(m0) * k;
     const int8_t *b_tile = w + static_cast<size_t>(n0) * k;
-    uint32_t a_off[2], b_off[2];
+    uint32_t a_off[kCopies], b_off[kCopies];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int row = 8 * (wid + 8 * t) + (lane >> 3);
+    for (int t = 0; t < kCopies; ++t) {
+        const int row = 8 * (wid + kWaves * t) + (lane >> 3);
         const int chunk = (lane & 7) ^ ((row >> 1) & 7);
         a_off[t] = static_cast<uint32_t>(min(row, a_rows - 1)) * k + 16 * chunk;
         b_off[t] = static_cast<uint32_t>(min(row, b_rows - 1)) * k + 16 * chunk;
@@ -808,47 +817,52 @@ __global__ __launch_bounds__(512) void i8_lds_gemm(const int8_t *__restrict__ co
     const int a_extent = a_rows * k, b_extent = b_rows * k;
     const int stages = k / kIgK;
 
-    int32x4 acc[4][4];
+    int32x4 acc[4][kNt];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = int32x4{0, 0, 0, 0};
+        for (int j = 0; j < kNt; ++j) acc[i][j] = int32x4{0, 0, 0, 0};
 
     const int ahead0 = min(kIgSlots - 1, stages);
-    for (int s = 0; s < ahead0; ++s) ig_copy_stage(a_tile, a_extent, b_tile, b_extent, a_off, b_off, wid, s);
+    for (int s = 0; s < ahead0; ++s) ig_copy_stage<kWaves>(a_tile, a_extent, b_tile, b_extent, a_off, b_off, wid, s);
     for (int s = 0; s < stages; ++s) {
-        ig_wait(min(kIgSlots - 2, stages - 1 - s));
+        ig_wait<2 * kCopies>(min(kIgSlots - 2, stages - 1 - s));
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("" ::: "memory");
         if (s + kIgSlots - 1 < stages)
-            ig_copy_stage(a_tile, a_extent, b_tile, b_extent, a_off, b_off, wid, s + kIgSlots - 1);
+            ig_copy_stage<kWaves>(a_tile, a_extent, b_tile, b_extent, a_off, b_off, wid, s + kIgSlots - 1);
         const uint8_t *abuf = ig_lds + (s % kIgSlots) * kIgStageBytes;
         const uint8_t *bbuf = abuf + kIgOpBytes;
         // k-group kg: step kg of the stage, chunks 4 kg + g of each row
-        int32x4 af[4], bf[4];
+        int32x4 af[4], bf[kNt];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int ra = wm * 64 + i * 16 + c, rb = wn * 64 + i * 16 + c;
+            const int ra = wm * 64 + i * 16 + c;
             af[i] = *reinterpret_cast<const int32x4 *>(abuf + ra * kIgK + (((4 * kg + g) ^ ((ra >> 1) & 7)) * 16));
-            bf[i] = *reinterpret_cast<const int32x4 *>(bbuf + rb * kIgK + (((4 * kg + g) ^ ((rb >> 1) & 7)) * 16));
+        }
+#pragma unroll
+        for (int j = 0; j < kNt; ++j) {
+            const int rb = wn * kWn + j * 16 + c;
+            bf[j] = *reinterpret_cast<const int32x4 *>(bbuf + rb * kIgK + (((4 * kg + g) ^ ((rb >> 1) & 7)) * 16));
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < kNt; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
 
     // k-group 1 hands its sums to k-group 0 (exact int32 adds), which combines
     __syncthreads();                                            // every copy landed (last wait: all), ring idle
-    int32x4 *xfer = reinterpret_cast<int32x4 *>(ig_lds) + (wid & 3) * 16 * kWave;
+    int32x4 *xfer = reinterpret_cast<int32x4 *>(ig_lds) + (wid % (2 * CW)) * 4 * kNt * kWave;
     if (kg == 1) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) xfer[(i * 4 + j) * kWave + lane] = acc[i][j];
+            for (int j = 0; j < kNt; ++j) xfer[(i * kNt + j) * kWave + lane] = acc[i][j];
     }
     __syncthreads();
     if (kg == 1) return;
@@ -856,13 +870,13 @@ __global__ __launch_bounds__(512) void i8_lds_gemm(const int8_t *__restrict__ co
     const float scale1 = final_max[1] / 127.0f;
     const float wmax = maxima[0] / 127.0f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int r = n0 + wn * 64 + j * 16 + c;
+    for (int j = 0; j < kNt; ++j) {
+        const int r = n0 + wn * kWn + j * 16 + c;
         if (r >= n) continue;
         const float rs = scales[r];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int32x4 d = acc[i][j] + xfer[(i * 4 + j) * kWave + lane];
+            const int32x4 d = acc[i][j] + xfer[(i * kNt + j) * kWave + lane];
             // D rows 4g .. 4g+3 of row tile i: (q0, q1) of two batch rows
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
@@ -936,13 +950,13 @@ extern "C" int kk_i8_matmul(const void *workspace, const int8_t *w, const float 
     if (route) *route = "i8_mfma_gemm";
     if (k % kIgK == 0 && static_cast<long long>(2 * batch) * k <= 0x7fffffffLL &&
         static_cast<long long>(n) * k <= 0x7fffffffLL) {
-        const hipError_t rc = kk::opt_in_lds(reinterpret_cast<const void *>(&i8_lds_gemm), kIgLdsBytes);
-        if (rc != hipSuccess) return rc;
         const int m_tiles = (2 * batch + kIgRows - 1) / kIgRows;
         const int tiles = m_tiles * ((n + kIgRows - 1) / kIgRows);
         const int tiles_per_xcd = (tiles + 7) / 8;
-        hipLaunchKernelGGL(i8_lds_gemm, dim3(tiles_per_xcd * 8), dim3(512), kIgLdsBytes, stream, ws.codes, w, scales,
-                           maxima, ws.final_max, y, k, n, batch, m_tiles, tiles, tiles_per_xcd);
+        const hipError_t rc = kk::opt_in_lds(reinterpret_cast<const void *>(&i8_lds_gemm<4>), kIgLdsBytes);
+        if (rc != hipSuccess) return rc;
+        hipLaunchKernelGGL(i8_lds_gemm<4>, dim3(tiles_per_xcd * 8), dim3(1024), kIgLdsBytes, stream, ws.codes, w,
+                           scales, maxima, ws.final_max, y, k, n, batch, m_tiles, tiles, tiles_per_xcd);
         return hipGetLastError();
     }
     return launch_i8<4, 4>(ws.codes, w, scales, maxima, ws.final_max, y, k, n, batch, stream);
