@@ -354,7 +354,7 @@ def gemm_leg(kernel, events, stream, device: int, reps: int) -> dict:
 
 
 SMALL_BATCH_Q4 = (4096, 14336, (2, 4, 8, 16))
-DECODE_PAIR_BATCHES = (1, 4, 8, 16)                    # matmul_swiglu at decode batch sizes
+DECODE_PAIR_BATCHES = (1, 4, 8, 16, 32)                # matmul_swiglu at decode batch sizes
 SMALL_DENSE = (4096, 4096, (1, 8))                   # F16 / F32 part of configs[2]
 DECODE_PAIR = (4096, 11008)                          # gate/up pair of the decode layer (matmul_swiglu, batch 1)
 

@@ -233,6 +233,58 @@ void matmul(Kernel & kernel, int id, void * y, const void * w, const void * x, i
     detail::count_matmul(id);
 }
 
+// Q4_0 gate/up pair of `batch` columns in one launch (both products and
+// SwiGLU), batch 1..16: the batch-1/2 GEMV's, the streamed, block-diagonal or
+// LDS-staged GEMV's pair form, whichever takes the shape; none: two GEMVs and
+// SwiGLU instead.
+enum class Q4PairRoute { none, dot8, stream, bdiag, mfma };
+
+static Q4PairRoute q4_pair_route(const void * w_gate, const void * w_up, const float * x, int k, int n, int batch) {
+    if (kk_q4_gemv_pair_swiglu_supported(w_gate, w_up, x, k, n, batch)) return Q4PairRoute::dot8;
+    if (kk::q4_stream_batch(batch) && kk_q4_stream_gemv_supported(w_gate, x, k, n, batch) &&
+        kk_q4_stream_gemv_supported(w_up, x, k, n, batch))
+        return Q4PairRoute::stream;
+    if (kk::q4_bdiag_batch(batch) && kk_q4_bdiag_gemv_supported(w_gate, x, k, n, batch) &&
+        kk_q4_bdiag_gemv_supported(w_up, x, k, n, batch))
+        return Q4PairRoute::bdiag;
+    if (q4_mfma_batch(batch, true) && kk_q4_mfma_pair_swiglu_supported(w_gate, w_up, x, k, n, batch))
+        return Q4PairRoute::mfma;
+    return Q4PairRoute::none;
+}
+
+static void run_q4_pair(Q4PairRoute route, Kernel::Impl & impl, detail::DeviceContext & ctx, int id, float * y,
+                        const void * w_gate, const void * w_up, const float * x, int k, int n, int batch) {
+    switch (route) {
+    case Q4PairRoute::dot8:
+        // decode: both matrices in one GEMV pass, SwiGLU in its epilogue
+        detail::check_hip((hipError_t)kk_q4_gemv_pair_swiglu(w_gate, w_up, x, y, k, n, batch, ctx.stream),
+                          "kk_q4_gemv_pair_swiglu");
+        impl.route = "q4_gemv_fused_pair_swiglu";
+        break;
+    case Q4PairRoute::stream:
+        detail::check_hip((hipError_t)kk_q4_stream_gemv_pair_swiglu(w_gate, w_up, x, y, k, n, batch, ctx.cus, ctx.stream),
+                          "kk_q4_stream_gemv_pair_swiglu");
+        impl.route = "q4_stream_pair_swiglu";
+        break;
+    case Q4PairRoute::bdiag:
+        detail::check_hip((hipError_t)kk_q4_bdiag_gemv_pair_swiglu(w_gate, w_up, x, y, k, n, batch, ctx.cus, ctx.stream),
+                          "kk_q4_bdiag_gemv_pair_swiglu");
+        impl.route = "q4_bdiag_pair_swiglu";
+        break;
+    case Q4PairRoute::mfma:
+        // the LDS-staged MFMA GEMV: one activation prepass, both products and
+        // SwiGLU in one launch
+        grow(id, ctx, impl.gemm_workspace, impl.gemm_workspace_size, kk_q4_mfma_gemv_workspace_bytes(k));
+        detail::check_hip((hipError_t)kk_q4_mfma_gemv_pair_swiglu(w_gate, w_up, x, y, k, n, batch, impl.gemm_workspace,
+                                                                  ctx.stream),
+                          "kk_q4_mfma_gemv_pair_swiglu");
+        impl.route = "q4_mfma_pair_swiglu";
+        break;
+    case Q4PairRoute::none:
+        break;
+    }
+}
+
 void matmul_swiglu(Kernel & kernel, int id, void * y, const void * w_gate, const void * w_up, const void * x,
                    int k, int n, int batch, WeightType type) {
     std::lock_guard<std::recursive_mutex> lock(detail::mutex());
@@ -254,44 +306,27 @@ void matmul_swiglu(Kernel & kernel, int id, void * y, const void * w_gate, const
                                                      ctx.stream, &impl.route),
                           "kk_gemm_swiglu");
     } else if (type == WeightType::q4_0 &&
-               kk_q4_gemv_pair_swiglu_supported(w_gate, w_up, static_cast<const float *>(x), k, n, batch)) {
-        // decode: both matrices in one GEMV pass, SwiGLU in its epilogue
-        detail::check_hip((hipError_t)kk_q4_gemv_pair_swiglu(w_gate, w_up, static_cast<const float *>(x),
-                                                             static_cast<float *>(y), k, n, batch, ctx.stream),
-                          "kk_q4_gemv_pair_swiglu");
-        impl.route = "q4_gemv_fused_pair_swiglu";
-    } else if (type == WeightType::q4_0 &&
-               ((kk::q4_stream_batch(batch) &&
-                 kk_q4_stream_gemv_supported(w_gate, static_cast<const float *>(x), k, n, batch) &&
-                 kk_q4_stream_gemv_supported(w_up, static_cast<const float *>(x), k, n, batch)) ||
-                (kk::q4_bdiag_batch(batch) &&
-                 kk_q4_bdiag_gemv_supported(w_gate, static_cast<const float *>(x), k, n, batch) &&
-                 kk_q4_bdiag_gemv_supported(w_up, static_cast<const float *>(x), k, n, batch)))) {
-        // small batch: both products and SwiGLU in one launch
-        const bool streamed = kk::q4_stream_batch(batch) &&
-                              kk_q4_stream_gemv_supported(w_gate, static_cast<const float *>(x), k, n, batch) &&
-                              kk_q4_stream_gemv_supported(w_up, static_cast<const float *>(x), k, n, batch);
-        if (streamed)
-            detail::check_hip((hipError_t)kk_q4_stream_gemv_pair_swiglu(w_gate, w_up, static_cast<const float *>(x),
-                                                                        static_cast<float *>(y), k, n, batch, ctx.cus,
-                                                                        ctx.stream),
-                              "kk_q4_stream_gemv_pair_swiglu");
-        else
-            detail::check_hip((hipError_t)kk_q4_bdiag_gemv_pair_swiglu(w_gate, w_up, static_cast<const float *>(x),
-                                                                       static_cast<float *>(y), k, n, batch, ctx.cus,
-                                                                       ctx.stream),
-                              "kk_q4_bdiag_gemv_pair_swiglu");
-        impl.route = streamed ? "q4_stream_pair_swiglu" : "q4_bdiag_pair_swiglu";
-    } else if (type == WeightType::q4_0 && q4_mfma_batch(batch, true) &&
-               kk_q4_mfma_pair_swiglu_supported(w_gate, w_up, static_cast<const float *>(x), k, n, batch)) {
-        // the LDS-staged MFMA GEMV: one activation prepass, both products and
-        // SwiGLU in one launch
-        grow(id, ctx, impl.gemm_workspace, impl.gemm_workspace_size, kk_q4_mfma_gemv_workspace_bytes(k));
-        detail::check_hip((hipError_t)kk_q4_mfma_gemv_pair_swiglu(w_gate, w_up, static_cast<const float *>(x),
-                                                                  static_cast<float *>(y), k, n, batch,
-                                                                  impl.gemm_workspace, ctx.stream),
-                          "kk_q4_mfma_gemv_pair_swiglu");
-        impl.route = "q4_mfma_pair_swiglu";
+               q4_pair_route(w_gate, w_up, static_cast<const float *>(x), k, n, batch) != Q4PairRoute::none) {
+        // decode and small batch: both products and SwiGLU in one launch
+        run_q4_pair(q4_pair_route(w_gate, w_up, static_cast<const float *>(x), k, n, batch), impl, ctx, id,
+                    static_cast<float *>(y), w_gate, w_up, static_cast<const float *>(x), k, n, batch);
+    } else if (type == WeightType::q4_0 && batch > 16 &&
+               q4_pair_route(w_gate, w_up, static_cast<const float *>(x), k, n, 16) != Q4PairRoute::none &&
+               (batch % 16 == 0 || q4_pair_route(w_gate, w_up, static_cast<const float *>(x), k, n, batch % 16) !=
+                                       Q4PairRoute::none)) {
+        // batches between the small-batch kernels and the GEMM: chunks of 16
+        // columns, each in one pair launch (X and Y chunks keep their
+        // alignment: K % 32 == 0)
+        const char * first = nullptr;
+        for (int b0 = 0; b0 < batch; b0 += 16) {
+            const int cols = std::min(16, batch - b0);
+            const float * xc = reinterpret_cast<const float *>(static_cast<const char *>(x) + (size_t)b0 * k * 4);
+            run_q4_pair(q4_pair_route(w_gate, w_up, xc, k, n, cols), impl, ctx, id,
+                        reinterpret_cast<float *>(static_cast<char *>(y) + (size_t)b0 * n * 4), w_gate, w_up, xc, k, n,
+                        cols);
+            if (!first) first = impl.route;
+        }
+        impl.route = first;
     } else {
         // gate and up rows side by side in the workspace: [batch][2n] F32
         const size_t half = (size_t)batch * n * 4;

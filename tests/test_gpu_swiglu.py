@@ -357,10 +357,15 @@ def test_matmul_swiglu_decode_pair_routes(gpu, oracle):
 # pair of tiles) holds the same rows of the gate and the up matrix (n = 300:
 # the last tile ends inside both). Batch 9..16 at K 4096, and batch 8 at K
 # 8192, take the LDS-staged kernel after one activation prepass.
+# Batches 17..63 run in chunks of 16 columns, each chunk in one pair launch
+# (the route reported is the first chunk's; the remainder takes its own size's).
 @pytest.mark.parametrize("batch,k,route", [(3, 4096, "q4_bdiag_pair_swiglu"), (4, 4096, "q4_bdiag_pair_swiglu"),
                                            (5, 4096, "q4_stream_pair_swiglu"), (8, 4096, "q4_stream_pair_swiglu"),
                                            (12, 4096, "q4_mfma_pair_swiglu"), (16, 4096, "q4_mfma_pair_swiglu"),
-                                           (8, 8192, "q4_mfma_pair_swiglu"), (16, 2560, "q4_mfma_pair_swiglu")])
+                                           (8, 8192, "q4_mfma_pair_swiglu"), (16, 2560, "q4_mfma_pair_swiglu"),
+                                           (20, 4096, "q4_mfma_pair_swiglu"), (32, 4096, "q4_mfma_pair_swiglu"),
+                                           (45, 4096, "q4_mfma_pair_swiglu"), (63, 4096, "q4_mfma_pair_swiglu"),
+                                           (33, 8192, "q4_mfma_pair_swiglu")])
 def test_matmul_swiglu_small_batch_one_launch(gpu, oracle, batch, k, route):
     n = 300
     wg = gaussian((n, k), 0.02, 81)
@@ -398,7 +403,9 @@ def test_matmul_swiglu_tile_variants(gpu, oracle, knobs, tile):
 @pytest.mark.parametrize("batch,k,pair_route,single_route", [(8, 4096, "q4_stream_pair_swiglu", "q4_stream_gemv"),
                                                              (6, 4096, "q4_stream_pair_swiglu", "q4_stream_gemv"),
                                                              (16, 4096, "q4_mfma_pair_swiglu", "q4_mfma_gemv"),
-                                                             (7, 8192, "q4_mfma_pair_swiglu", "q4_mfma_gemv")])
+                                                             (7, 8192, "q4_mfma_pair_swiglu", "q4_mfma_gemv"),
+                                                             (32, 4096, "q4_mfma_pair_swiglu", "q4_mfma_gemv"),
+                                                             (40, 4096, "q4_mfma_pair_swiglu", "q4_mfma_gemv")])
 def test_matmul_swiglu_small_batch_matches_two_matmuls(gpu, oracle, batch, k, pair_route, single_route):
     n = 1000
     wg = gaussian((n, k), 0.02, 91 + batch)
