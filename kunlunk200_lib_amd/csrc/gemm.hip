@@ -241,13 +241,24 @@ template <typename RowPtr>
 __device__ void build_tiny_masks(int rows, int blocks, RowPtr row_ptr, uint32_t *masks, int threads) {
     for (int i = threadIdx.x; i < rows * kTinyMaskWords; i += threads) masks[i] = 0u;
     __syncthreads();
-    for (int i = threadIdx.x; i < rows * blocks; i += threads) {
-        const int j = i / blocks, b = i - j * blocks;
-        const uint8_t *wrow = row_ptr(j);
-        if (!wrow) continue;
-        const uint32_t bits = wrow[18 * b] | (static_cast<uint32_t>(wrow[18 * b + 1]) << 8);
-        if ((bits & 0x7c00u) == 0 && (bits & 0x3ffu) != 0)
-            atomicOr(&masks[j * kTinyMaskWords + (b >> 5)], 1u << (b & 31));
+    // kU scales per thread and round: their loads go out together, then the marks
+    constexpr int kU = 8;
+    for (int base = threadIdx.x; base < rows * blocks; base += kU * threads) {
+        uint32_t bits[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int i = base + u * threads;
+            const int j = i / blocks, b = i - j * blocks;
+            const uint8_t *wrow = i < rows * blocks ? row_ptr(j) : nullptr;
+            bits[u] = wrow ? wrow[18 * b] | (static_cast<uint32_t>(wrow[18 * b + 1]) << 8) : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int i = base + u * threads;
+            const int j = i / blocks, b = i - j * blocks;
+            if ((bits[u] & 0x7c00u) == 0 && (bits[u] & 0x3ffu) != 0)
+                atomicOr(&masks[j * kTinyMaskWords + (b >> 5)], 1u << (b & 31));
+        }
     }
     __syncthreads();
 }
@@ -271,29 +282,38 @@ __device__ void tiny_scale_dots(const uint8_t *wrow, const uint32_t *mask, int b
         while (bitsleft) {
             const int b = 32 * word + __builtin_ctz(bitsleft);
             bitsleft &= bitsleft - 1u;
+            // the block's 18 bytes, all loads issued before the first use
             const uint8_t *blk = wrow + 18 * b;
-            const uint32_t bits = blk[0] | (static_cast<uint32_t>(blk[1]) << 8);
+            uint32_t by[18];
+#pragma unroll
+            for (int t = 0; t < 18; ++t) by[t] = blk[t];
+            const uint32_t bits = by[0] | (by[1] << 8);
             const float d = ldexpf(static_cast<float>(bits & 0x3ffu), -27) * ((bits & 0x8000u) ? -1.0f : 1.0f);   // d / 8
-#pragma unroll 1
+            float wv[4][8];
+#pragma unroll
             for (int i = 0; i < 4; ++i) {   // nibble dword i -> block-order positions 8i .. 8i+7
-                const uint8_t *nb = blk + 2 + 4 * i;
-                const uint32_t nib = nb[0] | static_cast<uint32_t>(nb[1]) << 8 | static_cast<uint32_t>(nb[2]) << 16 |
-                                     static_cast<uint32_t>(nb[3]) << 24;
+                const uint32_t *nb = by + 2 + 4 * i;
+                const uint32_t nib = nb[0] | nb[1] << 8 | nb[2] << 16 | nb[3] << 24;
                 const half8 dec = decode(nib, bits);
-                float wv[8];
 #pragma unroll
                 for (int t = 0; t < 8; ++t) {
                     const uint32_t byte = nb[(t & 1) << 1 | (t & 2) >> 1];   // bytes 0, 2, 1, 3
                     const uint32_t q = t < 4 ? byte & 15u : byte >> 4;
-                    wv[t] = (static_cast<float>(q) - 8.0f) * d - static_cast<float>(dec[t]);
+                    wv[i][t] = (static_cast<float>(q) - 8.0f) * d - static_cast<float>(dec[t]);
                 }
+            }
+            // per activation row: its four 8-value pieces loaded together, then
+            // added piece by piece in block order
+#pragma unroll 2
+            for (int r = 0; r < R; ++r) {
+                half8 xv[4];
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const half8 xv = *reinterpret_cast<const half8 *>(x16 + static_cast<size_t>(row_of(r)) * k_pad +
-                                                                      32 * b + 8 * i);
+                for (int i = 0; i < 4; ++i)
+                    xv[i] = *reinterpret_cast<const half8 *>(x16 + static_cast<size_t>(row_of(r)) * k_pad + 32 * b + 8 * i);
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) out[r] += static_cast<float>(xv[t]) * wv[t];
-                }
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) out[r] += static_cast<float>(xv[i][t]) * wv[i][t];
             }
         }
     }
@@ -670,6 +690,133 @@ struct QlShape {
     static_assert(LdsBytes <= 160 * 1024, "LDS");
 };
 
+// The subnormal-scale corrections of one wave's work items (item = one
+// weight row of the tile and 64 activation rows, a lane per row; items it0,
+// it0 + stride, ... below n_items): for each item, the sum over its row's
+// marked blocks, in increasing order, of x16 . (v - decode(v)), exactly as
+// tiny_scale_dots sums it, added to the lane's output (out_of). The walk over
+// the items' marked blocks is wave-uniform; NB marked blocks (of one item or
+// of several) are loaded at once (weight bytes at one address for all lanes,
+// and each lane's activations), then added in order. Lane p < 32 computes the
+// difference for block position p once, every lane takes it by readlane.
+// Items without marked blocks are not touched.
+template <int NB, typename MaskOf, typename RowOf, typename XOf, typename OutOf>
+__device__ void tiny_fix_items(int it0, int stride, int n_items, int blocks, MaskOf mask_of, RowOf wrow_of, XOf xrow_of,
+                               OutOf out_of) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int pi = (lane >> 3) & 3, pt = lane & 7;               // block position 8 pi + pt of lanes 0..31
+    const int words = (blocks + 31) / 32;
+    int it = it0, word = 0;
+    uint32_t left = it < n_items && wrow_of(it) ? __builtin_amdgcn_readfirstlane(mask_of(it)[0]) : 0u;
+    int cur = -1;
+    float fix = 0.0f;
+    for (;;) {
+        int pit[NB], pb[NB];
+#pragma unroll
+        for (int c = 0; c < NB; ++c) {
+            while (left == 0u && it < n_items) {                 // wave-uniform walk
+                if (word + 1 < words) {
+                    left = __builtin_amdgcn_readfirstlane(mask_of(it)[++word]);
+                } else {
+                    it += stride;
+                    word = 0;
+                    left = it < n_items && wrow_of(it) ? __builtin_amdgcn_readfirstlane(mask_of(it)[0]) : 0u;
+                }
+            }
+            pit[c] = left ? it : -1;
+            pb[c] = left ? 32 * word + __builtin_ctz(left) : 0;
+            left &= left - 1u;
+        }
+        if (pit[0] < 0) break;
+        uint32_t hw[NB][9];
+        half8 xv[NB][4];
+#pragma unroll
+        for (int c = 0; c < NB; ++c) {
+            const int ic = pit[c] >= 0 ? pit[c] : pit[0], bc = pit[c] >= 0 ? pb[c] : pb[0];   // an empty slot re-reads
+            const uint16_t *hp = reinterpret_cast<const uint16_t *>(wrow_of(ic) + 18 * bc);
+#pragma unroll
+            for (int t = 0; t < 9; ++t) hw[c][t] = hp[t];
+            const _Float16 *xp = xrow_of(ic) + 32 * bc;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xv[c][i] = *reinterpret_cast<const half8 *>(xp + 8 * i);
+        }
+#pragma unroll
+        for (int c = 0; c < NB; ++c) {
+            if (pit[c] < 0) break;                               // wave-uniform
+            if (pit[c] != cur) {
+                if (cur >= 0) *out_of(cur) += fix;
+                cur = pit[c];
+                fix = 0.0f;
+            }
+            const uint32_t bits = hw[c][0];
+            const float d = ldexpf(static_cast<float>(bits & 0x3ffu), -27) * ((bits & 0x8000u) ? -1.0f : 1.0f);   // d / 8
+            // this lane's position 8 pi + pt (nibble dword pi, slot pt)
+            const uint32_t nib = pi == 0 ? hw[c][1] | hw[c][2] << 16
+                               : pi == 1 ? hw[c][3] | hw[c][4] << 16
+                               : pi == 2 ? hw[c][5] | hw[c][6] << 16 : hw[c][7] | hw[c][8] << 16;
+            const half8 dec = decode_q4_scaled(nib, bits);
+            const uint32_t byte = (nib >> (8 * ((pt & 1) << 1 | (pt & 2) >> 1))) & 0xffu;   // bytes 0, 2, 1, 3
+            const uint32_t q = pt < 4 ? byte & 15u : byte >> 4;
+            _Float16 dl = dec[0];
+#pragma unroll
+            for (int t = 1; t < 8; ++t) dl = pt == t ? dec[t] : dl;
+            const float wv = (static_cast<float>(q) - 8.0f) * d - static_cast<float>(dl);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wv), 8 * i + t));
+                    fix += static_cast<float>(xv[c][i][t]) * ws;
+                }
+        }
+        if (pit[NB - 1] < 0) break;
+    }
+    if (cur >= 0) *out_of(cur) += fix;
+}
+
+// build_tiny_masks for a workgroup of W waves with one weight row per wave
+// task: wave w takes rows w, w + W, ..., lane l blocks l, l + 64, ...; each
+// 64-block group's marks are one ballot, written by lane 0 (no atomics, no
+// division). Rows are processed RB at a time with all their scale loads
+// issued together. Every mask word below (blocks + 31) / 32 of every row is
+// written; two workgroup barriers.
+template <int W, typename RowPtr>
+__device__ void build_tiny_masks_rows(int rows, int blocks, RowPtr row_ptr, uint32_t *masks) {
+    constexpr int RB = 4;
+    constexpr int kGroups = kTinyMaskWords / 2;                 // 64-block groups (K <= 16384)
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+    const int groups = (blocks + 63) / 64;
+    __syncthreads();                                            // the LDS the masks go into is idle
+    for (int j0 = wid * RB; j0 < rows; j0 += W * RB) {          // wave-uniform
+        uint32_t bits[RB][kGroups];
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const uint8_t *wrow = j0 + r < rows ? row_ptr(j0 + r) : nullptr;
+#pragma unroll
+            for (int g = 0; g < kGroups; ++g) {
+                const int b = 64 * g + lane;
+                bits[r][g] = wrow && g < groups && b < blocks ? *reinterpret_cast<const uint16_t *>(wrow + 18 * b) : 0u;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            if (j0 + r >= rows) break;                          // wave-uniform
+#pragma unroll
+            for (int g = 0; g < kGroups; ++g) {
+                if (g >= groups) break;                         // wave-uniform
+                const bool t = (bits[r][g] & 0x7c00u) == 0 && (bits[r][g] & 0x3ffu) != 0;
+                const uint64_t m = __ballot(t);
+                if (lane == 0) {
+                    masks[(j0 + r) * kTinyMaskWords + 2 * g] = static_cast<uint32_t>(m);
+                    masks[(j0 + r) * kTinyMaskWords + 2 * g + 1] = static_cast<uint32_t>(m >> 32);
+                }
+            }
+        }
+    }
+    __syncthreads();
+}
+
 // Copies of a q4_lds_gemm workgroup's wave `wid` (buffer_load_dwordx4 ... lds,
 // 1 KB of LDS each): the activation copies wid + Waves*t of stage s into A
 // buffer s % 3, and the weight copies wid + Waves*t (below BCopies; PAIR: below
@@ -942,31 +1089,25 @@ __global__ __launch_bounds__(128 * CW) void q4_lds_gemm(const uint8_t *__restric
     if (__syncthreads_or(tiny)) {   // workgroup-uniform
         // Q4_0 blocks with subnormal scales (given the decode's fp16
         // rounding) corrected in F32 into k-group 1's sums: the marked blocks
-        // of each B tile row j, for activation rows 8p .. 8p+7 per work item.
-        static_assert(BM % 8 == 0, "fixup rows");
+        // of each B tile row j.
         static_assert(S::XferBytes + S::BN * kTinyMaskWords * 4 <= S::RingBytes, "mask space");
         uint32_t *tiny_masks = reinterpret_cast<uint32_t *>(ql_lds + S::XferBytes);
         const int nblocks = static_cast<int>(row_bytes / 18);
-        build_tiny_masks(S::BN, nblocks, [&](int j) -> const uint8_t * {
+        build_tiny_masks_rows<S::Waves>(S::BN, nblocks, [&](int j) -> const uint8_t * {
             const int h = PAIR ? j / (S::BN / 2) : 0, jr = PAIR ? j % (S::BN / 2) : j;
             return n0 + jr < n_rows ? (h ? w2 : w) + static_cast<size_t>(n0 + jr) * row_bytes : nullptr;
-        }, tiny_masks, kQlThreads);
-        for (int item = threadIdx.x; item < S::BN * (BM / 8); item += kQlThreads) {
-            const int j = item % S::BN, p8 = item / S::BN;
+        }, tiny_masks);
+        // work item = (tile column j, 64 activation rows rh), a lane per row
+        static_assert(BM % 64 == 0, "fixup rows");
+        auto wrow_of = [&](int item) -> const uint8_t * {
+            const int j = item % S::BN;
             const int h = PAIR ? j / (S::BN / 2) : 0, jr = PAIR ? j % (S::BN / 2) : j;   // matrix, row in it
-            const int col = j;   // tile column (PAIR: gate rows 0 .. BN/2, up rows BN/2 .. BN)
-            if (n0 + jr >= n_rows) continue;
-            const uint8_t *wrow = (h ? w2 : w) + static_cast<size_t>(n0 + jr) * row_bytes;
-            const uint32_t *mask = tiny_masks + j * kTinyMaskWords;
-            auto row_of = [&](int r) { return m0 + 8 * p8 + r; };
-            float fix[8];
-#pragma unroll
-            for (int r = 0; r < 8; ++r) fix[r] = 0.0f;
-            auto decode = [](uint32_t nib, uint32_t bits) { return decode_q4_scaled(nib, bits); };
-            tiny_scale_dots<8>(wrow, mask, nblocks, x16, k_pad, row_of, decode, fix);
-#pragma unroll
-            for (int r = 0; r < 8; ++r) tile_lds[(8 * p8 + r) * kTs + col] += fix[r];
-        }
+            return n0 + jr < n_rows ? (h ? w2 : w) + static_cast<size_t>(n0 + jr) * row_bytes : nullptr;
+        };
+        tiny_fix_items<2>(wid, S::Waves, S::BN * (BM / 64), nblocks,
+                          [&](int item) { return tiny_masks + (item % S::BN) * kTinyMaskWords; }, wrow_of,
+                          [&](int item) { return x16 + static_cast<size_t>(m0 + 64 * (item / S::BN) + lane) * k_pad; },
+                          [&](int item) { return tile_lds + (64 * (item / S::BN) + lane) * kTs + item % S::BN; });
         __syncthreads();
     }
     if (kh == 0) {
