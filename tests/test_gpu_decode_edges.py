@@ -248,6 +248,53 @@ def test_q4_subnormal_scales_gemm_tiles(gpu, oracle, knobs, tile):
     assert ok, f"tile {tile}: error {ratio:.3g} x the bound"
 
 
+def q4_sparse_subnormal(k, n, seed):
+    """Q4_0 rows in three kinds: ordinary rows (normal scales near 0.0075),
+    rows whose only non-zero blocks are a few with subnormal scales (about 3%
+    of the blocks, three in four of them m * 2^-24 with m < 16; the others
+    hold q = 8 everywhere, so their values are 0),
+    and ordinary rows with the same sprinkling of subnormal blocks. Rows of the
+    second kind have outputs made of the subnormal blocks alone, so a missing
+    or misplaced correction breaks the bound there."""
+    rng = np.random.default_rng(seed)
+    blocks = k // 32
+    q4 = np.empty((n, blocks, 18), np.uint8)
+    scale = (rng.standard_normal((n, blocks)) * 0.0075).astype(np.float16).view(np.uint16)
+    q4[..., 2:] = rng.integers(0, 256, size=(n, blocks, 16), dtype=np.uint8)
+    kind = np.arange(n) % 3
+    sparse = rng.random((n, blocks)) < 0.03
+    sparse[kind == 0] = False
+    zero = (kind == 1)[:, None] & ~sparse
+    q4[zero, 2:] = 0x88
+    # magnitudes m * 2^-24 with m = 1..15 (the decode keeps almost nothing of
+    # them: without the correction the zero-block rows miss the bound by about
+    # 4.5x) and m = 1..1023
+    m = np.where(rng.random((n, blocks)) < 0.75, rng.integers(1, 16, size=(n, blocks)),
+                 rng.integers(1, 1024, size=(n, blocks))).astype(np.uint16)
+    sub = m | (rng.integers(0, 2, size=(n, blocks), dtype=np.uint16) << 15)
+    scale[sparse] = sub[sparse]
+    q4[..., 0:2] = scale.view(np.uint8).reshape(n, blocks, 2)
+    return q4.reshape(n, blocks * 18)
+
+
+@pytest.mark.parametrize("tile", ["128x48", "128x32", "64x64", "64x32"])
+def test_q4_sparse_subnormal_scales_gemm_tiles(gpu, oracle, knobs, tile):
+    # a few subnormal-scale blocks per row (the correction walks many work
+    # items, most with no marked block), partial M and N tiles
+    knobs("KUNLUN_GEMM_TILE", tile)
+    k, n, batch = 4096, 700, 200
+    q4 = q4_sparse_subnormal(k, n, 97)
+    dec = oracle.q4_decode(q4, k, n)
+    x = np.random.default_rng(98).standard_normal((batch, k)).astype(np.float32)
+    y, got_route, guard_ok = run_matmul(kl.WeightType.q4_0, q4, x, k, n, batch)
+    assert got_route == "q4_gemm_mfma" and guard_ok
+    gold = oracle.gold(dec, x, threads=16)
+    assert np.all(np.isfinite(y))
+    ok, ratio = gemm_bound_ok(y, gold, dec, x, 2e-3)
+    print(f"  q4 sparse subnormal scales tile {tile}: max err / bound = {ratio:.3g}", flush=True)
+    assert ok, f"tile {tile}: error {ratio:.3g} x the bound"
+
+
 @pytest.mark.parametrize("mixed", [False, True], ids=["all_subnormal", "mixed"])
 def test_native_q4_subnormal_scales(gpu, oracle, mixed):
     from test_gpu_native_q4 import NativeCase, check
