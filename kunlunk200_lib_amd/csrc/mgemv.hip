@@ -326,12 +326,17 @@ __global__ __launch_bounds__(kThreads) void q4_mfma_gemv(const uint8_t *__restri
 // into LDS (buffer_load_dwordx4 ... lds; per-lane offsets fixed over stages,
 // the stage offset in the SGPR soffset), into a ring of Slots stages, all but
 // one ahead. One barrier per stage: SB = 16 halves the barriers of SB = 8 for
-// the same LDS (3 x 50 KiB against 6 x 25 KiB). Weight rows sit 18 SB bytes
-// apart in LDS, so a tile's 16 rows read 16 distinct banks; A fragments are
-// lane-contiguous.
+// the same LDS (3 x 51 KiB against 6 x 26 KiB). PAD: weight rows sit 18 SB +
+// 16 bytes apart in LDS, one empty 16-byte chunk after each row (its copy
+// lane reads past the extent: zeros, no memory access; a pair's halves are
+// rounded up to whole copies the same way), so the 16 rows a wave reads at
+// once spread over the banks (at 18 SB bytes, 288 = 72 dwords for SB = 16,
+// bank conflicts took 53% of the LDS-active cycles; K4096 x N14336 at batch
+// 16 went from 18.1-18.5 to 17.3-17.4 us per call, the batch-16 gate/up pair
+// from 30.0-30.7 to 28.1-28.8 us). A fragments are lane-contiguous.
 constexpr int kLgRows = 64;                                  // weight rows per workgroup
 
-template <int SB, bool PACKED, int KG = 2>
+template <int SB, bool PACKED, int KG = 2, bool PAD = false, bool PAIR = false>
 struct LgShape {
     static_assert(SB == 8 || SB == 16, "stage of 8 or 16 blocks");
     static_assert(KG == 2 || (KG == 4 && SB == 16), "k-groups");
@@ -341,7 +346,12 @@ struct LgShape {
     static constexpr int Slots = SB == 8 ? 6 : PACKED ? 4 : 3;         // ring stages
     static constexpr int ABlockBytes = PACKED ? kFragBlockBytes / 2 : kFragBlockBytes;
     static constexpr int AStageBytes = SB * ABlockBytes;               // 8 / 16 / 32 KiB
-    static constexpr int BStageBytes = kLgRows * RowStage;             // 9 / 18 KiB
+    static constexpr int RowStride = PAD ? RowStage + 16 : RowStage;   // bytes of a row in LDS (PAD: one empty chunk)
+    // a pair's gate rows (0 .. 31) and up rows (32 .. 63) each fill whole
+    // 1 KiB copies: with PAD the halves are rounded up to HalfChunks
+    static constexpr int HalfChunks = PAIR && PAD ? ((kLgRows / 2) * (RowStride / 16) + 63) / 64 * 64
+                                                  : (kLgRows / 2) * (RowStride / 16);
+    static constexpr int BStageBytes = 2 * HalfChunks * 16;            // 9 / 18 KiB (PAD: 10 / 19, pair 20)
     static constexpr int StageBytes = AStageBytes + BStageBytes;
     static constexpr int ACopies = AStageBytes / 1024, BCopies = BStageBytes / 1024;
     static constexpr int ACopiesPerWave = ACopies / Waves;
@@ -384,12 +394,12 @@ __device__ __forceinline__ uint32_t lg_and_or(uint32_t a, uint32_t mask, uint32_
 // drops the launch stub.)
 // PAIR: copies below BCopies / 2 come from w_tile (the gate rows), the rest
 // from w2_tile (the up rows; b_off relative to it).
-template <int SB, bool PACKED, bool PAIR, int KG>
+template <int SB, bool PACKED, bool PAIR, int KG, bool PAD>
 __device__ __forceinline__ void lg_copy_stage(const uint8_t *frag, int frag_bytes, uint8_t *w_tile, int w_extent,
                                               uint8_t *w2_tile, int w2_extent,
-                                              const uint32_t (&b_off)[LgShape<SB, PACKED, KG>::BCopiesPerWave], int wid,
-                                              int lane, int s) {
-    using L = LgShape<SB, PACKED, KG>;
+                                              const uint32_t (&b_off)[LgShape<SB, PACKED, KG, PAD, PAIR>::BCopiesPerWave],
+                                              int wid, int lane, int s) {
+    using L = LgShape<SB, PACKED, KG, PAD, PAIR>;
     extern __shared__ __align__(16) uint8_t lg_lds[];
     const __amdgpu_buffer_rsrc_t a_rsrc =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(frag), 0, frag_bytes, 0x00020000);
@@ -419,15 +429,15 @@ __device__ __forceinline__ void lg_copy_stage(const uint8_t *frag, int frag_byte
 // the workgroup's rows 0..31 are rows 32i .. 32i + 31 of w (the gate
 // matrix), rows 32..63 the same rows of w2, and y = SiLU(gate) * up
 // ([batch][n], kk::swiglu_value) from the gate tiles' waves.
-template <int SB, bool PACKED, bool PAIR = false, int KG = 2>
+template <int SB, bool PACKED, bool PAIR = false, int KG = 2, bool PAD = false>
 __global__ __launch_bounds__(256 * KG) void q4_lds_gemv(const uint8_t *__restrict__ w,
                                                          const uint8_t *__restrict__ w2,
                                                          const _Float16 *__restrict__ frag,
                                                          const float *__restrict__ row_inv, float *__restrict__ y,
                                                          int n, int batch, int stages, uint32_t row_bytes,
                                                          int tiles, int tiles_per_xcd) {
-    using L = LgShape<SB, PACKED, KG>;
-    static_assert(!PAIR || (L::BCopies % 2 == 0 && (L::BCopies / 2) * 64 == (kLgRows / 2) * (L::RowStage / 16)),
+    using L = LgShape<SB, PACKED, KG, PAD, PAIR>;
+    static_assert(!PAIR || (L::BCopies % 2 == 0 && (L::BCopies / 2) * 64 == L::HalfChunks),
                   "a pair's weight copies split at the half");
     extern __shared__ __align__(16) uint8_t lg_lds[];
     const int bid = blockIdx.x;
@@ -442,7 +452,7 @@ __global__ __launch_bounds__(256 * KG) void q4_lds_gemv(const uint8_t *__restric
 
     // weight copy i: 16-byte chunks 64i .. 64i+63 of the stage's [row][RowStage]
     // bytes; rows past n repeat row n - 1 and are never stored
-    constexpr int kChunks = L::RowStage / 16;                   // per row: 9 / 18
+    constexpr int kChunks = L::RowStride / 16;                  // per row: 9 / 18 (PAD: + 1 empty)
     const int w_extent = min(kOutRows, n - n0) * static_cast<int>(row_bytes);
     uint8_t *const w_tile = const_cast<uint8_t *>(w + static_cast<size_t>(n0) * row_bytes);
     uint8_t *const w2_tile = PAIR ? const_cast<uint8_t *>(w2 + static_cast<size_t>(n0) * row_bytes) : nullptr;
@@ -450,9 +460,12 @@ __global__ __launch_bounds__(256 * KG) void q4_lds_gemv(const uint8_t *__restric
 #pragma unroll
     for (int t = 0; t < L::BCopiesPerWave; ++t) {
         const int q = min(wid + L::Waves * t, L::BCopies - 1) * 64 + lane;
-        const int row = q / kChunks, chunk = q - (q / kChunks) * kChunks;
-        const int mrow = PAIR ? row % kOutRows : row;           // row of its own matrix's tile
-        b_off[t] = static_cast<uint32_t>(min(n0 + mrow, n - 1) - n0) * row_bytes + 16 * chunk;
+        const int ql = PAIR && q >= L::HalfChunks ? q - L::HalfChunks : q;   // chunk within its matrix's rows
+        const int mrow = ql / kChunks, chunk = ql - (ql / kChunks) * kChunks;   // row of its own matrix's tile
+        // an empty chunk (PAD), or a pair half's rounding past its 32 rows:
+        // past the extent, so zeros without a memory access
+        const bool pad = (PAD && chunk == kChunks - 1) || (PAIR && mrow >= kOutRows);
+        b_off[t] = pad ? 0x80000000u : static_cast<uint32_t>(min(n0 + mrow, n - 1) - n0) * row_bytes + 16 * chunk;
     }
     const int frag_bytes = stages * L::AStageBytes;
     const uint8_t *fbytes = reinterpret_cast<const uint8_t *>(frag);
@@ -472,15 +485,17 @@ __global__ __launch_bounds__(256 * KG) void q4_lds_gemv(const uint8_t *__restric
     // s+1 .. min(s+Slots-2, stages-1) may still be in flight.
     const int ahead0 = min(L::Slots - 1, stages);
     for (int s = 0; s < ahead0; ++s)
-        lg_copy_stage<SB, PACKED, PAIR, KG>(fbytes, frag_bytes, w_tile, w_extent, w2_tile, w_extent, b_off, wid, lane, s);
+        lg_copy_stage<SB, PACKED, PAIR, KG, PAD>(fbytes, frag_bytes, w_tile, w_extent, w2_tile, w_extent, b_off, wid, lane, s);
     for (int s = 0; s < stages; ++s) {
         wait_vmcnt_dyn(my_copies * min(L::Slots - 2, stages - 1 - s));
         lds_barrier();
         if (s + L::Slots - 1 < stages)
-            lg_copy_stage<SB, PACKED, PAIR, KG>(fbytes, frag_bytes, w_tile, w_extent, w2_tile, w_extent, b_off, wid, lane,
+            lg_copy_stage<SB, PACKED, PAIR, KG, PAD>(fbytes, frag_bytes, w_tile, w_extent, w2_tile, w_extent, b_off, wid, lane,
                                             s + L::Slots - 1);
         const uint8_t *abuf = lg_lds + (s % L::Slots) * L::StageBytes;
-        const uint8_t *brow = abuf + L::AStageBytes + (wt * 16 + c16) * L::RowStage;
+        const int trow = wt * 16 + c16;                         // tile row (PAIR: 0 .. 31 gate, 32 .. 63 up)
+        const uint8_t *brow = abuf + L::AStageBytes +
+                              (PAIR ? (trow / 32) * L::HalfChunks * 16 + (trow % 32) * L::RowStride : trow * L::RowStride);
         uint32_t qs[L::WaveBlocks], d16[L::WaveBlocks];
         half8 ahi[L::WaveBlocks], alo[L::WaveBlocks];
 #pragma unroll
@@ -572,17 +587,17 @@ __global__ __launch_bounds__(256 * KG) void q4_lds_gemv(const uint8_t *__restric
 
 // Launch q4_lds_gemv<SB> (dynamic LDS above 64 KiB opted into once per
 // device).
-template <int SB, bool PACKED, bool PAIR = false, int KG = 2>
+template <int SB, bool PACKED, bool PAIR = false, int KG = 2, bool PAD = false>
 hipError_t launch_lds_gemv_kg(const uint8_t *w, const uint8_t *w2, const _Float16 *frag, const float *row_inv, float *y,
                               int k, int n, int batch, hipStream_t stream) {
-    using L = LgShape<SB, PACKED, KG>;
+    using L = LgShape<SB, PACKED, KG, PAD, PAIR>;
     const hipError_t rc =
-        kk::opt_in_lds(reinterpret_cast<const void *>(&q4_lds_gemv<SB, PACKED, PAIR, KG>), L::LdsBytes);
+        kk::opt_in_lds(reinterpret_cast<const void *>(&q4_lds_gemv<SB, PACKED, PAIR, KG, PAD>), L::LdsBytes);
     if (rc != hipSuccess) return rc;
     const int out_rows = PAIR ? kLgRows / 2 : kLgRows;
     const int tiles = (n + out_rows - 1) / out_rows;
     const int tiles_per_xcd = (tiles + 7) / 8;
-    hipLaunchKernelGGL((q4_lds_gemv<SB, PACKED, PAIR, KG>), dim3(tiles_per_xcd * 8), dim3(L::Threads), L::LdsBytes, stream,
+    hipLaunchKernelGGL((q4_lds_gemv<SB, PACKED, PAIR, KG, PAD>), dim3(tiles_per_xcd * 8), dim3(L::Threads), L::LdsBytes, stream,
                        w, w2, frag, row_inv, y, n, batch, k / (SB * 32), static_cast<uint32_t>(k / 32 * 18), tiles,
                        tiles_per_xcd);
     return hipGetLastError();
@@ -591,7 +606,7 @@ hipError_t launch_lds_gemv_kg(const uint8_t *w, const uint8_t *w2, const _Float1
 template <int SB, bool PACKED, bool PAIR = false>
 hipError_t launch_lds_gemv(const uint8_t *w, const uint8_t *w2, const _Float16 *frag, const float *row_inv, float *y,
                            int k, int n, int batch, hipStream_t stream) {
-    return launch_lds_gemv_kg<SB, PACKED, PAIR, SB == 16 ? 4 : 2>(w, w2, frag, row_inv, y, k, n, batch, stream);
+    return launch_lds_gemv_kg<SB, PACKED, PAIR, SB == 16 ? 4 : 2, true>(w, w2, frag, row_inv, y, k, n, batch, stream);
 }
 
 } // namespace
