@@ -119,18 +119,56 @@ __device__ __forceinline__ float absmax4(const float4 &v) {
     return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
 }
 
+// The grid passes below are latency-bound (X is read three times, 8 MB at
+// batch 512 x K4096): a thread issues the LOADS groups of a round, and in
+// passes 2 and 3 the partial maxima before them, ahead of the first wait; the
+// partial maxima are reduced behind LDS-only barriers, so that the X loads
+// stay in flight across them. The loads are unconditional (indices clamped
+// into X, slots past X discarded afterwards), so that the compiler's wait
+// counts stay exact.
+constexpr int kPartialsPerThread = kMaxGroups / kQuantThreads;
+static_assert(kPartialsPerThread * kQuantThreads == kMaxGroups, "whole partial slots per thread");
+
+// One round of a thread's X groups q, q + stride, ... (groups4 >= 1).
+template <int LOADS>
+__device__ __forceinline__ void load_round(const float *x, size_t q, size_t stride, size_t groups4,
+                                           float4 (&v)[LOADS]) {
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) v[u] = load_x4(x, min(q + static_cast<size_t>(u) * stride, groups4 - 1));
+}
+
+// A thread's slots of the per-workgroup partials (groups >= 1; slots past
+// groups repeat the last partial, which leaves the maximum unchanged).
+__device__ __forceinline__ void load_partials(const float *partial, int groups, float (&p)[kPartialsPerThread]) {
+#pragma unroll
+    for (int u = 0; u < kPartialsPerThread; ++u)
+        p[u] = partial[min(static_cast<int>(threadIdx.x) + u * kQuantThreads, groups - 1)];
+}
+__device__ __forceinline__ float max_of(const float (&p)[kPartialsPerThread]) {
+    float m = p[0];
+#pragma unroll
+    for (int u = 1; u < kPartialsPerThread; ++u) m = fmaxf(m, p[u]);
+    return m;
+}
+
 // Pass 1: per-workgroup max|x| and non-finite detection.
+template <int LOADS>
 __global__ __launch_bounds__(kQuantThreads) void i8_pass_max(const float *__restrict__ x, size_t count,
                                                             float *__restrict__ partial0, int *status) {
     __shared__ float scratch[kQuantThreads / kWave];
     float m = 0.0f;
     bool bad = false;
-    const size_t groups4 = count / 4;
+    const size_t groups4 = count / 4, stride = static_cast<size_t>(gridDim.x) * kQuantThreads;
     for (size_t q = static_cast<size_t>(blockIdx.x) * kQuantThreads + threadIdx.x; q < groups4;
-         q += static_cast<size_t>(gridDim.x) * kQuantThreads) {
-        const float4 v = load_x4(x, q);
-        bad |= !finite4(v);
-        m = fmaxf(m, absmax4(v));
+         q += stride * LOADS) {
+        float4 v[LOADS];
+        load_round<LOADS>(x, q, stride, groups4, v);
+#pragma unroll
+        for (int u = 0; u < LOADS; ++u) {
+            // a clamped slot repeats the last group: the max and the finite test are unchanged
+            bad |= !finite4(v[u]);
+            m = fmaxf(m, absmax4(v[u]));
+        }
     }
     if (bad) flag_nonfinite(status);
     m = block_max<kQuantThreads>(m, scratch);
@@ -138,57 +176,85 @@ __global__ __launch_bounds__(kQuantThreads) void i8_pass_max(const float *__rest
 }
 
 // Pass 2: max0 from the partials, q0 codes, per-workgroup max|r|.
+template <int LOADS>
 __global__ __launch_bounds__(kQuantThreads) void i8_pass_primary(const float *__restrict__ x, size_t count, int k,
                                                                 const float *__restrict__ partial0, int groups,
                                                                 int8_t *__restrict__ codes,
                                                                 float *__restrict__ partial1) {
     __shared__ float scratch[kQuantThreads / kWave];
-    float m = 0.0f;
-    for (int i = threadIdx.x; i < groups; i += kQuantThreads) m = fmaxf(m, partial0[i]);
-    float max0 = block_max<kQuantThreads>(m, scratch);
+    const size_t groups4 = count / 4, stride = static_cast<size_t>(gridDim.x) * kQuantThreads;
+    size_t q = static_cast<size_t>(blockIdx.x) * kQuantThreads + threadIdx.x;
+    float p0[kPartialsPerThread];
+    load_partials(partial0, groups, p0);
+    float4 v[LOADS];
+    load_round<LOADS>(x, q, stride, groups4, v);
+    float max0 = block_max<kQuantThreads, true>(max_of(p0), scratch);
     if (max0 == 0.0f) max0 = 1.0f;
     float m1 = 0.0f;
-    const size_t groups4 = count / 4;
-    for (size_t q = static_cast<size_t>(blockIdx.x) * kQuantThreads + threadIdx.x; q < groups4;
-         q += static_cast<size_t>(gridDim.x) * kQuantThreads) {
-        const float4 v = load_x4(x, q);
-        const int a = quant_primary(v.x, max0), b = quant_primary(v.y, max0);
-        const int c = quant_primary(v.z, max0), d = quant_primary(v.w, max0);
-        *reinterpret_cast<uint32_t *>(codes + group_code_offset(4 * q, k, 0)) = pack_codes(a, b, c, d);
-        m1 = fmaxf(m1, fmaxf(fmaxf(fabsf(residual_of(v.x, a, max0)), fabsf(residual_of(v.y, b, max0))),
-                             fmaxf(fabsf(residual_of(v.z, c, max0)), fabsf(residual_of(v.w, d, max0)))));
+    for (; q < groups4; q += stride * LOADS) {
+#pragma unroll
+        for (int u = 0; u < LOADS; ++u) {
+            const size_t g = q + static_cast<size_t>(u) * stride;
+            if (g < groups4) {
+                const int a = quant_primary(v[u].x, max0), b = quant_primary(v[u].y, max0);
+                const int c = quant_primary(v[u].z, max0), d = quant_primary(v[u].w, max0);
+                *reinterpret_cast<uint32_t *>(codes + group_code_offset(4 * g, k, 0)) = pack_codes(a, b, c, d);
+                m1 = fmaxf(m1,
+                           fmaxf(fmaxf(fabsf(residual_of(v[u].x, a, max0)), fabsf(residual_of(v[u].y, b, max0))),
+                                 fmaxf(fabsf(residual_of(v[u].z, c, max0)), fabsf(residual_of(v[u].w, d, max0)))));
+            }
+        }
+        if (q + stride * LOADS < groups4) load_round<LOADS>(x, q + stride * LOADS, stride, groups4, v);
     }
     m1 = block_max<kQuantThreads>(m1, scratch);
     if (threadIdx.x == 0) partial1[blockIdx.x] = m1;
 }
 
 // Pass 3: max1 from the partials, q1 codes; workgroup 0 publishes max0/max1.
+template <int LOADS>
 __global__ __launch_bounds__(kQuantThreads) void i8_pass_residual(const float *__restrict__ x, size_t count, int k,
                                                                  const float *__restrict__ partial0,
                                                                  const float *__restrict__ partial1, int groups,
                                                                  int8_t *__restrict__ codes,
                                                                  float *__restrict__ final_max) {
     __shared__ float scratch[kQuantThreads / kWave];
-    float m0 = 0.0f, m1 = 0.0f;
-    for (int i = threadIdx.x; i < groups; i += kQuantThreads) {
-        m0 = fmaxf(m0, partial0[i]);
-        m1 = fmaxf(m1, partial1[i]);
-    }
-    float max0 = block_max<kQuantThreads>(m0, scratch);
-    float max1 = block_max<kQuantThreads>(m1, scratch);
+    const size_t groups4 = count / 4, stride = static_cast<size_t>(gridDim.x) * kQuantThreads;
+    size_t q = static_cast<size_t>(blockIdx.x) * kQuantThreads + threadIdx.x;
+    float p0[kPartialsPerThread], p1[kPartialsPerThread];
+    load_partials(partial0, groups, p0);
+    load_partials(partial1, groups, p1);
+    float4 v[LOADS];
+    load_round<LOADS>(x, q, stride, groups4, v);
+    float max0 = block_max<kQuantThreads, true>(max_of(p0), scratch);
+    float max1 = block_max<kQuantThreads, true>(max_of(p1), scratch);
     if (max0 == 0.0f) max0 = 1.0f;
     if (max1 == 0.0f) max1 = 1.0f;
-    const size_t groups4 = count / 4;
-    for (size_t q = static_cast<size_t>(blockIdx.x) * kQuantThreads + threadIdx.x; q < groups4;
-         q += static_cast<size_t>(gridDim.x) * kQuantThreads) {
-        const float4 v = load_x4(x, q);
-        auto q1 = [&](float value) { return quant_residual(residual_of(value, quant_primary(value, max0), max0), max1); };
-        *reinterpret_cast<uint32_t *>(codes + group_code_offset(4 * q, k, 1)) = pack_codes(q1(v.x), q1(v.y), q1(v.z), q1(v.w));
+    auto q1 = [&](float value) { return quant_residual(residual_of(value, quant_primary(value, max0), max0), max1); };
+    for (; q < groups4; q += stride * LOADS) {
+#pragma unroll
+        for (int u = 0; u < LOADS; ++u) {
+            const size_t g = q + static_cast<size_t>(u) * stride;
+            if (g < groups4)
+                *reinterpret_cast<uint32_t *>(codes + group_code_offset(4 * g, k, 1)) =
+                    pack_codes(q1(v[u].x), q1(v[u].y), q1(v[u].z), q1(v[u].w));
+        }
+        if (q + stride * LOADS < groups4) load_round<LOADS>(x, q + stride * LOADS, stride, groups4, v);
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         final_max[0] = max0;
         final_max[1] = max1;
     }
+}
+
+template <int LOADS>
+void launch_passes(const float *x, size_t count, int k, int groups, const Workspace &ws, int *status,
+                   hipStream_t stream) {
+    hipLaunchKernelGGL(i8_pass_max<LOADS>, dim3(groups), dim3(kQuantThreads), 0, stream, x, count, ws.partial0,
+                       status);
+    hipLaunchKernelGGL(i8_pass_primary<LOADS>, dim3(groups), dim3(kQuantThreads), 0, stream, x, count, k,
+                       ws.partial0, groups, ws.codes, ws.partial1);
+    hipLaunchKernelGGL(i8_pass_residual<LOADS>, dim3(groups), dim3(kQuantThreads), 0, stream, x, count, k,
+                       ws.partial0, ws.partial1, groups, ws.codes, ws.final_max);
 }
 
 // All three passes in one workgroup, for small X (count <= 4 * kFusedThreads *
@@ -917,12 +983,15 @@ extern "C" int kk_i8_quantize(const float *x, int k, int batch, void *workspace,
                            ws.final_max, status);
         return hipGetLastError();
     }
-    const int groups = static_cast<int>(std::min<size_t>(kMaxGroups, (count + kQuantThreads * 8 - 1) / (kQuantThreads * 8)));
-    hipLaunchKernelGGL(i8_pass_max, dim3(groups), dim3(kQuantThreads), 0, stream, x, count, ws.partial0, status);
-    hipLaunchKernelGGL(i8_pass_primary, dim3(groups), dim3(kQuantThreads), 0, stream, x, count, k, ws.partial0,
-                       groups, ws.codes, ws.partial1);
-    hipLaunchKernelGGL(i8_pass_residual, dim3(groups), dim3(kQuantThreads), 0, stream, x, count, k, ws.partial0,
-                       ws.partial1, groups, ws.codes, ws.final_max);
+    // one group of 4 values per thread where X allows; past kMaxGroups
+    // workgroups, 2 or 4 groups per thread and round
+    const size_t groups4 = count / 4;
+    const int groups = static_cast<int>(std::min<size_t>(kMaxGroups, (groups4 + kQuantThreads - 1) / kQuantThreads));
+    const size_t per_thread = (groups4 + static_cast<size_t>(groups) * kQuantThreads - 1) /
+                              (static_cast<size_t>(groups) * kQuantThreads);
+    if (per_thread <= 1) launch_passes<1>(x, count, k, groups, ws, status, stream);
+    else if (per_thread <= 2) launch_passes<2>(x, count, k, groups, ws, status, stream);
+    else launch_passes<4>(x, count, k, groups, ws, status, stream);
     return hipGetLastError();
 }
 
