@@ -881,8 +881,10 @@ __global__ __launch_bounds__(128 * CW) void q4_lds_gemm(const uint8_t *__restric
     const int g = lane >> 4, c16 = lane & 15;
     // The tile's row scales, loaded before the first copy and handed to the
     // epilogue through LDS: no global load there (on gfx9 a wait for a load
-    // also waits for every store issued before it).
-    const float row_scale = threadIdx.x < BM ? row_inv[m0 + threadIdx.x] * 8.0f : 0.0f;
+    // also waits for every store issued before it). The load is unconditional
+    // (threads past BM repeat row BM - 1 of the padded rows) and its value is
+    // first used in the epilogue, so no wait for it precedes the copies.
+    const float row_inv_raw = row_inv[m0 + min(static_cast<int>(threadIdx.x), BM - 1)];
     float *scale_lds = reinterpret_cast<float *>(ql_lds + S::RingBytes);
 
     // Copies are raw buffer loads into LDS (buffer_load ... lds): the tile's
@@ -1076,7 +1078,7 @@ __global__ __launch_bounds__(128 * CW) void q4_lds_gemm(const uint8_t *__restric
     __syncthreads();                                            // ring idle
     constexpr int kTs = S::TileStride;
     float *tile_lds = reinterpret_cast<float *>(ql_lds);
-    if (threadIdx.x < BM) scale_lds[threadIdx.x] = row_scale;
+    if (threadIdx.x < BM) scale_lds[threadIdx.x] = row_inv_raw * 8.0f;
     if (kh == 1) {
 #pragma unroll
         for (int rg = 0; rg < S::RG; ++rg)

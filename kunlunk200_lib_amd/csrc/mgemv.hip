@@ -222,6 +222,11 @@ __global__ __launch_bounds__(kThreads) void q4_mfma_gemv(const uint8_t *__restri
     const int chunks = (blocks + kChunkBlocks - 1) / kChunkBlocks;
     const int nl = lane & 15, g = lane >> 4;
     const uint8_t *fbytes = reinterpret_cast<const uint8_t *>(frag);
+    // the scales of the lane's batch rows 4g .. 4g+3, requested first and first
+    // used in the epilogue (unconditional loads: no wait for them before)
+    float inv_rows[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) inv_rows[r] = row_inv[min(4 * g + r, batch - 1)];
 
     for (int base = blockIdx.x * kWaves; base < tiles; base += gridDim.x * kWaves) {
         const int tile = base + wid;
@@ -306,7 +311,7 @@ __global__ __launch_bounds__(kThreads) void q4_mfma_gemv(const uint8_t *__restri
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = 4 * g + r;
-                if (m < batch) y[static_cast<size_t>(m) * n + rr] = acc[r] * row_inv[m];
+                if (m < batch) y[static_cast<size_t>(m) * n + rr] = acc[r] * inv_rows[r];
             }
         }
     }
@@ -448,6 +453,11 @@ __global__ __launch_bounds__(256 * KG) void q4_lds_gemv(const uint8_t *__restric
     const int kh = wid >> 2, wt = wid & 3;
     const int g = lane >> 4, c16 = lane & 15;
     constexpr int kOutRows = PAIR ? kLgRows / 2 : kLgRows;      // output rows per workgroup
+    // the scales of the lane's batch rows 4g .. 4g+3, requested first and first
+    // used in the epilogue (unconditional loads: no wait for them before)
+    float inv_rows[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) inv_rows[r] = row_inv[min(4 * g + r, batch - 1)];
     const int n0 = tile * kOutRows;
 
     // weight copy i: 16-byte chunks 64i .. 64i+63 of the stage's [row][RowStage]
@@ -568,7 +578,7 @@ __global__ __launch_bounds__(256 * KG) void q4_lds_gemv(const uint8_t *__restric
             for (int r = 0; r < 4; ++r) {
                 const int m = 4 * g + r;
                 if (m < batch)
-                    y[static_cast<size_t>(m) * n + rr] = kk::swiglu_value(acc[r] * row_inv[m], up[r] * row_inv[m]);
+                    y[static_cast<size_t>(m) * n + rr] = kk::swiglu_value(acc[r] * inv_rows[r], up[r] * inv_rows[r]);
             }
         }
         return;
@@ -580,7 +590,7 @@ __global__ __launch_bounds__(256 * KG) void q4_lds_gemv(const uint8_t *__restric
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int m = 4 * g + r;
-            if (m < batch) y[static_cast<size_t>(m) * n + rr] = acc[r] * row_inv[m];
+            if (m < batch) y[static_cast<size_t>(m) * n + rr] = acc[r] * inv_rows[r];
         }
     }
 }

@@ -82,6 +82,7 @@ __device__ __forceinline__ uint32_t from_partner(uint32_t old, uint32_t src) {
 // w2 (gate/up pair, else null): tile i holds rows 16i .. 16i + 15 of w (the
 // gate matrix) as its rows 0..15 and the same rows of w2 (the up matrix) as
 // rows 16..31, and y = SiLU(gate) * up ([batch][n], kk::swiglu_value).
+template <bool PAIR>
 __global__ __launch_bounds__(kWave * kWaves) void q4_stream_gemv(const uint8_t *__restrict__ w,
                                                                const uint8_t *__restrict__ w2,
                                                                const float *__restrict__ x, float *__restrict__ y,
@@ -90,7 +91,7 @@ __global__ __launch_bounds__(kWave * kWaves) void q4_stream_gemv(const uint8_t *
     const int lane = threadIdx.x & (kWave - 1);
     const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
     const int r16 = lane & 15, g = lane >> 4;
-    const int tile_out = w2 ? kTileRows / 2 : kTileRows;         // output rows per tile
+    const int tile_out = PAIR ? kTileRows / 2 : kTileRows;       // output rows per tile
     const int tiles = (n + tile_out - 1) / tile_out;
     const int tile0 = blockIdx.x * tiles_per_group;
     const int c = wid;                                            // this wave's K chunk
@@ -128,21 +129,31 @@ __global__ __launch_bounds__(kWave * kWaves) void q4_stream_gemv(const uint8_t *
     };
     // pair tiles: pieces 0..255 are gate rows 0..13, 288..575 up rows 16..31;
     // load 4 (pieces 256..319) spans both: each half's lanes read the other
-    // matrix's buffer out of bounds (zero) and the two loads are or-ed
+    // matrix's buffer out of bounds (zero); the up half goes to a slot of its
+    // own and the two are or-ed when the piece is staged, not at the load
+    // (which would wait for it there)
     constexpr uint32_t kOutOfBounds = 0x7ffffff0u;
     constexpr uint32_t kUpHalf = (kTileRows / 2) * kRowBytes;
+    constexpr int kSplit = kTileRows / 2 * 18 / kWave;             // the load spanning both halves
+    u32x4 ring[kPiecesPerLane], ring_up{0u, 0u, 0u, 0u};
     auto load = [&](int t, int i) {
-        if (!w2) return load_at(rows_buffer(w, static_cast<size_t>(tile0 + t) * kTileRows, kTileRows), goff[i]);
+        if (!PAIR) {
+            ring[i] = load_at(rows_buffer(w, static_cast<size_t>(tile0 + t) * kTileRows, kTileRows), goff[i]);
+            return;
+        }
         const size_t row0 = static_cast<size_t>(tile0 + t) * (kTileRows / 2);
-        if (i * kWave + kWave <= kTileRows / 2 * 18) return load_at(rows_buffer(w, row0, kTileRows / 2), goff[i]);
-        if (i * kWave >= kTileRows / 2 * 18) return load_at(rows_buffer(w2, row0, kTileRows / 2), goff[i] - kUpHalf);
-        const bool up = i * kWave + lane >= kTileRows / 2 * 18;
-        return load_at(rows_buffer(w, row0, kTileRows / 2), up ? kOutOfBounds : goff[i]) |
-               load_at(rows_buffer(w2, row0, kTileRows / 2), up ? goff[i] - kUpHalf : kOutOfBounds);
+        if (i < kSplit) {
+            ring[i] = load_at(rows_buffer(w, row0, kTileRows / 2), goff[i]);
+        } else if (i > kSplit) {
+            ring[i] = load_at(rows_buffer(w2, row0, kTileRows / 2), goff[i] - kUpHalf);
+        } else {
+            const bool up = i * kWave + lane >= kTileRows / 2 * 18;
+            ring[i] = load_at(rows_buffer(w, row0, kTileRows / 2), up ? kOutOfBounds : goff[i]);
+            ring_up = load_at(rows_buffer(w2, row0, kTileRows / 2), up ? goff[i] - kUpHalf : kOutOfBounds);
+        }
     };
-    u32x4 ring[kPiecesPerLane];
 #pragma unroll
-    for (int i = 0; i < kPiecesPerLane; ++i) ring[i] = load(0, i);
+    for (int i = 0; i < kPiecesPerLane; ++i) load(0, i);
     __builtin_amdgcn_sched_barrier(0);
 
     // 3. X into the A layout: lane (r, g) takes quad g (r < 8) or 4 + g (r >= 8) of column r % 8
@@ -266,8 +277,8 @@ __global__ __launch_bounds__(kWave * kWaves) void q4_stream_gemv(const uint8_t *
     for (int tt = 0; tt < tiles_per_group; ++tt) {
 #pragma unroll
         for (int i = 0; i < kPiecesPerLane; ++i) {
-            stage_piece(i, ring[i]);
-            if (tt + 1 < tiles_per_group) ring[i] = load(tt + 1, i);
+            stage_piece(i, PAIR && i == kSplit ? ring[i] | ring_up : ring[i]);
+            if (tt + 1 < tiles_per_group) load(tt + 1, i);
             if (i == 4) group_compute(tt, 0);
         }
         group_compute(tt, 1);
@@ -282,13 +293,13 @@ __global__ __launch_bounds__(kWave * kWaves) void q4_stream_gemv(const uint8_t *
         for (int ww = 0; ww < kWaves; ++ww) sum += partial[((t * 2 + rg) * kWaves + ww) * 32 + src][m & 3];
         return sum;
     };
-    const int per_tile = w2 ? 128 : 256;
+    const int per_tile = PAIR ? 128 : 256;
     for (int idx = threadIdx.x; idx < tiles_per_group * per_tile; idx += kWave * kWaves) {
-        const int t = idx / per_tile, rg = w2 ? 0 : (idx >> 7) & 1, m = (idx >> 4) & 7, nn = idx & 15;
+        const int t = idx / per_tile, rg = PAIR ? 0 : (idx >> 7) & 1, m = (idx >> 4) & 7, nn = idx & 15;
         const int gt = tile0 + t;
         const int out_row = gt * tile_out + rg * 16 + nn;
         if (m >= batch || gt >= tiles || out_row >= n) continue;
-        const float v = w2 ? kk::swiglu_value(row_sum(t, 0, m, nn), row_sum(t, 1, m, nn)) : row_sum(t, rg, m, nn);
+        const float v = PAIR ? kk::swiglu_value(row_sum(t, 0, m, nn), row_sum(t, 1, m, nn)) : row_sum(t, rg, m, nn);
         y[static_cast<size_t>(m) * n + out_row] = v;
     }
 }
@@ -304,13 +315,18 @@ extern "C" int kk_q4_stream_gemv_supported(const void *w, const float *x, int k,
 namespace {
 hipError_t launch_stream(const void *w, const void *w2, const float *x, float *y, int n, int batch, int cus,
                          hipStream_t stream) {
-    const hipError_t rc = kk::opt_in_lds(reinterpret_cast<const void *>(&q4_stream_gemv), kLdsBytes);
+    const hipError_t rc = w2 ? kk::opt_in_lds(reinterpret_cast<const void *>(&q4_stream_gemv<true>), kLdsBytes)
+                             : kk::opt_in_lds(reinterpret_cast<const void *>(&q4_stream_gemv<false>), kLdsBytes);
     if (rc != hipSuccess) return rc;
     const int tile_out = w2 ? kTileRows / 2 : kTileRows;     // a pair tile: 16 gate and 16 up rows
     const int tiles = (n + tile_out - 1) / tile_out;
     const int t = std::max(1, std::min(kMaxTiles, (tiles + cus - 1) / cus));
-    hipLaunchKernelGGL(q4_stream_gemv, dim3((tiles + t - 1) / t), dim3(kWave * kWaves), kLdsBytes, stream,
-                       static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(w2), x, y, n, batch, t);
+    if (w2)
+        hipLaunchKernelGGL(q4_stream_gemv<true>, dim3((tiles + t - 1) / t), dim3(kWave * kWaves), kLdsBytes, stream,
+                           static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(w2), x, y, n, batch, t);
+    else
+        hipLaunchKernelGGL(q4_stream_gemv<false>, dim3((tiles + t - 1) / t), dim3(kWave * kWaves), kLdsBytes, stream,
+                           static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(w2), x, y, n, batch, t);
     return hipGetLastError();
 }
 } // namespace
