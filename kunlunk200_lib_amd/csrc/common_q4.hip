@@ -46,8 +46,27 @@ __device__ uint32_t block_max_bits(uint32_t v, uint32_t *scratch) {
     return m;
 }
 
-__device__ __forceinline__ float load_value(const void *x, int x_f16, size_t i) {
-    return x_f16 ? kk::half_bits_to_float(static_cast<const uint16_t *>(x)[i]) : static_cast<const float *>(x)[i];
+// One row of X (k F16 or F32 values, the type a template parameter of the
+// kernels: a runtime flag would put a branch around every load, and each
+// load would be waited for before the next is issued) through a buffer
+// resource whose extent is the row's bytes: value j outside [0, k) reads zero
+// without a memory access, so the loads need no bounds branch either.
+struct XRow {
+    __amdgpu_buffer_rsrc_t rsrc;
+    int k;
+};
+template <bool F16>
+__device__ __forceinline__ XRow x_row(const void *x, size_t row, int k) {
+    constexpr size_t kElem = F16 ? 2 : 4;
+    const uint8_t *base = static_cast<const uint8_t *>(x) + row * static_cast<size_t>(k) * kElem;
+    return {__builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), 0, static_cast<int>(k * kElem), 0x00020000),
+            k};
+}
+template <bool F16>
+__device__ __forceinline__ float x_value(const XRow &r, int j) {
+    const uint32_t jj = static_cast<uint32_t>(j) < static_cast<uint32_t>(r.k) ? static_cast<uint32_t>(j) : 0x20000000u;
+    if (F16) return kk::half_bits_to_float(__builtin_amdgcn_raw_buffer_load_b16(r.rsrc, static_cast<int>(2u * jj), 0, 0));
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r.rsrc, static_cast<int>(4u * jj), 0, 0));
 }
 
 __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
@@ -122,6 +141,7 @@ __device__ __forceinline__ void write_view_tail(int8_t *values, int kp, float *p
 // the other 32 bytes of each 64-byte group and values[4kp .. 4kp+1024) zero;
 // params = {max0/127, max1/127, max0, max1, 0 ...} (16 floats).
 // One workgroup; thread t owns groups of 8 values g = t + 1024 i.
+template <bool F16>
 __global__ __launch_bounds__(kQuantThreads) void common_quant_pair(const void *__restrict__ x, int x_f16, int k,
                                                                   int kp, int8_t *__restrict__ values,
                                                                   float *__restrict__ params) {
@@ -130,14 +150,12 @@ __global__ __launch_bounds__(kQuantThreads) void common_quant_pair(const void *_
     constexpr int kMaxGroups = 2;              // kp <= 16384 = 2 * 1024 * 8
     const int groups = kp / 8;
     float v[kMaxGroups][8];
+    const XRow xr = x_row<F16>(x, 0, k);
 #pragma unroll
     for (int i = 0; i < kMaxGroups; ++i) {
         const int g = threadIdx.x + kQuantThreads * i;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const int j = 8 * g + t;
-            v[i][t] = (g < groups && j < k) ? load_value(x, x_f16, j) : 0.0f;
-        }
+        for (int t = 0; t < 8; ++t) v[i][t] = x_value<F16>(xr, g < groups ? 8 * g + t : -1);
     }
     int q0[kMaxGroups][8], q1[kMaxGroups][8];
     float sc[4];
@@ -162,6 +180,7 @@ __device__ __forceinline__ size_t tiled_offset(int r, int j, int blocks) {
            ((j / 32) % 2) * 8 + j % 8;
 }
 
+template <bool F16>
 __global__ __launch_bounds__(kRowThreads) void common_quant_rows(const void *__restrict__ x, int x_f16, int k,
                                                                 int kp, int rows, int8_t *__restrict__ values,
                                                                 float *__restrict__ params,
@@ -170,10 +189,15 @@ __global__ __launch_bounds__(kRowThreads) void common_quant_rows(const void *__r
     __shared__ uint32_t scratch[kRowThreads / 64];
     const int row = blockIdx.x;
     const bool real = row < rows;
-    const size_t base = static_cast<size_t>(row) * k;
+    const XRow xr = x_row<F16>(x, real ? row : 0, real ? k : 0);   // a padding row reads zeros
     uint32_t m = 0;
-    for (int j = threadIdx.x; j < k && real; j += kRowThreads)
-        m = max(m, __float_as_uint(load_value(x, x_f16, base + j)) & 0x7fffffffu);
+    for (int j0 = 0; j0 < k; j0 += 8 * kRowThreads) {
+        float v[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) v[t] = x_value<F16>(xr, j0 + t * kRowThreads + static_cast<int>(threadIdx.x));
+#pragma unroll
+        for (int t = 0; t < 8; ++t) m = max(m, __float_as_uint(v[t]) & 0x7fffffffu);
+    }
     m = block_max_bits<kRowThreads>(m, scratch);
     const float mx = m ? __uint_as_float(m) : 1.0f;
     const float scale = mx / 127.0f, inv = 127.0f / mx;
@@ -184,7 +208,7 @@ __global__ __launch_bounds__(kRowThreads) void common_quant_rows(const void *__r
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int j = 4 * d + t;
-            const float v = (real && j < k) ? load_value(x, x_f16, base + j) : 0.0f;
+            const float v = x_value<F16>(xr, j);
             q[t] = kk::round_clamp(v * inv, 127);
         }
         const uint32_t word = pack4(q[0], q[1], q[2], q[3]);
@@ -215,7 +239,7 @@ struct GemvMatrix {
 // view to view_values / view_params), kExact (act = X).
 constexpr int kPrepared = 0, kQuantize = 1, kExact = 2;
 
-template <int MODE>
+template <int MODE, bool F16>
 __global__ __launch_bounds__(kCqThreads) void common_gemv(GemvMatrix m0, GemvMatrix m1, int tiles_per_matrix,
                                                          const void *__restrict__ act, int x_f16,
                                                          const float *__restrict__ params,
@@ -248,14 +272,14 @@ __global__ __launch_bounds__(kCqThreads) void common_gemv(GemvMatrix m0, GemvMat
     const int groups = kp / 8;
     uint32_t raw[kMaxPasses][4];
     float xv[kMaxPasses][8];
+    const XRow xr = x_row<F16>(act, 0, k);
 #pragma unroll
     for (int pass = 0; pass < kMaxPasses; ++pass) {
         const int g = min(pass * kCqThreads + static_cast<int>(threadIdx.x), groups - 1);
         if (RAW_X) {
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
-                const int j = 8 * g + t;
-                xv[pass][t] = j < k ? load_value(act, x_f16, j) : 0.0f;
+                xv[pass][t] = x_value<F16>(xr, 8 * g + t);
             }
         } else {
             const int8_t *codes = static_cast<const int8_t *>(act);
@@ -604,8 +628,12 @@ __global__ __launch_bounds__(256 * KS) void common_gemm(const uint8_t *__restric
 extern "C" int kk_common_quant_pair(const void *x, int x_f16, int k, int kp, void *values, void *params,
                                     hipStream_t stream) {
     if (!x || !values || !params || k <= 0 || kp < k || kp % 256 != 0 || kp > 16384) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(common_quant_pair, dim3(1), dim3(kQuantThreads), 0, stream, x, x_f16, k, kp,
-                       static_cast<int8_t *>(values), static_cast<float *>(params));
+    if (x_f16)
+        hipLaunchKernelGGL(common_quant_pair<true>, dim3(1), dim3(kQuantThreads), 0, stream, x, x_f16, k, kp,
+                           static_cast<int8_t *>(values), static_cast<float *>(params));
+    else
+        hipLaunchKernelGGL(common_quant_pair<false>, dim3(1), dim3(kQuantThreads), 0, stream, x, x_f16, k, kp,
+                           static_cast<int8_t *>(values), static_cast<float *>(params));
     return hipGetLastError();
 }
 
@@ -614,8 +642,14 @@ extern "C" int kk_common_quant_rows(const void *x, int x_f16, int k, int kp, int
     if (!x || !values || !params || !tiled || k <= 0 || kp < k || kp % 256 != 0 || rows <= 0 ||
         defined_rows < rows || defined_rows % 32 != 0)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(common_quant_rows, dim3(defined_rows), dim3(kRowThreads), 0, stream, x, x_f16, k, kp, rows,
-                       static_cast<int8_t *>(values), static_cast<float *>(params), static_cast<int8_t *>(tiled));
+    if (x_f16)
+        hipLaunchKernelGGL(common_quant_rows<true>, dim3(defined_rows), dim3(kRowThreads), 0, stream, x, x_f16, k, kp,
+                           rows, static_cast<int8_t *>(values), static_cast<float *>(params),
+                           static_cast<int8_t *>(tiled));
+    else
+        hipLaunchKernelGGL(common_quant_rows<false>, dim3(defined_rows), dim3(kRowThreads), 0, stream, x, x_f16, k,
+                           kp, rows, static_cast<int8_t *>(values), static_cast<float *>(params),
+                           static_cast<int8_t *>(tiled));
     return hipGetLastError();
 }
 
@@ -639,15 +673,17 @@ extern "C" int kk_common_gemv(const void *w0, float *y0, const void *w1, float *
     const dim3 grid(tiles * count), block(kCqThreads);
     int8_t *vv = static_cast<int8_t *>(view_values);
     float *pp = static_cast<float *>(params);
-    if (mode == kExact)
-        hipLaunchKernelGGL(common_gemv<kExact>, grid, block, lds, stream, m0, m1, tiles, act, x_f16, pp, vv, pp, k,
-                           kp, n, np);
-    else if (mode == kQuantize)
-        hipLaunchKernelGGL(common_gemv<kQuantize>, grid, block, lds, stream, m0, m1, tiles, act, x_f16, pp, vv, pp,
-                           k, kp, n, np);
-    else
-        hipLaunchKernelGGL(common_gemv<kPrepared>, grid, block, lds, stream, m0, m1, tiles, act, x_f16, pp, vv, pp,
-                           k, kp, n, np);
+#define KK_COMMON_GEMV(M, F)                                                                                \
+    hipLaunchKernelGGL((common_gemv<M, F>), grid, block, lds, stream, m0, m1, tiles, act, x_f16, pp, vv, pp, k, kp, n, \
+                       np)
+    if (mode == kExact) {
+        if (x_f16) KK_COMMON_GEMV(kExact, true); else KK_COMMON_GEMV(kExact, false);
+    } else if (mode == kQuantize) {
+        if (x_f16) KK_COMMON_GEMV(kQuantize, true); else KK_COMMON_GEMV(kQuantize, false);
+    } else {
+        if (x_f16) KK_COMMON_GEMV(kPrepared, true); else KK_COMMON_GEMV(kPrepared, false);
+    }
+#undef KK_COMMON_GEMV
     return hipGetLastError();
 }
 
